@@ -1,0 +1,248 @@
+"""Headline benchmark: paged decode KV-read GB/s (+ tokens/s) at Qwen3-0.6B KV
+shapes, batch 128.
+
+One step = one decode step of the hot path: upload the batch metadata (block
+tables, positions, slots) once, then for each of 28 layers append one token's
+K/V per sequence through the slot mapping and run paged GQA decode attention
+over every sequence's full context. Context lengths start uniform in
+[1024, 8192] (seeded) and grow by one token per step; pages are handed out in
+a seeded random order so tables are non-contiguous. K/V/Q are synthetic
+N(0,1) bf16 already resident in HBM when timing starts.
+
+Prints one JSON line (see the keys below). --gpus N > 1 is refused: this
+build measures one GPU.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+LAYERS, BATCH, KV_HEADS, Q_HEADS, HEAD_DIM, BLOCK = 28, 128, 8, 16, 128, 16
+CTX_LO, CTX_HI = 1024, 8192
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(threads):
+    """Oracle decode attention (the CPU restatement of the reference kernel) on
+    a bounded sample of the workload: 64 sequences of one layer at the same
+    length distribution, bf16 K/V, fp32 accumulation."""
+    from oracle import oracle as orc
+
+    gen = np.random.default_rng(1)
+    rows = 64
+    lengths = [int(x) for x in gen.integers(CTX_LO, CTX_HI + 1, rows)]
+    F = KV_HEADS * HEAD_DIM
+    pages = [math.ceil(n / BLOCK) for n in lengths]
+    n_pages = sum(pages)
+    kc = orc.from_f32(gen.standard_normal(n_pages * BLOCK * F, np.float32), orc.BF16)
+    vc = orc.from_f32(gen.standard_normal(n_pages * BLOCK * F, np.float32), orc.BF16)
+    q = orc.from_f32(gen.standard_normal((rows, Q_HEADS * HEAD_DIM), np.float32), orc.BF16)
+    perm = gen.permutation(n_pages).astype(np.uint32)
+    offsets = np.cumsum([0] + pages[:-1])
+    att = orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, orc.BF16, q, orc.BF16,
+                        [n - 1 for n in lengths], perm, offsets, pages, Q_HEADS, 0,
+                        1 / math.sqrt(HEAD_DIM))
+    kv_bytes = sum(lengths) * F * 2 * 2
+    t0 = time.perf_counter()
+    att.online_threads(threads)
+    dt = time.perf_counter() - t0
+    one = orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, orc.BF16, q[:4],
+                        orc.BF16, [n - 1 for n in lengths[:4]], perm, offsets[:4], pages[:4],
+                        Q_HEADS, 0, 1 / math.sqrt(HEAD_DIM))
+    t1 = time.perf_counter()
+    one.online_threads(1)
+    dt1 = time.perf_counter() - t1
+    single_gbs = sum(lengths[:4]) * F * 4 / dt1 / 1e9
+    return {
+        "value": round(kv_bytes / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle/oracle.c decode attention (restated paged_attention_f32, fp32 "
+                   f"accumulate) over 1 layer x {rows} sequences, {sum(lengths)} tokens of "
+                   f"bf16 K/V ({kv_bytes / 1e6:.0f} MB) in {dt:.2f} s on {threads} threads; "
+                   f"single-thread {single_gbs:.3f} GB/s on 4 of them"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from chibillm_amd import ckv
+    from oracle import oracle as orc  # seeded lengths / page order only
+
+    device = torch.device("cuda:0")
+    rng = orc.Mt64(args.seed)
+    lengths = np.array([rng.uniform_int(CTX_LO, CTX_HI) for _ in range(BATCH)], np.int64)
+    total_steps = args.warmup + args.steps
+    max_len = lengths + total_steps
+    pages_needed = [math.ceil(n / BLOCK) for n in max_len]
+    n_pool = sum(pages_needed) + 64
+    perm = rng.permutation(n_pool)
+    F = KV_HEADS * HEAD_DIM
+    max_pages = max(pages_needed)
+
+    # per-sequence table regions of the flat table; pages appear as needed
+    flat = np.zeros(BATCH * max_pages, np.uint32)
+    owned = [0] * BATCH
+    next_free = 0
+
+    def ensure_pages(s, tokens):
+        nonlocal next_free
+        need = math.ceil(tokens / BLOCK)
+        while owned[s] < need:
+            flat[s * max_pages + owned[s]] = perm[next_free]
+            next_free += 1
+            owned[s] += 1
+
+    for s in range(BATCH):
+        ensure_pages(s, int(lengths[s]))
+
+    kv_gb = LAYERS * n_pool * BLOCK * F * 2 * 2 / 1e9
+    log(f"pool {n_pool} pages x {LAYERS} layers = {kv_gb:.1f} GB K+V; "
+        f"context tokens {int(lengths.sum())}")
+    ctx = ckv.Context(0, stream=torch.cuda.current_stream())
+    elems = LAYERS * n_pool * BLOCK * F
+    keys = torch.empty(elems, dtype=torch.bfloat16, device=device)
+    values = torch.empty(elems, dtype=torch.bfloat16, device=device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed)
+    t0 = time.perf_counter()
+    step = 1 << 30
+    for buf in (keys, values):
+        for i in range(0, elems, step):
+            buf[i:i + step].normal_(generator=gen)
+    torch.cuda.synchronize()
+    log(f"filled K/V with N(0,1) in {time.perf_counter() - t0:.1f} s")
+    pool = ckv.Pool(ctx, LAYERS, n_pool, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16, keys, values)
+
+    q = torch.randn(LAYERS, BATCH, Q_HEADS * HEAD_DIM, generator=gen, device=device).to(torch.bfloat16)
+    k_new = torch.randn(LAYERS, BATCH, F, generator=gen, device=device).to(torch.bfloat16)
+    v_new = torch.randn(LAYERS, BATCH, F, generator=gen, device=device).to(torch.bfloat16)
+    out = torch.empty(LAYERS, BATCH, Q_HEADS * HEAD_DIM, dtype=torch.bfloat16, device=device)
+    scale = 1.0 / math.sqrt(HEAD_DIM)
+    offsets = np.arange(BATCH, dtype=np.uint32) * max_pages
+
+    def one_step():
+        positions = lengths.copy()  # the new token's position
+        for s in range(BATCH):
+            ensure_pages(s, int(positions[s]) + 1)
+        slots = [int(flat[s * max_pages + p // BLOCK]) * BLOCK + p % BLOCK
+                 for s, p in enumerate(positions)]
+        pool.upload(flat, offsets, owned, positions, slots)
+        for layer in range(LAYERS):
+            pool.append(layer, k_new[layer], v_new[layer])
+            pool.decode(layer, q[layer], Q_HEADS, scale, out[layer])
+        attended = positions + 1
+        lengths[:] = attended
+        return int(attended.sum()), int(sum(math.ceil(a / BLOCK) for a in attended))
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    log(f"warmup {args.warmup} steps done")
+
+    ctx.profile(True)
+    ctx.profile_reset()
+    tokens_attended = pages_read = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        toks, pages = one_step()
+        tokens_attended += toks
+        pages_read += pages
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    decode_ms, decode_n = ctx.profile_query("paged_attention_decode")
+    merge_ms, merge_n = ctx.profile_query("paged_attention_merge")
+    store_ms, store_n = ctx.profile_query("store_kv")
+    ctx.profile(False)
+    log(f"timed {args.steps} steps in {elapsed:.3f} s")
+
+    kv_row_bytes = F * 2 * 2  # K + V, bf16, all KV heads
+    kv_bytes = LAYERS * tokens_attended * kv_row_bytes
+    value = kv_bytes / elapsed / 1e9
+    ms_per_step = elapsed * 1e3 / args.steps
+    # algorithmic bytes of one decode launch (one layer): KV of every attended
+    # token + Q + O + the table entries read
+    per_launch = (tokens_attended * kv_row_bytes + pages_read * 4
+                  + args.steps * 2 * BATCH * Q_HEADS * HEAD_DIM * 2) / args.steps
+    decode_avg_s = decode_ms / decode_n / 1e3
+    achieved = per_launch / decode_avg_s / 1e9
+    result = {
+        "metric": "paged decode KV-read GB/s (% HBM peak) + tokens/s, Qwen3-0.6B KV, batch 128",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) K/V/Q, seeded lengths and page order",
+        "config": {
+            "workload": "config3: 28-layer decode step (append 1 token/seq/layer + paged GQA "
+                        "decode attention), batch 128, context U[1024,8192] growing 1/step",
+            "layers": LAYERS, "batch": BATCH, "kv_heads": KV_HEADS, "q_heads": Q_HEADS,
+            "head_dim": HEAD_DIM, "block_size": BLOCK, "pool_pages": n_pool,
+            "kv_pool_gb": round(kv_gb, 2),
+            "mean_context": round(tokens_attended / args.steps / BATCH, 1),
+        },
+        "tokens_per_s": round(BATCH * args.steps / elapsed, 1),
+        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "kernels_ms_per_step": {
+            "paged_attention_decode": round(decode_ms / args.steps, 4),
+            "paged_attention_merge": round(merge_ms / args.steps, 4),
+            "store_kv": round(store_ms / args.steps, 4),
+        },
+        "roofline": {
+            "kernel": "paged_attention_decode",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(decode_avg_s * 1e6, 2),
+            "algorithmic_bytes_per_launch": int(per_launch),
+        },
+        "cpu_baseline": None,
+    }
+    pool.close()
+    del keys, values
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
+        log(f"CPU baseline on {threads} threads")
+        result["cpu_baseline"] = cpu_baseline(threads)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,918 @@
+// C ABI of libckv: context, pool, metadata upload and op entry points.
+//
+// Every op validates on the host from the caller's arrays (the host cannot
+// read device memory the way the reference reads Metal shared buffers), then
+// enqueues HIP work on the context stream. Metadata goes up with one pinned
+// host-to-device copy per call.
+#include "ckv_internal.h"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <unordered_set>
+
+using namespace ckv;
+
+namespace {
+
+int set_error(ckv_context* ctx, int code, const std::string& detail)
+{
+    if (ctx)
+        ctx->last_error = detail;
+    return code;
+}
+
+int hip_error(ckv_context* ctx, hipError_t e, const char* what)
+{
+    return set_error(ctx, CKV_E_HIP_FAILURE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool mul_fits(size_t a, size_t b, size_t* out)
+{
+    return !__builtin_mul_overflow(a, b, out);
+}
+
+pool_view view_of(const ckv_pool* p)
+{
+    pool_view v {};
+    v.keys = p->keys;
+    v.values = p->values;
+    v.layer_elems = (uint64_t)p->blocks * p->block_size * p->kv_heads * p->head_dim;
+    v.blocks = (uint32_t)p->blocks;
+    v.block_size = (uint32_t)p->block_size;
+    v.kv_heads = (uint32_t)p->kv_heads;
+    v.head_dim = (uint32_t)p->head_dim;
+    v.features = (uint32_t)(p->kv_heads * p->head_dim);
+    v.elem_size = (uint32_t)p->elem_size;
+    v.dtype = p->dtype;
+    return v;
+}
+
+hipEvent_t take_event(ckv_context* ctx)
+{
+    if (!ctx->spare_events.empty()) {
+        hipEvent_t e = ctx->spare_events.back();
+        ctx->spare_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess)
+        return nullptr;
+    return e;
+}
+
+// Launches through `launch`, bracketing it with timing events when profiling.
+template <class Launch>
+int run_kernel(ckv_context* ctx, const char* name, Launch&& launch)
+{
+    hipEvent_t start = nullptr, stop = nullptr;
+    if (ctx->profile) {
+        start = take_event(ctx);
+        stop = take_event(ctx);
+        if (start && stop)
+            (void)hipEventRecord(start, ctx->stream);
+    }
+    const hipError_t e = launch();
+    if (start && stop) {
+        (void)hipEventRecord(stop, ctx->stream);
+        ctx->pending.push_back({ name, start, stop });
+    }
+    if (e != hipSuccess)
+        return hip_error(ctx, e, name);
+    return CKV_OK;
+}
+
+// Returns pinned staging memory of at least `bytes`, after the previous
+// upload from it has completed.
+int stage(ckv_context* ctx, size_t bytes, void** host)
+{
+    if (ctx->staging_pending) {
+        const hipError_t e = hipEventSynchronize(ctx->staging_done);
+        if (e != hipSuccess)
+            return hip_error(ctx, e, "staging wait");
+        ctx->staging_pending = false;
+    }
+    if (bytes > ctx->pinned_bytes) {
+        if (ctx->pinned)
+            (void)hipHostFree(ctx->pinned);
+        ctx->pinned = nullptr;
+        ctx->pinned_bytes = 0;
+        const size_t size = std::max<size_t>(bytes, 1 << 20);
+        const hipError_t e = hipHostMalloc(&ctx->pinned, size, hipHostMallocDefault);
+        if (e != hipSuccess)
+            return hip_error(ctx, e, "pinned staging allocation");
+        ctx->pinned_bytes = size;
+    }
+    *host = ctx->pinned;
+    return CKV_OK;
+}
+
+int upload_staged(ckv_context* ctx, void* device, size_t bytes)
+{
+    hipError_t e = hipMemcpyAsync(device, ctx->pinned, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess)
+        return hip_error(ctx, e, "metadata upload");
+    e = hipEventRecord(ctx->staging_done, ctx->stream);
+    if (e != hipSuccess)
+        return hip_error(ctx, e, "metadata upload event");
+    ctx->staging_pending = true;
+    return CKV_OK;
+}
+
+// Grow-only device buffer; the stream is drained before an old buffer is freed.
+template <class T>
+int ensure_device(ckv_context* ctx, T** ptr, size_t* capacity, size_t needed, const char* what)
+{
+    if (needed <= *capacity)
+        return CKV_OK;
+    if (*ptr) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(*ptr);
+        *ptr = nullptr;
+        *capacity = 0;
+    }
+    const size_t count = std::max(needed, (size_t)1024);
+    const hipError_t e = hipMalloc(reinterpret_cast<void**>(ptr), count * sizeof(T));
+    if (e != hipSuccess)
+        return hip_error(ctx, e, what);
+    *capacity = count;
+    return CKV_OK;
+}
+
+// Tokens per decode work item: enough (chunk, kv_head) waves for about 64 per
+// compute unit, a multiple of 16 tokens, between 32 and 4096. CKV_DECODE_CHUNK
+// overrides it (rounded to a multiple of 16).
+uint32_t choose_chunk(uint64_t token_heads, int cu_count)
+{
+    if (const char* forced = std::getenv("CKV_DECODE_CHUNK")) {
+        const long v = std::strtol(forced, nullptr, 10);
+        if (v >= 16)
+            return (uint32_t)((v + 15) / 16 * 16);
+    }
+    const uint64_t target = (uint64_t)std::max(cu_count, 1) * 64;
+    uint64_t chunk = (token_heads + target - 1) / target;
+    chunk = (chunk + 15) / 16 * 16;
+    return (uint32_t)std::clamp<uint64_t>(chunk, 32, 4096);
+}
+
+size_t round4(size_t words)
+{
+    return (words + 3) & ~(size_t)3;
+}
+
+int check_attention(const ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                    const void* output, size_t rows)
+{
+    ckv_context* ctx = pool->ctx;
+    if (rows && (!queries || !output))
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "queries and output are required");
+    // the order of validate_shapes (src/tensor/attention.cc:32-87)
+    if (!pool->uploaded)
+        return set_error(ctx, CKV_E_NO_TABLES, "attention before ckv_tables_upload");
+    if (rows != pool->positions.size())
+        return set_error(ctx, CKV_E_POSITION_COUNT_MISMATCH, "rows != uploaded positions");
+    if (q_heads == 0)
+        return set_error(ctx, CKV_E_INVALID_HEAD_COUNT, "q_heads == 0");
+    if (q_heads % pool->kv_heads != 0)
+        return set_error(ctx, CKV_E_INVALID_KV_HEAD_MAPPING, "q_heads % kv_heads != 0");
+    if (layer >= pool->layers)
+        return set_error(ctx, CKV_E_CACHE_LAYER_OUT_OF_RANGE, "layer >= layers");
+    return CKV_OK;
+}
+
+int run_decode(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads, float scale,
+               void* output)
+{
+    ckv_context* ctx = pool->ctx;
+    const pool_view view = view_of(pool);
+    float* partials = nullptr;
+    const bool needs_merge = std::any_of(pool->row_count.begin(), pool->row_count.end(),
+                                         [](uint32_t c) { return c > 1; });
+    if (needs_merge) {
+        size_t capacity_floats = pool->d_partials_bytes / sizeof(float);
+        const size_t needed = (pool->items.size() / 2) * q_heads
+            * partial_record_floats((uint32_t)pool->head_dim);
+        int status = ensure_device(ctx, &pool->d_partials, &capacity_floats, needed,
+                                   "decode partials");
+        if (status)
+            return status;
+        pool->d_partials_bytes = capacity_floats * sizeof(float);
+        partials = pool->d_partials;
+    }
+    int status = run_kernel(ctx, "paged_attention_decode", [&] {
+        return launch_decode(ctx->stream, view, pool->meta, (uint32_t)layer, queries,
+                             (uint32_t)q_heads, scale, output, partials);
+    });
+    if (status || !needs_merge)
+        return status;
+    return run_kernel(ctx, "paged_attention_merge", [&] {
+        return launch_merge(ctx->stream, view, pool->meta, (uint32_t)q_heads, output, partials);
+    });
+}
+
+int stage_pairs(ckv_pool* pool, const uint32_t* a, const uint32_t* b, size_t n)
+{
+    ckv_context* ctx = pool->ctx;
+    void* host = nullptr;
+    int status = stage(ctx, 2 * n * sizeof(uint32_t), &host);
+    if (status)
+        return status;
+    auto* words = static_cast<uint32_t*>(host);
+    for (size_t i = 0; i < n; ++i) {
+        words[2 * i] = a[i];
+        words[2 * i + 1] = b[i];
+    }
+    status = ensure_device(ctx, &pool->d_pairs, &pool->d_pairs_words, 2 * n, "pair buffer");
+    if (status)
+        return status;
+    return upload_staged(ctx, pool->d_pairs, 2 * n * sizeof(uint32_t));
+}
+
+// Uploads a plain u32 list into the pool's pair buffer.
+int stage_list(ckv_pool* pool, const uint32_t* list, size_t n)
+{
+    ckv_context* ctx = pool->ctx;
+    void* host = nullptr;
+    int status = stage(ctx, n * sizeof(uint32_t), &host);
+    if (status)
+        return status;
+    std::memcpy(host, list, n * sizeof(uint32_t));
+    status = ensure_device(ctx, &pool->d_pairs, &pool->d_pairs_words, n, "block list");
+    if (status)
+        return status;
+    return upload_staged(ctx, pool->d_pairs, n * sizeof(uint32_t));
+}
+
+int validate_prefix(const ckv_pool* pool, const uint32_t* blocks, size_t n_blocks, size_t tokens)
+{
+    // metal_kv_cache::valid_prefix (src/metal/metal_kv_cache.cc:205-223)
+    if (!tokens || tokens > pool->blocks * pool->block_size)
+        return CKV_E_STATE_INVALID_RESERVATION;
+    const size_t required = 1 + (tokens - 1) / pool->block_size;
+    if (!blocks || n_blocks < required)
+        return CKV_E_STATE_INVALID_RESERVATION;
+    for (size_t i = 0; i < required; ++i)
+        if (blocks[i] >= pool->blocks)
+            return CKV_E_STATE_INVALID_RESERVATION;
+    return CKV_OK;
+}
+
+int run_checkpoint(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks, size_t tokens,
+                   const void* packed_keys, const void* packed_values, bool unpack)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    int status = validate_prefix(pool, blocks, n_blocks, tokens);
+    if (status)
+        return set_error(ctx, status, "invalid checkpoint prefix");
+    if (!packed_keys || !packed_values)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "packed buffers are required");
+    const size_t required = 1 + (tokens - 1) / pool->block_size;
+    status = stage_list(pool, blocks, required);
+    if (status)
+        return status;
+    const pool_view view = view_of(pool);
+    return run_kernel(ctx, unpack ? "checkpoint_unpack" : "checkpoint_pack", [&] {
+        return launch_checkpoint(ctx->stream, view, (uint32_t)pool->layers, pool->d_pairs,
+                                 (uint32_t)tokens, const_cast<void*>(packed_keys),
+                                 const_cast<void*>(packed_values), unpack);
+    });
+}
+
+int create_pool(ckv_context* ctx, size_t layers, size_t blocks, size_t block_size,
+                size_t kv_heads, size_t head_dim, int dtype, void* keys, void* values,
+                ckv_pool** out)
+{
+    if (!ctx || !out)
+        return CKV_E_INVALID_ARGUMENT;
+    *out = nullptr;
+    // metal_kv_cache::make (src/metal/metal_kv_cache.cc:38-82)
+    if (layers == 0)
+        return set_error(ctx, CKV_E_INVALID_LAYER_COUNT, "layers == 0");
+    if (blocks == 0)
+        return set_error(ctx, CKV_E_INVALID_BLOCK_COUNT, "blocks == 0");
+    if (block_size == 0)
+        return set_error(ctx, CKV_E_INVALID_BLOCK_SIZE, "block_size == 0");
+    if (kv_heads == 0)
+        return set_error(ctx, CKV_E_INVALID_KV_HEAD_COUNT, "kv_heads == 0");
+    if (head_dim == 0)
+        return set_error(ctx, CKV_E_INVALID_HEAD_DIMENSION_KV, "head_dim == 0");
+    if (dtype != CKV_F32 && dtype != CKV_BF16 && dtype != CKV_F16)
+        return set_error(ctx, CKV_E_UNSUPPORTED_DTYPE, "dtype must be f32, bf16 or f16");
+    const size_t elem = dtype == CKV_F32 ? 4 : 2;
+    size_t elements = layers, bytes = 0, slots = 0, features = 0;
+    if (!mul_fits(elements, blocks, &elements) || !mul_fits(elements, block_size, &elements)
+        || !mul_fits(elements, kv_heads, &elements) || !mul_fits(elements, head_dim, &elements)
+        || !mul_fits(elements, elem, &bytes) || !mul_fits(blocks, block_size, &slots)
+        || slots > UINT32_MAX || !mul_fits(kv_heads, head_dim, &features)
+        || features > UINT32_MAX || layers > UINT32_MAX)
+        return set_error(ctx, CKV_E_LAYOUT_SIZE_OVERFLOW, "KV layout does not fit");
+    auto* pool = new (std::nothrow) ckv_pool;
+    if (!pool)
+        return set_error(ctx, CKV_E_KV_ALLOCATION_FAILED, "pool object");
+    pool->ctx = ctx;
+    pool->layers = layers;
+    pool->blocks = blocks;
+    pool->block_size = block_size;
+    pool->kv_heads = kv_heads;
+    pool->head_dim = head_dim;
+    pool->dtype = dtype;
+    pool->elem_size = elem;
+    pool->bytes_each = bytes;
+    if (keys || values) {
+        if (!keys || !values) {
+            delete pool;
+            return set_error(ctx, CKV_E_INVALID_ARGUMENT, "both buffers are required");
+        }
+        pool->keys = keys;
+        pool->values = values;
+        pool->owned = false;
+    } else {
+        (void)hipSetDevice(ctx->device);
+        hipError_t e = hipMalloc(&pool->keys, bytes);
+        if (e == hipSuccess)
+            e = hipMalloc(&pool->values, bytes);
+        if (e != hipSuccess) {
+            if (pool->keys)
+                (void)hipFree(pool->keys);
+            delete pool;
+            (void)hipGetLastError();
+            return set_error(ctx, CKV_E_KV_ALLOCATION_FAILED,
+                             std::string("KV allocation: ") + hipGetErrorString(e));
+        }
+        pool->owned = true;
+    }
+    *out = pool;
+    return CKV_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int ckv_abi_version(void)
+{
+    return CKV_ABI_VERSION;
+}
+
+const char* ckv_error_name(int code)
+{
+    static const char* tensor_op[] = {
+        "tensor_op.tensor_creation_failed",
+        "tensor_op.allocation_failed",
+        "tensor_op.empty_tokens",
+        "tensor_op.empty_logits_indices",
+        "tensor_op.invalid_hidden_states",
+        "tensor_op.logits_index_out_of_range",
+        "tensor_op.token_id_overflow",
+        "tensor_op.invalid_rank",
+        "tensor_op.unsupported_dtype",
+        "tensor_op.input_shape_mismatch",
+        "tensor_op.inner_dimension_mismatch",
+        "tensor_op.output_shape_mismatch",
+        "tensor_op.token_out_of_range",
+        "tensor_op.invalid_epsilon",
+        "tensor_op.position_count_mismatch",
+        "tensor_op.invalid_head_count",
+        "tensor_op.invalid_head_dimension",
+        "tensor_op.invalid_rope_theta",
+        "tensor_op.cache_slot_count_mismatch",
+        "tensor_op.cache_feature_count_mismatch",
+        "tensor_op.cache_layer_out_of_range",
+        "tensor_op.cache_slot_out_of_range",
+        "tensor_op.block_table_metadata_count_mismatch",
+        "tensor_op.block_table_range_out_of_bounds",
+        "tensor_op.cache_block_out_of_range",
+        "tensor_op.cache_head_dimension_mismatch",
+        "tensor_op.invalid_kv_head_mapping",
+        "tensor_op.backend_failure",
+        "tensor_op.unsupported_aliasing",
+    };
+    static const char* kv_cache[] = {
+        "kv_cache.invalid_layer_count",    "kv_cache.invalid_block_count",
+        "kv_cache.invalid_block_size",     "kv_cache.invalid_kv_head_count",
+        "kv_cache.invalid_head_dimension", "kv_cache.layout_size_overflow",
+        "kv_cache.allocation_failed",      "kv_cache.layer_out_of_range",
+        "kv_cache.block_out_of_range",     "kv_cache.token_offset_out_of_range",
+        "kv_cache.kv_head_out_of_range",   "kv_cache.head_feature_out_of_range",
+    };
+    static const char* state[] = {
+        "state.capacity_exhausted",
+        "state.invalid_reservation",
+        "state.backend_failure",
+        "state.allocation_failed",
+    };
+    static const char* own[] = {
+        "ckv.invalid_argument",
+        "ckv.hip_failure",
+        "ckv.no_device",
+        "ckv.no_tables",
+    };
+    if (code == 0)
+        return "ok";
+    if (code >= 100 && code < 100 + (int)(sizeof tensor_op / sizeof *tensor_op))
+        return tensor_op[code - 100];
+    if (code >= 200 && code < 200 + (int)(sizeof kv_cache / sizeof *kv_cache))
+        return kv_cache[code - 200];
+    if (code >= 300 && code < 300 + (int)(sizeof state / sizeof *state))
+        return state[code - 300];
+    if (code >= 400 && code < 400 + (int)(sizeof own / sizeof *own))
+        return own[code - 400];
+    return "ckv.unknown_error";
+}
+
+const char* ckv_last_error(const ckv_context* ctx)
+{
+    return ctx ? ctx->last_error.c_str() : "";
+}
+
+int ckv_context_create(int device, ckv_context** out)
+{
+    if (!out)
+        return CKV_E_INVALID_ARGUMENT;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) {
+        (void)hipGetLastError();
+        return CKV_E_NO_DEVICE;
+    }
+    auto* ctx = new (std::nothrow) ckv_context;
+    if (!ctx)
+        return CKV_E_INVALID_ARGUMENT;
+    ctx->device = device;
+    hipError_t e = hipSetDevice(device);
+    hipDeviceProp_t props {};
+    if (e == hipSuccess)
+        e = hipGetDeviceProperties(&props, device);
+    if (e == hipSuccess)
+        e = hipStreamCreate(&ctx->own_stream);
+    if (e == hipSuccess)
+        e = hipEventCreateWithFlags(&ctx->staging_done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        if (ctx->own_stream)
+            (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return CKV_E_HIP_FAILURE;
+    }
+    ctx->cu_count = props.multiProcessorCount;
+    ctx->stream = ctx->own_stream;
+    *out = ctx;
+    return CKV_OK;
+}
+
+int ckv_context_destroy(ckv_context* ctx)
+{
+    if (!ctx)
+        return CKV_E_INVALID_ARGUMENT;
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto& p : ctx->pending) {
+        (void)hipEventDestroy(p.start);
+        (void)hipEventDestroy(p.stop);
+    }
+    for (auto e : ctx->spare_events)
+        (void)hipEventDestroy(e);
+    if (ctx->pinned)
+        (void)hipHostFree(ctx->pinned);
+    (void)hipEventDestroy(ctx->staging_done);
+    (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return CKV_OK;
+}
+
+int ckv_context_set_stream(ckv_context* ctx, void* hip_stream)
+{
+    if (!ctx)
+        return CKV_E_INVALID_ARGUMENT;
+    // work already enqueued on the old stream finishes before the switch
+    (void)hipStreamSynchronize(ctx->stream);
+    ctx->stream = static_cast<hipStream_t>(hip_stream);
+    return CKV_OK;
+}
+
+void* ckv_context_stream(const ckv_context* ctx)
+{
+    return ctx ? ctx->stream : nullptr;
+}
+
+void* ckv_context_own_stream(const ckv_context* ctx)
+{
+    return ctx ? ctx->own_stream : nullptr;
+}
+
+int ckv_sync(ckv_context* ctx)
+{
+    if (!ctx)
+        return CKV_E_INVALID_ARGUMENT;
+    const hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess)
+        return hip_error(ctx, e, "stream synchronize");
+    return CKV_OK;
+}
+
+int ckv_profile_enable(ckv_context* ctx, int enabled)
+{
+    if (!ctx)
+        return CKV_E_INVALID_ARGUMENT;
+    ctx->profile = enabled != 0;
+    return CKV_OK;
+}
+
+int ckv_profile_query(ckv_context* ctx, const char* kernel, double* total_ms, uint64_t* launches)
+{
+    if (!ctx || !kernel)
+        return CKV_E_INVALID_ARGUMENT;
+    for (auto& p : ctx->pending) {
+        hipError_t e = hipEventSynchronize(p.stop);
+        float ms = 0.0f;
+        if (e == hipSuccess)
+            e = hipEventElapsedTime(&ms, p.start, p.stop);
+        if (e != hipSuccess)
+            return hip_error(ctx, e, "profile events");
+        auto& total = ctx->totals[p.name];
+        total.ms += ms;
+        total.launches += 1;
+        ctx->spare_events.push_back(p.start);
+        ctx->spare_events.push_back(p.stop);
+    }
+    ctx->pending.clear();
+    const auto found = ctx->totals.find(kernel);
+    if (total_ms)
+        *total_ms = found == ctx->totals.end() ? 0.0 : found->second.ms;
+    if (launches)
+        *launches = found == ctx->totals.end() ? 0 : found->second.launches;
+    return CKV_OK;
+}
+
+int ckv_profile_reset(ckv_context* ctx)
+{
+    if (!ctx)
+        return CKV_E_INVALID_ARGUMENT;
+    double ms;
+    uint64_t n;
+    const int status = ckv_profile_query(ctx, "", &ms, &n); // drains pending events
+    ctx->totals.clear();
+    return status;
+}
+
+int ckv_pool_create(ckv_context* ctx, size_t layers, size_t blocks, size_t block_size,
+                    size_t kv_heads, size_t head_dim, int dtype, ckv_pool** out)
+{
+    return create_pool(ctx, layers, blocks, block_size, kv_heads, head_dim, dtype, nullptr,
+                       nullptr, out);
+}
+
+int ckv_pool_wrap(ckv_context* ctx, size_t layers, size_t blocks, size_t block_size,
+                  size_t kv_heads, size_t head_dim, int dtype, void* keys, void* values,
+                  ckv_pool** out)
+{
+    if (!keys || !values)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "both buffers are required");
+    return create_pool(ctx, layers, blocks, block_size, kv_heads, head_dim, dtype, keys, values,
+                       out);
+}
+
+int ckv_pool_destroy(ckv_pool* pool)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    (void)hipStreamSynchronize(pool->ctx->stream);
+    if (pool->owned) {
+        (void)hipFree(pool->keys);
+        (void)hipFree(pool->values);
+    }
+    if (pool->d_meta)
+        (void)hipFree(pool->d_meta);
+    if (pool->d_partials)
+        (void)hipFree(pool->d_partials);
+    if (pool->d_pairs)
+        (void)hipFree(pool->d_pairs);
+    delete pool;
+    return CKV_OK;
+}
+
+int ckv_pool_buffers(const ckv_pool* pool, void** keys, void** values, size_t* bytes_each)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    if (keys)
+        *keys = pool->keys;
+    if (values)
+        *values = pool->values;
+    if (bytes_each)
+        *bytes_each = pool->bytes_each;
+    return CKV_OK;
+}
+
+int ckv_element_offset(const ckv_pool* pool, size_t layer, size_t block, size_t token_offset,
+                       size_t kv_head, size_t head_feature, size_t* offset)
+{
+    if (!pool || !offset)
+        return CKV_E_INVALID_ARGUMENT;
+    if (layer >= pool->layers)
+        return CKV_E_LAYER_OUT_OF_RANGE;
+    if (block >= pool->blocks)
+        return CKV_E_BLOCK_OUT_OF_RANGE;
+    if (token_offset >= pool->block_size)
+        return CKV_E_TOKEN_OFFSET_OUT_OF_RANGE;
+    if (kv_head >= pool->kv_heads)
+        return CKV_E_KV_HEAD_OUT_OF_RANGE;
+    if (head_feature >= pool->head_dim)
+        return CKV_E_HEAD_FEATURE_OUT_OF_RANGE;
+    *offset = (((layer * pool->blocks + block) * pool->block_size + token_offset) * pool->kv_heads
+               + kv_head)
+            * pool->head_dim
+        + head_feature;
+    return CKV_OK;
+}
+
+int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entries,
+                      const uint32_t* offsets, const uint32_t* lengths,
+                      const uint32_t* positions, const uint32_t* slots, size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if ((n_entries && !block_table) || (rows && (!offsets || !lengths || !positions)))
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "metadata arrays are required");
+    if (n_entries > UINT32_MAX || rows > UINT32_MAX)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "metadata exceeds u32 counts");
+    const size_t bs = pool->block_size;
+    // prepared_attention_batch::make (src/tensor/attention.cc:110-137): row ranges
+    // first, then every table entry
+    for (size_t r = 0; r < rows; ++r) {
+        const size_t required = positions[r] / bs + 1;
+        if (offsets[r] > n_entries || lengths[r] > n_entries - offsets[r] || required > lengths[r])
+            return set_error(ctx, CKV_E_BLOCK_TABLE_RANGE_OUT_OF_BOUNDS,
+                             "row " + std::to_string(r) + " table range");
+    }
+    for (size_t i = 0; i < n_entries; ++i)
+        if (block_table[i] >= pool->blocks)
+            return set_error(ctx, CKV_E_CACHE_BLOCK_OUT_OF_RANGE,
+                             "table entry " + std::to_string(i));
+    // store_kv's slot check (src/tensor/tensor_ops.cc:445-453)
+    const size_t slot_count = pool->blocks * bs;
+    if (slots)
+        for (size_t r = 0; r < rows; ++r)
+            if (slots[r] >= slot_count)
+                return set_error(ctx, CKV_E_CACHE_SLOT_OUT_OF_RANGE,
+                                 "slot of row " + std::to_string(r));
+
+    // decode work list
+    uint64_t token_heads = 0;
+    for (size_t r = 0; r < rows; ++r)
+        token_heads += ((uint64_t)positions[r] + 1) * pool->kv_heads;
+    const uint32_t chunk = choose_chunk(token_heads, ctx->cu_count);
+    std::vector<uint32_t> items, row_first(rows), row_count(rows);
+    for (size_t r = 0; r < rows; ++r) {
+        const uint32_t n = positions[r] / chunk + 1;
+        row_first[r] = (uint32_t)(items.size() / 2);
+        row_count[r] = n;
+        for (uint32_t c = 0; c < n; ++c) {
+            items.push_back((uint32_t)r);
+            items.push_back(c);
+        }
+    }
+    if (items.size() / 2 > UINT32_MAX / pool->kv_heads)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "too many decode work items");
+    // query tiles: runs of consecutive positions sharing a table range
+    // (src/tensor/attention.cc:142-167), up to prefill_tile_rows rows
+    std::vector<uint32_t> tiles;
+    bool shared = false;
+    for (size_t r = 0; r < rows;) {
+        size_t n = 1;
+        while (n < prefill_tile_rows && r + n < rows && offsets[r + n] == offsets[r]
+               && lengths[r + n] == lengths[r] && positions[r + n] == positions[r + n - 1] + 1)
+            ++n;
+        tiles.push_back((uint32_t)r);
+        tiles.push_back((uint32_t)n);
+        shared = shared || n > 1;
+        r += n;
+    }
+
+    // pack: table | offsets | lengths | positions | slots | items | row_first | row_count | tiles
+    const size_t s_table = 0;
+    const size_t s_offsets = s_table + round4(n_entries);
+    const size_t s_lengths = s_offsets + round4(rows);
+    const size_t s_positions = s_lengths + round4(rows);
+    const size_t s_slots = s_positions + round4(rows);
+    const size_t s_items = s_slots + round4(rows);
+    const size_t s_first = s_items + round4(items.size());
+    const size_t s_count = s_first + round4(rows);
+    const size_t s_tiles = s_count + round4(rows);
+    const size_t words = s_tiles + round4(tiles.size());
+    void* host = nullptr;
+    int status = stage(ctx, std::max<size_t>(words, 4) * sizeof(uint32_t), &host);
+    if (status)
+        return status;
+    auto* w = static_cast<uint32_t*>(host);
+    std::memset(w, 0, words * sizeof(uint32_t));
+    auto put = [&](size_t at, const uint32_t* src, size_t n) {
+        if (n)
+            std::memcpy(w + at, src, n * sizeof(uint32_t));
+    };
+    put(s_table, block_table, n_entries);
+    put(s_offsets, offsets, rows);
+    put(s_lengths, lengths, rows);
+    put(s_positions, positions, rows);
+    if (slots)
+        put(s_slots, slots, rows);
+    put(s_items, items.data(), items.size());
+    put(s_first, row_first.data(), rows);
+    put(s_count, row_count.data(), rows);
+    put(s_tiles, tiles.data(), tiles.size());
+    status = ensure_device(ctx, &pool->d_meta, &pool->d_meta_words, std::max<size_t>(words, 4),
+                           "metadata buffer");
+    if (status)
+        return status;
+    status = upload_staged(ctx, pool->d_meta, words * sizeof(uint32_t));
+    if (status)
+        return status;
+
+    meta_view& m = pool->meta;
+    m.table = pool->d_meta + s_table;
+    m.offsets = pool->d_meta + s_offsets;
+    m.lengths = pool->d_meta + s_lengths;
+    m.positions = pool->d_meta + s_positions;
+    m.slots = pool->d_meta + s_slots;
+    m.items = pool->d_meta + s_items;
+    m.row_first = pool->d_meta + s_first;
+    m.row_count = pool->d_meta + s_count;
+    m.tiles = pool->d_meta + s_tiles;
+    m.n_entries = (uint32_t)n_entries;
+    m.rows = (uint32_t)rows;
+    m.n_items = (uint32_t)(items.size() / 2);
+    m.chunk = chunk;
+    m.n_tiles = (uint32_t)(tiles.size() / 2);
+
+    pool->table.assign(block_table, block_table + n_entries);
+    pool->offsets.assign(offsets, offsets + rows);
+    pool->lengths.assign(lengths, lengths + rows);
+    pool->positions.assign(positions, positions + rows);
+    pool->has_slots = slots != nullptr;
+    if (slots)
+        pool->slots.assign(slots, slots + rows);
+    else
+        pool->slots.clear();
+    pool->items = std::move(items);
+    pool->row_first = std::move(row_first);
+    pool->row_count = std::move(row_count);
+    pool->tiles = std::move(tiles);
+    pool->chunk = chunk;
+    pool->shared_tile = shared;
+    pool->uploaded = true;
+    return CKV_OK;
+}
+
+int ckv_tables_patch(ckv_pool* pool, const uint32_t* idx, const uint32_t* val, size_t n)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if (!n)
+        return CKV_OK;
+    if (!idx || !val)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "patch arrays are required");
+    if (!pool->uploaded)
+        return set_error(ctx, CKV_E_NO_TABLES, "patch before ckv_tables_upload");
+    for (size_t i = 0; i < n; ++i) {
+        if (idx[i] >= pool->table.size())
+            return set_error(ctx, CKV_E_BLOCK_TABLE_RANGE_OUT_OF_BOUNDS, "patch index");
+        if (val[i] >= pool->blocks)
+            return set_error(ctx, CKV_E_CACHE_BLOCK_OUT_OF_RANGE, "patch value");
+    }
+    int status = stage_pairs(pool, idx, val, n);
+    if (status)
+        return status;
+    for (size_t i = 0; i < n; ++i)
+        pool->table[idx[i]] = val[i];
+    uint32_t* table = pool->d_meta; // the table section starts the metadata block
+    return run_kernel(ctx, "tables_patch", [&] {
+        return launch_table_patch(ctx->stream, table, pool->d_pairs, (uint32_t)n);
+    });
+}
+
+int ckv_append(ckv_pool* pool, size_t layer, const void* keys, const void* values, size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if (rows && (!keys || !values))
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "keys and values are required");
+    if (!pool->uploaded || !pool->has_slots)
+        return set_error(ctx, CKV_E_NO_TABLES, "append before slots were uploaded");
+    if (rows != pool->slots.size())
+        return set_error(ctx, CKV_E_CACHE_SLOT_COUNT_MISMATCH, "rows != uploaded slots");
+    if (layer >= pool->layers)
+        return set_error(ctx, CKV_E_CACHE_LAYER_OUT_OF_RANGE, "layer >= layers");
+    const pool_view view = view_of(pool);
+    return run_kernel(ctx, "store_kv", [&] {
+        return launch_store_kv(ctx->stream, view, pool->meta, (uint32_t)layer, keys, values,
+                               (uint32_t)rows);
+    });
+}
+
+int ckv_gather(ckv_pool* pool, size_t layer, size_t table_offset, size_t table_length,
+               size_t n_tokens, void* out_keys, void* out_values)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if (n_tokens && (!out_keys || !out_values))
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "outputs are required");
+    if (!pool->uploaded)
+        return set_error(ctx, CKV_E_NO_TABLES, "gather before ckv_tables_upload");
+    if (layer >= pool->layers)
+        return set_error(ctx, CKV_E_CACHE_LAYER_OUT_OF_RANGE, "layer >= layers");
+    if (table_offset > pool->table.size() || table_length > pool->table.size() - table_offset
+        || n_tokens > table_length * pool->block_size)
+        return set_error(ctx, CKV_E_BLOCK_TABLE_RANGE_OUT_OF_BOUNDS, "gather range");
+    const pool_view view = view_of(pool);
+    const uint32_t* table = pool->meta.table + table_offset;
+    return run_kernel(ctx, "gather_kv", [&] {
+        return launch_gather(ctx->stream, view, table, (uint32_t)layer, (uint32_t)n_tokens,
+                             out_keys, out_values);
+    });
+}
+
+int ckv_decode_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                         float scale, void* output, size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    const int status = check_attention(pool, layer, queries, q_heads, output, rows);
+    if (status || !rows)
+        return status;
+    return run_decode(pool, layer, queries, q_heads, scale, output);
+}
+
+int ckv_prefill_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                          float scale, void* output, size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    const int status = check_attention(pool, layer, queries, q_heads, output, rows);
+    if (status || !rows)
+        return status;
+    const pool_view view = view_of(pool);
+    if (!prefill_supported(view, (uint32_t)q_heads))
+        return run_decode(pool, layer, queries, q_heads, scale, output);
+    ckv_context* ctx = pool->ctx;
+    return run_kernel(ctx, "paged_attention_prefill", [&] {
+        return launch_prefill(ctx->stream, view, pool->meta, (uint32_t)layer, queries,
+                              (uint32_t)q_heads, scale, output);
+    });
+}
+
+int ckv_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                  float scale, void* output, size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    // src/tensor/attention.cc:290-309: tiles are used when some run of rows
+    // shares a query tile and head_dim <= 128
+    if (pool->shared_tile && pool->head_dim <= 128)
+        return ckv_prefill_attention(pool, layer, queries, q_heads, scale, output, rows);
+    return ckv_decode_attention(pool, layer, queries, q_heads, scale, output, rows);
+}
+
+int ckv_copy_blocks(ckv_pool* pool, const uint32_t* src, const uint32_t* dst, size_t n)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if (!n)
+        return CKV_OK;
+    if (!src || !dst)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "block lists are required");
+    std::unordered_set<uint32_t> targets, sources(src, src + n);
+    for (size_t i = 0; i < n; ++i) {
+        if (src[i] >= pool->blocks || dst[i] >= pool->blocks)
+            return set_error(ctx, CKV_E_CACHE_BLOCK_OUT_OF_RANGE, "copy block id");
+        if (!targets.insert(dst[i]).second || sources.count(dst[i]))
+            return set_error(ctx, CKV_E_UNSUPPORTED_ALIASING, "copy targets overlap");
+    }
+    int status = stage_pairs(pool, src, dst, n);
+    if (status)
+        return status;
+    const pool_view view = view_of(pool);
+    return run_kernel(ctx, "copy_blocks", [&] {
+        return launch_copy_blocks(ctx->stream, view, (uint32_t)pool->layers, pool->d_pairs,
+                                  (uint32_t)n);
+    });
+}
+
+int ckv_checkpoint_pack(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks, size_t tokens,
+                        void* packed_keys, void* packed_values)
+{
+    return run_checkpoint(pool, blocks, n_blocks, tokens, packed_keys, packed_values, false);
+}
+
+int ckv_checkpoint_unpack(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks,
+                          size_t tokens, const void* packed_keys, const void* packed_values)
+{
+    return run_checkpoint(pool, blocks, n_blocks, tokens, packed_keys, packed_values, true);
+}
+
+} // extern "C"

@@ -1,0 +1,144 @@
+// Internal declarations of libckv: context/pool state and kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "ckv.h"
+
+namespace ckv {
+
+// Geometry of one KV tensor as the kernels see it. Element index of
+// (layer, slot, kv_head, feature) is (layer*slot_count + slot)*F + kv_head*D + feature.
+struct pool_view {
+    void* keys;
+    void* values;
+    uint64_t layer_elems; // blocks * block_size * F
+    uint32_t blocks;
+    uint32_t block_size;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t features; // kv_heads * head_dim
+    uint32_t elem_size;
+    int dtype; // ckv_dtype
+};
+
+// Device pointers into the uploaded metadata block (one H2D copy per upload).
+struct meta_view {
+    const uint32_t* table;
+    const uint32_t* offsets;
+    const uint32_t* lengths;
+    const uint32_t* positions;
+    const uint32_t* slots;
+    const uint32_t* items; // decode work list: (row, chunk) pairs
+    const uint32_t* row_first; // first work item of each row
+    const uint32_t* row_count; // work items (chunks) of each row
+    const uint32_t* tiles;     // prefill query tiles: (first row, row count) pairs
+    uint32_t n_entries;
+    uint32_t rows;
+    uint32_t n_items;
+    uint32_t chunk; // tokens per decode work item, a multiple of 16
+    uint32_t n_tiles;
+};
+
+// Largest query tile of the prefill kernel, in rows (positions).
+constexpr uint32_t prefill_tile_rows = 64;
+
+struct pending_timing {
+    const char* name;
+    hipEvent_t start;
+    hipEvent_t stop;
+};
+
+struct profile_total {
+    double ms = 0.0;
+    uint64_t launches = 0;
+};
+
+} // namespace ckv
+
+struct ckv_context {
+    int device = 0;
+    int cu_count = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::string last_error;
+
+    // pinned staging for metadata uploads; reused after staging_done completes
+    void* pinned = nullptr;
+    size_t pinned_bytes = 0;
+    hipEvent_t staging_done = nullptr;
+    bool staging_pending = false;
+
+    bool profile = false;
+    std::vector<ckv::pending_timing> pending;
+    std::vector<hipEvent_t> spare_events;
+    std::map<std::string, ckv::profile_total> totals;
+};
+
+struct ckv_pool {
+    ckv_context* ctx = nullptr;
+    size_t layers = 0, blocks = 0, block_size = 0, kv_heads = 0, head_dim = 0;
+    int dtype = CKV_BF16;
+    size_t elem_size = 2;
+    void* keys = nullptr;
+    void* values = nullptr;
+    size_t bytes_each = 0;
+    bool owned = false;
+
+    // host mirror of the uploaded metadata
+    bool uploaded = false;
+    bool has_slots = false;
+    std::vector<uint32_t> table, offsets, lengths, positions, slots;
+    std::vector<uint32_t> items, row_first, row_count, tiles;
+    uint32_t chunk = 0;
+    bool shared_tile = false;
+
+    // device copies
+    uint32_t* d_meta = nullptr;
+    size_t d_meta_words = 0;
+    ckv::meta_view meta {};
+
+    // device scratch
+    float* d_partials = nullptr;
+    size_t d_partials_bytes = 0;
+    uint32_t* d_pairs = nullptr; // block-id pairs / patch pairs
+    size_t d_pairs_words = 0;
+};
+
+namespace ckv {
+
+// ---- launchers (kernels_copy.hip) ------------------------------------------
+hipError_t launch_store_kv(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
+                           const void* keys, const void* values, uint32_t rows);
+hipError_t launch_gather(hipStream_t s, const pool_view& p, const uint32_t* table,
+                         uint32_t layer, uint32_t n_tokens, void* out_keys, void* out_values);
+hipError_t launch_copy_blocks(hipStream_t s, const pool_view& p, uint32_t layers,
+                              const uint32_t* pairs, uint32_t n);
+hipError_t launch_checkpoint(hipStream_t s, const pool_view& p, uint32_t layers,
+                             const uint32_t* blocks, uint32_t tokens, void* packed_keys,
+                             void* packed_values, bool unpack);
+hipError_t launch_table_patch(hipStream_t s, uint32_t* table, const uint32_t* pairs, uint32_t n);
+
+// ---- launchers (kernels_decode.hip) ------------------------------------------
+// Returns hipErrorInvalidValue when no kernel fits the geometry.
+hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
+                         const void* q, uint32_t q_heads, float scale, void* out,
+                         float* partials);
+hipError_t launch_merge(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t q_heads,
+                        void* out, const float* partials);
+bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads);
+// Floats per (work item, q head) partial record: [max, denominator, 0, 0, acc[head_dim]].
+uint32_t partial_record_floats(uint32_t head_dim);
+
+// ---- launchers (kernels_prefill.hip) ------------------------------------------
+bool prefill_supported(const pool_view& p, uint32_t q_heads);
+hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
+                          const void* q, uint32_t q_heads, float scale, void* out);
+
+} // namespace ckv

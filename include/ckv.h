@@ -1,0 +1,229 @@
+/*
+ * ckv.h - C ABI of the MI355X paged KV-cache + attention path (libckv.so).
+ *
+ * The library replaces chibillm's Metal KV-cache path: the KV tensors and
+ * dispatches of metal_kv_cache / metal_kernels (src/metal/metal_kv_cache.h:75-122,
+ * src/metal/metal_kernels.h:76-123) and the host checks of store_kv /
+ * paged_attention (src/tensor/tensor_ops.cc:412-463, src/tensor/attention.cc:8-254).
+ * The C++ host layer (block_manager, scheduler, prefix_cache, model_batch,
+ * hip_model_state) calls these functions; so can a ctypes or other FFI binding.
+ *
+ * Conventions
+ *  - Every function returns an int status: 0 on success, else one of the
+ *    CKV_E_* codes below. ckv_error_name(code) gives the reference's
+ *    "namespace.name" string for it.
+ *  - Pointers named in device memory (keys, values, queries, output,
+ *    checkpoint buffers) are HIP device pointers. Metadata arrays (tables,
+ *    slots, positions, block ids) are host pointers, borrowed only for the
+ *    duration of the call; the library validates them on the host and uploads
+ *    them with one pinned host-to-device copy.
+ *  - All work is enqueued on the context's stream, in call order. ckv_sync is
+ *    the single wait (the role of end_compute_pass, src/metal/metal_context.h:99-110).
+ *  - A context and its pools are not thread-safe; one thread drives them
+ *    (src/serving_runtime.cc:364-392 has exactly one engine thread).
+ *
+ * KV layout in HBM (one allocation each for keys and values):
+ *   [layer][block][token_in_block][kv_head][feature]
+ * exactly the reference's element_offset order (src/metal/metal_kv_cache.cc:150-179),
+ * stored as f32, bf16 or fp16 (the reference stores f32).
+ */
+#ifndef CHIBILLM_CKV_H
+#define CHIBILLM_CKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CKV_ABI_VERSION 1
+
+typedef struct ckv_context ckv_context;
+typedef struct ckv_pool ckv_pool;
+
+/* Element types. f32 and bf16 follow src/tensor/types.h:90-95; fp16 is new. */
+enum ckv_dtype { CKV_F32 = 0, CKV_BF16 = 1, CKV_F16 = 2 };
+
+/* Status codes. 1xx = tensor_op_errc + 100 (src/tensor/tensor_ops.h:18-48),
+ * 2xx = kv_cache_errc + 200 (src/metal/metal_kv_cache.h:42-55),
+ * 3xx = state_errc + 300 (src/model_state.h:10-15), 4xx = this library. */
+enum ckv_status {
+    CKV_OK = 0,
+    CKV_E_TENSOR_ALLOCATION_FAILED = 101,
+    CKV_E_INVALID_RANK = 107,
+    CKV_E_UNSUPPORTED_DTYPE = 108,
+    CKV_E_INPUT_SHAPE_MISMATCH = 109,
+    CKV_E_OUTPUT_SHAPE_MISMATCH = 111,
+    CKV_E_POSITION_COUNT_MISMATCH = 114,
+    CKV_E_INVALID_HEAD_COUNT = 115,
+    CKV_E_INVALID_HEAD_DIMENSION = 116,
+    CKV_E_CACHE_SLOT_COUNT_MISMATCH = 118,
+    CKV_E_CACHE_FEATURE_COUNT_MISMATCH = 119,
+    CKV_E_CACHE_LAYER_OUT_OF_RANGE = 120,
+    CKV_E_CACHE_SLOT_OUT_OF_RANGE = 121,
+    CKV_E_BLOCK_TABLE_METADATA_COUNT_MISMATCH = 122,
+    CKV_E_BLOCK_TABLE_RANGE_OUT_OF_BOUNDS = 123,
+    CKV_E_CACHE_BLOCK_OUT_OF_RANGE = 124,
+    CKV_E_CACHE_HEAD_DIMENSION_MISMATCH = 125,
+    CKV_E_INVALID_KV_HEAD_MAPPING = 126,
+    CKV_E_BACKEND_FAILURE = 127,
+    CKV_E_UNSUPPORTED_ALIASING = 128,
+    CKV_E_INVALID_LAYER_COUNT = 200,
+    CKV_E_INVALID_BLOCK_COUNT = 201,
+    CKV_E_INVALID_BLOCK_SIZE = 202,
+    CKV_E_INVALID_KV_HEAD_COUNT = 203,
+    CKV_E_INVALID_HEAD_DIMENSION_KV = 204,
+    CKV_E_LAYOUT_SIZE_OVERFLOW = 205,
+    CKV_E_KV_ALLOCATION_FAILED = 206,
+    CKV_E_LAYER_OUT_OF_RANGE = 207,
+    CKV_E_BLOCK_OUT_OF_RANGE = 208,
+    CKV_E_TOKEN_OFFSET_OUT_OF_RANGE = 209,
+    CKV_E_KV_HEAD_OUT_OF_RANGE = 210,
+    CKV_E_HEAD_FEATURE_OUT_OF_RANGE = 211,
+    CKV_E_STATE_CAPACITY_EXHAUSTED = 300,
+    CKV_E_STATE_INVALID_RESERVATION = 301,
+    CKV_E_STATE_BACKEND_FAILURE = 302,
+    CKV_E_STATE_ALLOCATION_FAILED = 303,
+    CKV_E_INVALID_ARGUMENT = 400, /* null pointer or zero where a value is required */
+    CKV_E_HIP_FAILURE = 401,      /* a HIP runtime call failed; see ckv_last_error */
+    CKV_E_NO_DEVICE = 402,
+    CKV_E_NO_TABLES = 403,        /* an op needs metadata that was never uploaded */
+};
+
+/* Name of a status code, e.g. "tensor_op.cache_slot_out_of_range".
+ * Replaces error_name() of each reference enum (src/tensor/tensor_ops.h:50-86,
+ * src/metal/metal_kv_cache.h:57-70, src/model_state.h:17-28). */
+const char* ckv_error_name(int code);
+/* Detail text of the last failure on this context (HIP error string, etc.);
+ * the role of error<Code>::detail (src/error.h:13-31). Never NULL. */
+const char* ckv_last_error(const ckv_context* ctx);
+int ckv_abi_version(void);
+
+/* ---- Context: device + stream (src/metal/metal_context.h:87-120) ---------- */
+int ckv_context_create(int device, ckv_context** out);
+int ckv_context_destroy(ckv_context* ctx);
+/* Enqueue on hip_stream from now on, e.g. a framework's current stream so
+ * that ckv work is ordered after the framework's writes of its inputs. NULL
+ * is the device's null (default) stream. Work already enqueued on the
+ * previous stream is drained first. */
+int ckv_context_set_stream(ckv_context* ctx, void* hip_stream);
+/* The stream currently used, and the stream the context created for itself
+ * (used until ckv_context_set_stream is called). */
+void* ckv_context_stream(const ckv_context* ctx);
+void* ckv_context_own_stream(const ckv_context* ctx);
+/* Waits for all work enqueued on the context's stream. */
+int ckv_sync(ckv_context* ctx);
+
+/* Per-kernel GPU timing, the role of CHIBILLM_PROFILE
+ * (src/metal/metal_context.mm:94-169): when enabled, every launch is bracketed
+ * by HIP events on the launch stream and its duration is added under the
+ * kernel's name. Query synchronises the stream. Names: "store_kv",
+ * "gather_kv", "paged_attention_decode", "paged_attention_merge",
+ * "paged_attention_prefill", "copy_blocks", "checkpoint_pack",
+ * "checkpoint_unpack", "tables_patch". */
+int ckv_profile_enable(ckv_context* ctx, int enabled);
+int ckv_profile_query(ckv_context* ctx, const char* kernel, double* total_ms,
+                      uint64_t* launches);
+int ckv_profile_reset(ckv_context* ctx);
+
+/* ---- KV pool (metal_kv_cache::make, src/metal/metal_kv_cache.cc:38-82) ----- */
+/* Allocates keys and values, each layers*blocks*block_size*kv_heads*head_dim
+ * elements of dtype. Geometry checks and their order follow the reference:
+ * invalid_layer_count, invalid_block_count, invalid_block_size,
+ * invalid_kv_head_count, invalid_head_dimension, layout_size_overflow,
+ * allocation_failed. Slots (blocks*block_size) must fit in u32. */
+int ckv_pool_create(ckv_context* ctx, size_t layers, size_t blocks, size_t block_size,
+                    size_t kv_heads, size_t head_dim, int dtype, ckv_pool** out);
+/* Same geometry checks, over caller-owned device memory (not freed by the pool). */
+int ckv_pool_wrap(ckv_context* ctx, size_t layers, size_t blocks, size_t block_size,
+                  size_t kv_heads, size_t head_dim, int dtype, void* keys, void* values,
+                  ckv_pool** out);
+int ckv_pool_destroy(ckv_pool* pool);
+int ckv_pool_buffers(const ckv_pool* pool, void** keys, void** values, size_t* bytes_each);
+/* metal_kv_cache::element_offset (src/metal/metal_kv_cache.cc:150-179): the
+ * element index into either tensor, or layer/block/token/head/feature
+ * _out_of_range. */
+int ckv_element_offset(const ckv_pool* pool, size_t layer, size_t block, size_t token_offset,
+                       size_t kv_head, size_t head_feature, size_t* offset);
+
+/* ---- Device-resident metadata ------------------------------------------------ */
+/* Uploads the batch metadata of prepare_paged_batch (src/model_batch.cc:127-204):
+ * the flat block table, per-row table offset/length, positions and slots,
+ * after the host checks of prepared_attention_batch::make
+ * (src/tensor/attention.cc:110-137) and store_kv (src/tensor/tensor_ops.cc:445-453):
+ *   block_table_range_out_of_bounds  a row's [offset, offset+length) leaves the
+ *                                    table, or position/block_size >= length
+ *   cache_block_out_of_range         a table entry >= blocks
+ *   cache_slot_out_of_range          a slot >= blocks*block_size
+ * slots may be NULL when no append follows. The query tiles of
+ * prepared_attention_batch::make (src/tensor/attention.cc:142-167) and the
+ * split-KV decode work list are derived here, once per batch, and reused by
+ * every layer. */
+int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entries,
+                      const uint32_t* offsets, const uint32_t* lengths,
+                      const uint32_t* positions, const uint32_t* slots, size_t rows);
+/* Device-side delta update of the uploaded block table: table[idx[i]] = val[i],
+ * so a block_manager change is mirrored without re-sending the table. Rows'
+ * offsets/lengths are unchanged; every idx must be < n_entries
+ * (block_table_range_out_of_bounds) and every val < blocks
+ * (cache_block_out_of_range). */
+int ckv_tables_patch(ckv_pool* pool, const uint32_t* idx, const uint32_t* val, size_t n);
+
+/* ---- Ops -------------------------------------------------------------------------- */
+/* store_kv (src/tensor/tensor_ops.cc:412-463; kernel src/metal/kernels/attention.metal:3-33):
+ * keys/values are device [rows, kv_heads*head_dim] of the pool dtype; row r is
+ * copied bit-for-bit to slot slots[r] of `layer`. rows must equal the uploaded
+ * row count (cache_slot_count_mismatch); layer < layers
+ * (cache_layer_out_of_range); slots must have been uploaded (no_tables). */
+int ckv_append(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+               size_t rows);
+/* Reads tokens 0..n_tokens-1 of one sequence back through the uploaded table
+ * entries [table_offset, table_offset+table_length) into device
+ * [n_tokens, kv_heads*head_dim] arrays (the inverse of ckv_append). */
+int ckv_gather(ckv_pool* pool, size_t layer, size_t table_offset, size_t table_length,
+               size_t n_tokens, void* out_keys, void* out_values);
+/* paged_attention (src/tensor/attention.cc:188-254) for rows that each attend
+ * to logical positions 0..positions[r] through their table range:
+ * out = softmax(q . k * scale) . v with fp32 accumulation. queries and
+ * output are device [rows, q_heads*head_dim] of the pool dtype.
+ * Decode form: split-KV over fixed token chunks of each (row, kv_head), the
+ * q heads of a GQA group sharing every K/V read, then a merge
+ * (paged_attention_partial_f32 / paged_attention_reduce_f32,
+ * src/metal/kernels/attention.metal:446-615, generalised to every row).
+ * Checks: invalid_head_count, invalid_kv_head_mapping (q_heads % kv_heads),
+ * cache_layer_out_of_range, position_count_mismatch (rows != uploaded rows). */
+int ckv_decode_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                         float scale, void* output, size_t rows);
+/* Prefill form (paged_flash_attention_prefill_f32,
+ * src/metal/kernels/attention.metal:246-444): query tiles of consecutive
+ * positions of one sequence share every K/V tile; QK^T and PV run on MFMA
+ * for 16-bit pools. Same arguments and checks as ckv_decode_attention. */
+int ckv_prefill_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                          float scale, void* output, size_t rows);
+/* Kernel selection of dispatch_paged_attention_f32 / paged_attention
+ * (src/metal/metal_kernels_attention.mm:143-298, src/tensor/attention.cc:290-309):
+ * the prefill form when some query tile has more than one row, else decode. */
+int ckv_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                  float scale, void* output, size_t rows);
+
+/* ---- Pages: copy-on-write and checkpoints ------------------------------------------ */
+/* For every layer, keys and values: page dst[i] := page src[i]. The copy-on-write
+ * step for a shared page (new; the reference never shares pages). Checks:
+ * cache_block_out_of_range; unsupported_aliasing when a dst repeats or is
+ * also a src. */
+int ckv_copy_blocks(ckv_pool* pool, const uint32_t* src, const uint32_t* dst, size_t n);
+/* metal_kv_cache::checkpoint / restore (src/metal/metal_kv_cache.cc:14-35, :225-253):
+ * packed device buffers [layer][token][kv_head][feature] of the pool dtype;
+ * only the first `tokens` tokens are copied (the tail page partially).
+ * blocks must hold at least ceil(tokens/block_size) ids < blocks
+ * (state.invalid_reservation otherwise, as valid_prefix, :205-223). */
+int ckv_checkpoint_pack(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks, size_t tokens,
+                        void* packed_keys, void* packed_values);
+int ckv_checkpoint_unpack(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks,
+                          size_t tokens, const void* packed_keys, const void* packed_values);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

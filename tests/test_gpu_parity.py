@@ -1,0 +1,431 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle on the same
+inputs: append / gather / page copies / checkpoints bit-exact, attention within
+2e-2 abs + 1e-2 rel (the reference's own known-answer tests at their stated
+tolerances). Runs on the MI355X only."""
+import functools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from chibillm_amd import ckv
+from oracle import oracle as orc
+from tests.golden import config1
+from tests.gpu_util import (approx, assert_close, new_context, new_pool, to_dev, to_f32,
+                            to_host)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = new_context()
+    yield c
+    c.sync()
+    c.close()
+
+
+# ---- append ------------------------------------------------------------------------
+
+@pytest.mark.parametrize("code", [orc.F32, orc.BF16, orc.F16])
+def test_store_kv_writes_rows_into_selected_slots(ctx, code):
+    # tests/tensor_ops_test.cc:610-633 (cache L2 B2 bs2 H1 D2, slots {1, 3}, layer 1)
+    pool, keys, values = new_pool(ctx, (2, 2, 2, 1, 2), code, fill=-1.0)
+    pool.upload([0, 1], [0, 0], [2, 2], [0, 0], slots=[1, 3])
+    k = to_dev(orc.from_f32(np.array([[1, 2], [3, 4]]), code), code)
+    v = to_dev(orc.from_f32(np.array([[5, 6], [7, 8]]), code), code)
+    pool.append(1, k, v)
+    ctx.sync()
+    assert to_f32(keys).tolist() == [-1] * 10 + [1, 2, -1, -1, 3, 4]
+    assert to_f32(values).tolist() == [-1] * 10 + [5, 6, -1, -1, 7, 8]
+
+
+def test_store_kv_validation_codes(ctx):
+    # tests/tensor_ops_test.cc:635-691 (the checks that exist at this boundary)
+    pool, _, _ = new_pool(ctx, (2, 2, 2, 1, 2), orc.F32)
+    k = torch.zeros(2, 2, device="cuda")
+    with pytest.raises(ckv.CkvError) as e:
+        pool.append(0, k, k)
+    assert e.value.code == 403  # nothing uploaded yet
+    pool.upload([0, 1], [0, 0], [2, 2], [0, 0], slots=[0, 1])
+    with pytest.raises(ckv.CkvError) as e:
+        pool.append(0, k, k, rows=1)
+    assert e.value.name == "tensor_op.cache_slot_count_mismatch"
+    with pytest.raises(ckv.CkvError) as e:
+        pool.append(2, k, k)
+    assert e.value.name == "tensor_op.cache_layer_out_of_range"
+    with pytest.raises(ckv.CkvError) as e:
+        pool.upload([0, 1], [0, 0], [2, 2], [0, 0], slots=[0, 4])
+    assert e.value.name == "tensor_op.cache_slot_out_of_range"
+
+
+def test_attention_metadata_validation_codes(ctx):
+    # tests/tensor_ops_test.cc:986-1099 (host checks of the table metadata)
+    pool, _, _ = new_pool(ctx, (2, 2, 2, 1, 2), orc.F32)
+    with pytest.raises(ckv.CkvError) as e:  # missing required block
+        pool.upload([0], [0], [1], [2])
+    assert e.value.name == "tensor_op.block_table_range_out_of_bounds"
+    with pytest.raises(ckv.CkvError) as e:  # range outside the flattened table
+        pool.upload([0, 1], [1], [2], [0])
+    assert e.value.name == "tensor_op.block_table_range_out_of_bounds"
+    with pytest.raises(ckv.CkvError) as e:  # physical block out of range
+        pool.upload([2], [0], [1], [0])
+    assert e.value.name == "tensor_op.cache_block_out_of_range"
+    pool.upload([0], [0], [1], [0])
+    q = torch.zeros(1, 2, device="cuda")
+    out = torch.zeros(1, 2, device="cuda")
+    with pytest.raises(ckv.CkvError) as e:
+        pool.decode(0, q, 0, 1.0, out)
+    assert e.value.name == "tensor_op.invalid_head_count"
+    with pytest.raises(ckv.CkvError) as e:
+        pool.decode(2, q, 1, 1.0, out)
+    assert e.value.name == "tensor_op.cache_layer_out_of_range"
+    with pytest.raises(ckv.CkvError) as e:
+        pool.decode(0, q, 1, 1.0, out, rows=2)
+    assert e.value.name == "tensor_op.position_count_mismatch"
+    gqa, _, _ = new_pool(ctx, (1, 1, 1, 2, 2), orc.F32)
+    gqa.upload([0], [0], [1], [0])
+    with pytest.raises(ckv.CkvError) as e:
+        gqa.decode(0, torch.zeros(1, 6, device="cuda"), 3, 1.0, torch.zeros(1, 6, device="cuda"))
+    assert e.value.name == "tensor_op.invalid_kv_head_mapping"
+
+
+def test_pool_geometry_codes_and_offsets(ctx):
+    # tests/metal_kv_cache_test.cc:64-101
+    for geom, name in [((0, 3, 4, 2, 8), "kv_cache.invalid_layer_count"),
+                       ((2, 0, 4, 2, 8), "kv_cache.invalid_block_count"),
+                       ((2, 3, 0, 2, 8), "kv_cache.invalid_block_size"),
+                       ((2, 3, 4, 0, 8), "kv_cache.invalid_kv_head_count"),
+                       ((2, 3, 4, 2, 0), "kv_cache.invalid_head_dimension"),
+                       ((2**64 - 1, 3, 4, 2, 8), "kv_cache.layout_size_overflow")]:
+        with pytest.raises(ckv.CkvError) as e:
+            ckv.Pool(ctx, *geom, ckv.F32)
+        assert e.value.name == name
+    pool = ckv.Pool(ctx, 2, 3, 4, 2, 8, ckv.F32)
+    k, v, n = pool.buffers()
+    assert n == 384 * 4 and k and v and k != v
+    offsets = [pool.element_offset(*c) for c in [(0, 0, 0, 0, 0), (0, 0, 0, 0, 1), (0, 0, 0, 1, 0),
+                                                 (0, 0, 1, 0, 0), (0, 1, 0, 0, 0), (1, 0, 0, 0, 0),
+                                                 (1, 2, 3, 1, 7)]]
+    assert offsets == [0, 1, 8, 16, 64, 192, 383]
+    for coords, name in [((2, 0, 0, 0, 0), "layer"), ((0, 3, 0, 0, 0), "block"),
+                         ((0, 0, 4, 0, 0), "token_offset"), ((0, 0, 0, 2, 0), "kv_head"),
+                         ((0, 0, 0, 0, 8), "head_feature")]:
+        with pytest.raises(ckv.CkvError) as e:
+            pool.element_offset(*coords)
+        assert e.value.name == f"kv_cache.{name}_out_of_range"
+    pool.close()
+
+
+# ---- attention known answers ------------------------------------------------------------
+
+def run_attention(ctx, geom, keys, values, q, positions, table, offsets, lengths, q_heads,
+                  layer=0, code=orc.F32):
+    pool, kd, vd = new_pool(ctx, geom, code)
+    kd.copy_(to_dev(keys, code))
+    vd.copy_(to_dev(values, code))
+    pool.upload(table, offsets, lengths, positions)
+    qd = to_dev(q, code)
+    scale = float(np.float32(1.0 / math.sqrt(geom[4])))
+    outs = {}
+    for name in ("decode", "prefill", "attention"):
+        out = torch.full_like(qd, float("nan"))
+        getattr(pool, name)(layer, qd, q_heads, scale, out)
+        outs[name] = to_f32(out)
+    ctx.sync()
+    pool.close()
+    return outs
+
+
+def test_decode_closed_form_through_page_table(ctx):
+    # tests/tensor_ops_test.cc:693-735
+    keys = np.array([1, 1, 0, 0, 1, 0, 0, 1] + [0] * 8, np.float32)
+    values = np.array([30, 3, 0, 0, 10, 1, 20, 2] + [0] * 8, np.float32)
+    outs = run_attention(ctx, (2, 2, 2, 1, 2), keys, values, np.array([[1, 0, 0, 1]], np.float32),
+                         [2], [1, 0], [0], [2], 2)
+    e = math.exp(1 / math.sqrt(2))
+    d = 2 * e + 1
+    expected = [(40 * e + 20) / d, (4 * e + 2) / d, (10 + 50 * e) / d, (1 + 5 * e) / d]
+    for name, out in outs.items():
+        assert approx(out[0], expected, 1e-5), name
+
+
+def test_prefill_tiles_known_answer(ctx):
+    # tests/tensor_ops_test.cc:737-822
+    geom = (1, 2, 2, 1, 2)
+    keys = np.array([0.25, 0.75, -0.5, 1.0, 1.0, 0.0, 0.5, -0.25], np.float32)
+    values = np.array([30, 3, 40, 4, 10, 1, 20, 2], np.float32)
+    q = np.array([1.0, 0.5, -0.5, 1.0, 0.25, 1.0, 1.0, -0.25, -0.5, 0.75, 0.5, 0.5, 1.0, -1.0,
+                  -0.25, 0.75], np.float32).reshape(4, 4)
+    args = ([0, 1, 2, 3], [1, 0], [0] * 4, [2] * 4)
+    expected = orc.Attention(geom, keys, values, orc.F32, q, orc.F32, *args, 2, 0,
+                             1 / math.sqrt(2)).reference()
+    for name, out in run_attention(ctx, geom, keys, values, q, *args, 2).items():
+        assert approx(out, expected, 1e-5), name
+
+
+def test_prefill_merges_key_tiles_across_cached_prefix(ctx):
+    # tests/tensor_ops_test.cc:824-870
+    values = np.array([[t, 2 * t] for t in range(32)], np.float32).ravel()
+    outs = run_attention(ctx, (1, 2, 16, 1, 2), np.zeros(64, np.float32), values,
+                         np.ones((8, 2), np.float32), list(range(16, 24)), [0, 1], [0] * 8,
+                         [2] * 8, 1)
+    for name, out in outs.items():
+        for r in range(8):
+            assert approx(out[r], [(16 + r) / 2, 16 + r], 1e-5), name
+
+
+def test_split_decode_combines_chunks(ctx):
+    # tests/tensor_ops_test.cc:941-984: mean of (t, 2t) over 0..128 = (64, 128)
+    values = np.array([[t, 2 * t] for t in range(144)], np.float32).ravel()
+    outs = run_attention(ctx, (1, 9, 16, 1, 2), np.zeros(288, np.float32), values,
+                         np.ones((1, 2), np.float32), [128], list(range(9)), [0], [9], 1)
+    for name, out in outs.items():
+        assert approx(out[0], [64, 128], 1e-5), name
+
+
+@pytest.mark.parametrize("dim", [129, 192, 256, 257])
+def test_wide_heads_ragged_batch(ctx, dim):
+    # tests/tensor_ops_test.cc:872-939 (rel 3e-5 against a double reference)
+    rows, heads, kv_heads = 5, 4, 2
+    geom = (2, 6, 16, kv_heads, dim)
+    n = 2 * 6 * 16 * kv_heads * dim
+    i = np.arange(n, dtype=np.float32)
+    keys = np.sin(i * np.float32(0.17)).astype(np.float32)
+    values = np.cos(i * np.float32(0.11)).astype(np.float32)
+    q = (20 * np.sin(np.arange(rows * heads * dim, dtype=np.float32) * np.float32(0.13))
+         ).astype(np.float32).reshape(rows, -1)
+    args = ([17, 18, 7, 32, 9], [4, 1, 5, 3, 0, 2], [0, 0, 3, 3, 0], [3] * rows)
+    expected = orc.Attention(geom, keys, values, orc.F32, q, orc.F32, *args, heads, 1,
+                             1 / math.sqrt(dim)).reference()
+    for name, out in run_attention(ctx, geom, keys, values, q, *args, heads, layer=1).items():
+        assert approx(out, expected, 3e-5, 1.0), name
+
+
+# ---- token-by-token fp16 appends + one decode step ----------------------
+
+def test_config1_fp16_appends_bit_exact_and_decode_within_tolerance(ctx):
+    steps, q, tables = config1.generate()
+    L, B, bs, H, D = config1.GEOMETRY
+    pool, keys, values = new_pool(ctx, config1.GEOMETRY, orc.F16)
+    for active, t, ks, vs, step_tables in steps:
+        flat, offsets, lengths, positions, slots = config1.step_metadata(step_tables, active, t)
+        pool.upload(flat, offsets, lengths, positions, slots)
+        pool.append(0, to_dev(ks, orc.F16), to_dev(vs, orc.F16))
+    kc, vc = config1.oracle_cache(steps)
+    assert np.array_equal(to_host(keys, orc.F16), kc)
+    assert np.array_equal(to_host(values, orc.F16), vc)
+
+    flat, offsets, lengths, positions = config1.decode_metadata(tables)
+    pool.upload(flat, offsets, lengths, positions)
+    F = H * D
+    for s, n in enumerate(config1.LENGTHS):  # gather = the rows drawn for the sequence
+        gk = torch.empty(n, F, dtype=torch.float16, device="cuda")
+        gv = torch.empty_like(gk)
+        pool.gather(0, int(offsets[s]), lengths[s], n, gk, gv)
+        drawn_k = np.stack([st[2][st[0].index(s)] for st in steps if s in st[0]])
+        drawn_v = np.stack([st[3][st[0].index(s)] for st in steps if s in st[0]])
+        assert np.array_equal(to_host(gk, orc.F16), drawn_k)
+        assert np.array_equal(to_host(gv, orc.F16), drawn_v)
+
+    online, reference = config1.oracle_attention(kc, vc, q, tables)
+    qd = to_dev(q, orc.F16)
+    for name in ("decode", "attention", "prefill"):
+        out = torch.empty_like(qd)
+        getattr(pool, name)(0, qd, config1.Q_HEADS, config1.SCALE, out)
+        assert_close(to_f32(out), online, what=f"{name} vs oracle online")
+        assert_close(to_f32(out), reference, what=f"{name} vs double reference")
+    ctx.sync()
+
+
+# ---- single-layer bf16 decode over a permuted 65,536-page pool -----------
+
+@functools.lru_cache(maxsize=2)
+def config2_inputs(seed=0, batch=32):
+    rng = orc.Mt64(seed)
+    lengths = [rng.uniform_int(256, 4096) for _ in range(batch)]
+    perm = rng.permutation(65536)
+    tables, at = [], 0
+    for n in lengths:
+        pages = -(-n // 16)
+        tables.append(perm[at:at + pages])
+        at += pages
+    F = 8 * 128
+    ks = [rng.normal(n * F, orc.BF16).reshape(n, F) for n in lengths]
+    vs = [rng.normal(n * F, orc.BF16).reshape(n, F) for n in lengths]
+    q = rng.normal(batch * 16 * 128, orc.BF16).reshape(batch, 16 * 128)
+    return lengths, tables, ks, vs, q
+
+
+def compact_oracle(geom_h_d, lengths, tables, ks, vs, q, q_heads, positions=None,
+                   code=orc.BF16, threads=8):
+    """Oracle attention over a compact host pool holding only the pages in use
+    (page ids renumbered in table order; the attention result depends only on
+    the values reached through the tables)."""
+    H, D = geom_h_d
+    F = H * D
+    n_pages = sum(len(t) for t in tables)
+    kc = np.zeros(n_pages * 16 * F, np.uint16)
+    vc = np.zeros_like(kc)
+    flat, offsets, at = [], [], 0
+    for n, t, k, v in zip(lengths, tables, ks, vs):
+        compact = np.arange(at, at + len(t), dtype=np.uint32)
+        offsets.append(at)
+        flat.append(compact)
+        slots = [int(compact[p // 16]) * 16 + p % 16 for p in range(n)]
+        orc.store_kv(kc, vc, k, v, slots, 0, n_pages * 16)
+        at += len(t)
+    flat = np.concatenate(flat)
+    positions = [n - 1 for n in lengths] if positions is None else positions
+    att = orc.Attention((1, n_pages, 16, H, D), kc, vc, code, q, code, positions, flat, offsets,
+                        [len(t) for t in tables], q_heads, 0, float(np.float32(1 / math.sqrt(D))))
+    return att.online_threads(threads)
+
+
+def fill_by_append(pool, lengths, tables, ks, vs, layer=0, code=orc.BF16):
+    """Writes every sequence's rows through ckv_append, one sequence per call."""
+    for n, t, k, v in zip(lengths, tables, ks, vs):
+        slots = [orc.slot(t, p, 16) for p in range(n)]
+        pool.upload(t, [0] * n, [len(t)] * n, list(range(n)), slots)
+        pool.append(layer, to_dev(k, code), to_dev(v, code))
+
+
+@pytest.mark.parametrize("chunk", [None, "32", "4096"])
+def test_config2_bf16_decode_over_permuted_pages(ctx, chunk, monkeypatch):
+    if chunk:
+        monkeypatch.setenv("CKV_DECODE_CHUNK", chunk)
+    lengths, tables, ks, vs, q = config2_inputs()
+    pool, _, _ = new_pool(ctx, (1, 65536, 16, 8, 128), orc.BF16)
+    fill_by_append(pool, lengths, tables, ks, vs)
+    # gather of every sequence returns its rows bit for bit
+    for n, t, k, v in zip(lengths[:4], tables, ks, vs):
+        pool.upload(t, [0], [len(t)], [n - 1])
+        gk = torch.empty(n, 1024, dtype=torch.bfloat16, device="cuda")
+        gv = torch.empty_like(gk)
+        pool.gather(0, 0, len(t), n, gk, gv)
+        assert np.array_equal(to_host(gk, orc.BF16), k)
+        assert np.array_equal(to_host(gv, orc.BF16), v)
+    flat = np.concatenate(tables)
+    offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
+    pool.upload(flat, offsets, [len(t) for t in tables], [n - 1 for n in lengths])
+    out = torch.empty(32, 16 * 128, dtype=torch.bfloat16, device="cuda")
+    pool.decode(0, to_dev(q, orc.BF16), 16, float(np.float32(1 / math.sqrt(128))), out)
+    expected = compact_oracle((8, 128), lengths, tables, ks, vs, q, 16)
+    assert_close(to_f32(out), expected, what=f"config 2 decode (chunk {chunk})")
+    ctx.sync()
+    pool.close()
+
+
+def test_edge_positions_and_gqa_groups(ctx):
+    """Single-token rows, rows ending exactly on page and chunk boundaries, and
+    every GQA group size the fast kernel specialises."""
+    rng = orc.Mt64(9)
+    lengths = [1, 16, 17, 32, 33, 64, 257, 1024, 1025]
+    B = sum(-(-n // 16) for n in lengths) + 3
+    perm = rng.permutation(B)
+    tables, at = [], 0
+    for n in lengths:
+        tables.append(perm[at:at + -(-n // 16)])
+        at += len(tables[-1])
+    for group in (1, 2, 4, 8):
+        H = 16 // group if group < 8 else 2
+        q_heads = H * group
+        F = H * 128
+        ks = [rng.normal(n * F, orc.BF16).reshape(n, F) for n in lengths]
+        vs = [rng.normal(n * F, orc.BF16).reshape(n, F) for n in lengths]
+        q = rng.normal(len(lengths) * q_heads * 128, orc.BF16).reshape(len(lengths), -1)
+        pool, _, _ = new_pool(ctx, (1, B, 16, H, 128), orc.BF16)
+        fill_by_append(pool, lengths, tables, ks, vs)
+        flat = np.concatenate(tables)
+        offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
+        pool.upload(flat, offsets, [len(t) for t in tables], [n - 1 for n in lengths])
+        out = torch.empty(len(lengths), q_heads * 128, dtype=torch.bfloat16, device="cuda")
+        pool.decode(0, to_dev(q, orc.BF16), q_heads, float(np.float32(1 / math.sqrt(128))), out)
+        expected = compact_oracle((H, 128), lengths, tables, ks, vs, q, q_heads)
+        assert_close(to_f32(out), expected, what=f"group {group}")
+        pool.close()
+    ctx.sync()
+
+
+# ---- pages: copies, checkpoints, table patches ----------------------------------------------
+
+def test_copy_blocks_bit_exact_and_aliasing_rejected(ctx):
+    geom = (3, 10, 16, 2, 8)
+    pool, keys, values = new_pool(ctx, geom, orc.BF16)
+    rng = np.random.default_rng(7)
+    kc = rng.integers(0, 2**16, keys.numel(), dtype=np.uint16)
+    vc = rng.integers(0, 2**16, keys.numel(), dtype=np.uint16)
+    keys.copy_(to_dev(kc, orc.BF16))
+    values.copy_(to_dev(vc, orc.BF16))
+    pool.copy_blocks([1, 4, 9], [7, 2, 0])
+    orc.copy_blocks(kc, vc, geom, [1, 4, 9], [7, 2, 0])
+    assert np.array_equal(to_host(keys, orc.BF16), kc)
+    assert np.array_equal(to_host(values, orc.BF16), vc)
+    for src, dst, name in [([1, 2], [3, 3], "tensor_op.unsupported_aliasing"),
+                           ([1, 2], [2, 5], "tensor_op.unsupported_aliasing"),
+                           ([10], [3], "tensor_op.cache_block_out_of_range")]:
+        with pytest.raises(ckv.CkvError) as e:
+            pool.copy_blocks(src, dst)
+        assert e.value.name == name
+    pool.close()
+
+
+def test_checkpoint_pack_and_restore_known_answer(ctx):
+    # tests/metal_kv_cache_test.cc:103-142
+    geom = (2, 3, 4, 2, 8)
+    pool, keys, values = new_pool(ctx, geom, orc.F32)
+    k = np.arange(1, 385, dtype=np.float32)
+    v = np.arange(1001, 1385, dtype=np.float32)
+    keys.copy_(torch.from_numpy(k))
+    values.copy_(torch.from_numpy(v))
+    pk = torch.zeros(2 * 5 * 16, device="cuda")
+    pv = torch.zeros_like(pk)
+    pool.checkpoint_pack([2, 0], 5, pk, pv)
+    keys.zero_()
+    values.zero_()
+    pool.checkpoint_unpack([0, 1], 5, pk, pv)
+    rk, rv = to_f32(keys), to_f32(values)
+    for layer in range(2):
+        for token in range(8):
+            for f in range(16):
+                dest = layer * 192 + token * 16 + f
+                orig = layer * 192 + [2, 0][token // 4] * 64 + (token % 4) * 16 + f
+                assert rk[dest] == (k[orig] if token < 5 else 0)
+                assert rv[dest] == (v[orig] if token < 5 else 0)
+    for blocks, tokens in (([3], 1), ([2, 0], 9), ([2], 5), ([2, 0], 0)):
+        with pytest.raises(ckv.CkvError) as e:
+            pool.checkpoint_pack(blocks, tokens, pk, pv)
+        assert e.value.name == "state.invalid_reservation"
+    pool.close()
+
+
+def test_table_patch_equals_reupload(ctx):
+    lengths, tables, ks, vs, q = config2_inputs(seed=3, batch=6)
+    pool, _, _ = new_pool(ctx, (1, 65536, 16, 8, 128), orc.BF16)
+    fill_by_append(pool, lengths, tables, ks, vs)
+    flat = np.concatenate(tables)
+    offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
+    positions = [n - 1 for n in lengths]
+    # upload a wrong table, then patch it into the right one on the device
+    wrong = flat.copy()
+    idx = np.arange(0, flat.size, 3)
+    wrong[idx] = (wrong[idx] + 1) % 65536
+    pool.upload(wrong, offsets, [len(t) for t in tables], positions)
+    pool.patch(idx, flat[idx])
+    qd = to_dev(q, orc.BF16)
+    scale = float(np.float32(1 / math.sqrt(128)))
+    patched = torch.empty(6, 2048, dtype=torch.bfloat16, device="cuda")
+    pool.decode(0, qd, 16, scale, patched)
+    pool.upload(flat, offsets, [len(t) for t in tables], positions)
+    fresh = torch.empty_like(patched)
+    pool.decode(0, qd, 16, scale, fresh)
+    ctx.sync()
+    assert torch.equal(patched, fresh)
+    with pytest.raises(ckv.CkvError) as e:
+        pool.patch([flat.size], [0])
+    assert e.value.name == "tensor_op.block_table_range_out_of_bounds"
+    with pytest.raises(ckv.CkvError) as e:
+        pool.patch([0], [65536])
+    assert e.value.name == "tensor_op.cache_block_out_of_range"
+    pool.close()

@@ -187,8 +187,10 @@ int run_decode(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads
     ckv_context* ctx = pool->ctx;
     const pool_view view = view_of(pool);
     float* partials = nullptr;
-    const bool needs_merge = std::any_of(pool->row_count.begin(), pool->row_count.end(),
-                                         [](uint32_t c) { return c > 1; });
+    const bool fast = decode_fast_applies(view, (uint32_t)q_heads, queries, output);
+    const bool needs_merge = !fast
+        && std::any_of(pool->row_count.begin(), pool->row_count.end(),
+                       [](uint32_t c) { return c > 1; });
     if (needs_merge) {
         size_t capacity_floats = pool->d_partials_bytes / sizeof(float);
         const size_t needed = (pool->items.size() / 2) * q_heads
@@ -202,7 +204,7 @@ int run_decode(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads
     }
     int status = run_kernel(ctx, "paged_attention_decode", [&] {
         return launch_decode(ctx->stream, view, pool->meta, (uint32_t)layer, queries,
-                             (uint32_t)q_heads, scale, output, partials);
+                             (uint32_t)q_heads, scale, output, partials, ctx->cu_count);
     });
     if (status || !needs_merge)
         return status;
@@ -691,7 +693,15 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
         r += n;
     }
 
-    // pack: table | offsets | lengths | positions | slots | items | row_first | row_count | tiles
+    // rows by decreasing position: the decode kernel dispatches the longest work first
+    std::vector<uint32_t> order(rows);
+    for (size_t r = 0; r < rows; ++r)
+        order[r] = (uint32_t)r;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](uint32_t a, uint32_t b) { return positions[a] > positions[b]; });
+
+    // pack: table | offsets | lengths | positions | slots | items | row_first | row_count |
+    // tiles | order
     const size_t s_table = 0;
     const size_t s_offsets = s_table + round4(n_entries);
     const size_t s_lengths = s_offsets + round4(rows);
@@ -701,7 +711,8 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     const size_t s_first = s_items + round4(items.size());
     const size_t s_count = s_first + round4(rows);
     const size_t s_tiles = s_count + round4(rows);
-    const size_t words = s_tiles + round4(tiles.size());
+    const size_t s_order = s_tiles + round4(tiles.size());
+    const size_t words = s_order + round4(rows);
     void* host = nullptr;
     int status = stage(ctx, std::max<size_t>(words, 4) * sizeof(uint32_t), &host);
     if (status)
@@ -722,6 +733,7 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     put(s_first, row_first.data(), rows);
     put(s_count, row_count.data(), rows);
     put(s_tiles, tiles.data(), tiles.size());
+    put(s_order, order.data(), rows);
     status = ensure_device(ctx, &pool->d_meta, &pool->d_meta_words, std::max<size_t>(words, 4),
                            "metadata buffer");
     if (status)
@@ -740,6 +752,7 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     m.row_first = pool->d_meta + s_first;
     m.row_count = pool->d_meta + s_count;
     m.tiles = pool->d_meta + s_tiles;
+    m.order = pool->d_meta + s_order;
     m.n_entries = (uint32_t)n_entries;
     m.rows = (uint32_t)rows;
     m.n_items = (uint32_t)(items.size() / 2);
@@ -759,6 +772,7 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     pool->row_first = std::move(row_first);
     pool->row_count = std::move(row_count);
     pool->tiles = std::move(tiles);
+    pool->order = std::move(order);
     pool->chunk = chunk;
     pool->shared_tile = shared;
     pool->uploaded = true;

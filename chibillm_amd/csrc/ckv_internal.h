@@ -39,6 +39,7 @@ struct meta_view {
     const uint32_t* row_first; // first work item of each row
     const uint32_t* row_count; // work items (chunks) of each row
     const uint32_t* tiles;     // prefill query tiles: (first row, row count) pairs
+    const uint32_t* order;     // rows by decreasing position (longest work first)
     uint32_t n_entries;
     uint32_t rows;
     uint32_t n_items;
@@ -95,7 +96,7 @@ struct ckv_pool {
     bool uploaded = false;
     bool has_slots = false;
     std::vector<uint32_t> table, offsets, lengths, positions, slots;
-    std::vector<uint32_t> items, row_first, row_count, tiles;
+    std::vector<uint32_t> items, row_first, row_count, tiles, order;
     uint32_t chunk = 0;
     bool shared_tile = false;
 
@@ -126,10 +127,13 @@ hipError_t launch_checkpoint(hipStream_t s, const pool_view& p, uint32_t layers,
 hipError_t launch_table_patch(hipStream_t s, uint32_t* table, const uint32_t* pairs, uint32_t n);
 
 // ---- launchers (kernels_decode.hip) ------------------------------------------
-// Returns hipErrorInvalidValue when no kernel fits the geometry.
+// Returns hipErrorInvalidValue when no kernel fits the geometry. The fast
+// path (decode_fast_applies) merges in the workgroup and needs no partials;
+// the generic path writes partials for rows with several chunks.
 hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                          const void* q, uint32_t q_heads, float scale, void* out,
-                         float* partials);
+                         float* partials, int cu_count);
+bool decode_fast_applies(const pool_view& p, uint32_t q_heads, const void* q, const void* out);
 hipError_t launch_merge(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t q_heads,
                         void* out, const float* partials);
 bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads);

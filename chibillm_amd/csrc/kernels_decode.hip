@@ -20,6 +20,7 @@
 #include "ckv_internal.h"
 
 #include <cmath>
+#include <cstdlib>
 
 namespace ckv {
 namespace {
@@ -113,33 +114,41 @@ __host__ __device__ constexpr uint32_t record_floats(uint32_t head_dim)
     return head_dim + 4;
 }
 
+// Fast path, one workgroup per (row, kv_head), W waves. Wave w walks pages
+// w, w+W, w+2W, ... of the row (16-token pages, one scalar table read per
+// page); the next page's K/V loads are issued before the current page is
+// processed. Lane 16*group + part reads features 8*part..8*part+7 of token
+// 4j + group of the page (j = 0..3): four 1 KiB wave loads per page for K and
+// four for V. The wave's four row-group softmax states are merged with
+// shuffles, the W wave states through LDS, and the workgroup writes the
+// normalised output of the group's q heads.
 template <int G, bool F16>
-__global__ __launch_bounds__(64) void decode_d128_kernel(pool_view p, meta_view m, uint32_t layer,
-                                                         const uint16_t* __restrict__ q,
-                                                         uint32_t q_heads, float scale_log2,
-                                                         uint16_t* __restrict__ out,
-                                                         float* __restrict__ partials)
+__global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg_kernel(pool_view p, meta_view m, uint32_t layer,
+                                                        const uint16_t* __restrict__ q,
+                                                        uint32_t q_heads, float scale_log2,
+                                                        uint16_t* __restrict__ out)
 {
     using ops = half2_ops<F16>;
     constexpr uint32_t D = 128;
+    constexpr uint32_t BS = 16;
+    extern __shared__ float lds[];
+    const uint32_t W = blockDim.x >> 6;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t group = lane >> 4;
+    const uint32_t part = lane & 15;
     const uint32_t H = p.kv_heads;
+    const uint32_t row = m.order[blockIdx.x / H];
     const uint32_t kv_head = blockIdx.x % H;
-    const uint32_t item = blockIdx.x / H;
-    const uint32_t row = m.items[2 * item];
-    const uint32_t chunk_index = m.items[2 * item + 1];
     const uint32_t position = m.positions[row];
-    const uint32_t table_base = m.offsets[row];
-    const uint32_t begin = chunk_index * m.chunk;
-    const uint32_t end = min(position + 1, begin + m.chunk);
-    const uint32_t lane = threadIdx.x;
-    const uint32_t group = lane >> 4; // token of a 4-token step
-    const uint32_t part = lane & 15;  // features 8*part .. 8*part + 7
-    const uint32_t bs = p.block_size;
-    const uint64_t F = p.features;
-    const uint16_t* kbase = static_cast<const uint16_t*>(p.keys) + (uint64_t)layer * p.layer_elems
-        + kv_head * D + part * 8;
-    const uint16_t* vbase = static_cast<const uint16_t*>(p.values)
-        + (uint64_t)layer * p.layer_elems + kv_head * D + part * 8;
+    const uint32_t n_pages = position / BS + 1;
+    const uint32_t last_in_page = position % BS;
+    const uint32_t row_bytes = p.features * 2u;
+    const uint64_t page_bytes = (uint64_t)BS * row_bytes;
+    const char* kl = static_cast<const char*>(p.keys) + (uint64_t)layer * p.layer_elems * 2u;
+    const char* vl = static_cast<const char*>(p.values) + (uint64_t)layer * p.layer_elems * 2u;
+    const uint32_t* tbl = m.table + m.offsets[row];
+    const uint32_t head_off = kv_head * (D * 2u) + part * 16u;
 
     uint4 qv[G];
 #pragma unroll
@@ -157,70 +166,89 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(pool_view p, meta_view 
             acc[g][f] = 0.0f;
     }
 
-    for (uint32_t t0 = begin; t0 < end; t0 += 16) {
-        uint4 kr[4], vr[4];
+    // rows past the row's last token re-read that token (in bounds, written)
+    auto load_page = [&](uint32_t pg, uint4* k, uint4* v) {
+        const uint64_t base = (uint64_t)tbl[pg] * page_bytes;
+        const char* kb = kl + base;
+        const char* vb = vl + base;
+        const uint32_t last = pg == n_pages - 1 ? last_in_page : BS - 1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t r = min(4u * j + group, last);
+            const uint32_t off = r * row_bytes + head_off;
+            k[j] = *reinterpret_cast<const uint4*>(kb + off);
+            v[j] = *reinterpret_cast<const uint4*>(vb + off);
+        }
+    };
+
+    auto process = [&](const uint4* k, const uint4* v, uint32_t pg) {
+        const uint32_t valid = pg == n_pages - 1 ? last_in_page + 1 : BS;
         bool ok[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t step = t0 + 4 * j;         // wave-uniform
-            const uint32_t last = min(step, end - 1); // a token this row owns
-            const uint32_t page = m.table[table_base + last / bs];
-            const uint32_t token = step + group;
-            ok[j] = token < end;
-            // invalid lanes re-read the row's own token `last`: in bounds and written
-            const uint32_t in_page = ok[j] ? token % bs : last % bs;
-            const uint64_t slot = (uint64_t)page * bs + in_page;
-            kr[j] = *reinterpret_cast<const uint4*>(kbase + slot * F);
-            vr[j] = *reinterpret_cast<const uint4*>(vbase + slot * F);
-        }
-
-        float vf[4][8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            vf[j][0] = ops::lo(vr[j].x);
-            vf[j][1] = ops::hi(vr[j].x);
-            vf[j][2] = ops::lo(vr[j].y);
-            vf[j][3] = ops::hi(vr[j].y);
-            vf[j][4] = ops::lo(vr[j].z);
-            vf[j][5] = ops::hi(vr[j].z);
-            vf[j][6] = ops::lo(vr[j].w);
-            vf[j][7] = ops::hi(vr[j].w);
-        }
-
+        for (int j = 0; j < 4; ++j)
+            ok[j] = 4u * j + group < valid;
+        float pw[G][4];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float s[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                float d = ops::dot2(qv[g].x, kr[j].x, 0.0f);
-                d = ops::dot2(qv[g].y, kr[j].y, d);
-                d = ops::dot2(qv[g].z, kr[j].z, d);
-                d = ops::dot2(qv[g].w, kr[j].w, d);
-                s[j] = ok[j] ? row16_sum(d) * scale_log2 : -INFINITY;
+                float d = ops::dot2(qv[g].x, k[j].x, 0.0f);
+                d = ops::dot2(qv[g].y, k[j].y, d);
+                d = ops::dot2(qv[g].z, k[j].z, d);
+                d = ops::dot2(qv[g].w, k[j].w, d);
+                const float r = row16_sum(d) * scale_log2;
+                s[j] = ok[j] ? r : -INFINITY;
             }
-            const float tile = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-            const float nm = fmaxf(mx[g], tile);
-            const bool none = nm == -INFINITY; // this row group has no token yet
-            const float alpha = none ? 1.0f : fast_exp2(mx[g] - nm);
-            float pw[4];
+            const float nm = fmaxf(mx[g], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+            // rescale only when some lane's running max grew (alpha is 1 elsewhere)
+            if (__builtin_amdgcn_ballot_w64(nm > mx[g])) {
+                const float alpha = nm == -INFINITY ? 1.0f : fast_exp2(mx[g] - nm);
+                den[g] *= alpha;
+#pragma unroll
+                for (int f = 0; f < 8; ++f)
+                    acc[g][f] *= alpha;
+                mx[g] = nm;
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                pw[j] = ok[j] ? fast_exp2(s[j] - nm) : 0.0f;
-            den[g] = den[g] * alpha + ((pw[0] + pw[1]) + (pw[2] + pw[3]));
-#pragma unroll
-            for (int f = 0; f < 8; ++f) {
-                float a = acc[g][f] * alpha;
-                a += pw[0] * vf[0][f];
-                a += pw[1] * vf[1][f];
-                a += pw[2] * vf[2][f];
-                a += pw[3] * vf[3][f];
-                acc[g][f] = a;
-            }
-            mx[g] = nm;
+                pw[g][j] = ok[j] ? fast_exp2(s[j] - mx[g]) : 0.0f;
+            den[g] += (pw[g][0] + pw[g][1]) + (pw[g][2] + pw[g][3]);
         }
+        // token by token: widen the V row once, accumulate it into every q head
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float vf[8] = { ops::lo(v[j].x), ops::hi(v[j].x), ops::lo(v[j].y),
+                                  ops::hi(v[j].y), ops::lo(v[j].z), ops::hi(v[j].z),
+                                  ops::lo(v[j].w), ops::hi(v[j].w) };
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int f = 0; f < 8; ++f)
+                    acc[g][f] += pw[g][j] * vf[f];
+        }
+    };
+
+    uint4 ka[4], va[4], kb[4], vb[4];
+    uint32_t pg = wave;
+    if (pg < n_pages)
+        load_page(pg, ka, va);
+    while (pg < n_pages) {
+        uint32_t next = pg + W;
+        if (next < n_pages)
+            load_page(next, kb, vb);
+        process(ka, va, pg);
+        pg = next;
+        if (pg >= n_pages)
+            break;
+        next = pg + W;
+        if (next < n_pages)
+            load_page(next, ka, va);
+        process(kb, vb, pg);
+        pg = next;
     }
 
-    // merge the four row-group states (lanes l, l^16, l^32, l^48)
+    // merge the wave's four row-group states (lanes l, l^16, l^32, l^48)
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         float M = fmaxf(mx[g], __shfl_xor(mx[g], 16));
@@ -239,31 +267,38 @@ __global__ __launch_bounds__(64) void decode_d128_kernel(pool_view p, meta_view 
         den[g] = d;
         mx[g] = M;
     }
-
-    if (group != 0)
-        return;
-    const bool single = m.row_count[row] == 1;
+    // LDS: acc [W][G][D], then (max, denominator) [W][G][2]
+    float* lds_acc = lds;
+    float* lds_ml = lds + W * G * D;
+    if (group == 0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const uint32_t qh = kv_head * G + g;
-        if (single) {
-            const float inv = 1.0f / den[g];
-            uint4 o;
-            o.x = ops::pack(acc[g][0] * inv, acc[g][1] * inv);
-            o.y = ops::pack(acc[g][2] * inv, acc[g][3] * inv);
-            o.z = ops::pack(acc[g][4] * inv, acc[g][5] * inv);
-            o.w = ops::pack(acc[g][6] * inv, acc[g][7] * inv);
-            *reinterpret_cast<uint4*>(out + ((uint64_t)row * q_heads + qh) * D + part * 8) = o;
-        } else {
-            float* rec = partials + ((uint64_t)item * q_heads + qh) * record_floats(D);
-            float4* dst = reinterpret_cast<float4*>(rec + 4 + part * 8);
+        for (int g = 0; g < G; ++g) {
+            float4* dst = reinterpret_cast<float4*>(lds_acc + (wave * G + g) * D + part * 8);
             dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
             dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
             if (part == 0) {
-                rec[0] = mx[g];
-                rec[1] = den[g];
+                lds_ml[(wave * G + g) * 2] = mx[g];
+                lds_ml[(wave * G + g) * 2 + 1] = den[g];
             }
         }
+    }
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t < G * D; t += blockDim.x) {
+        const uint32_t g = t / D;
+        const uint32_t f = t % D;
+        float M = -INFINITY;
+        for (uint32_t w = 0; w < W; ++w)
+            M = fmaxf(M, lds_ml[(w * G + g) * 2]);
+        float d = 0.0f, a = 0.0f;
+        for (uint32_t w = 0; w < W; ++w) {
+            const float mw = lds_ml[(w * G + g) * 2];
+            const float weight = mw == -INFINITY ? 0.0f : fast_exp2(mw - M);
+            d += lds_ml[(w * G + g) * 2 + 1] * weight;
+            a += lds_acc[(w * G + g) * D + f] * weight;
+        }
+        const float o = a / d;
+        out[((uint64_t)row * q_heads + kv_head * G + g) * D + f] =
+            static_cast<uint16_t>(F16 ? f16_bits(o) : bf16_bits(o));
     }
 }
 
@@ -420,20 +455,36 @@ bool aligned16(const void* ptr)
     return reinterpret_cast<uintptr_t>(ptr) % 16 == 0;
 }
 
+// Waves per workgroup of the fast path. Shorter workgroups balance better
+// (the longest rows are dispatched first and short ones fill the gaps), so
+// the largest count the kernel's occupancy allows is used: 16 for GQA groups
+// of at most 2 (a full compute unit), else 8. CKV_DECODE_WAVES overrides.
+uint32_t fast_waves(uint32_t group)
+{
+    const uint32_t limit = group <= 2 ? 16u : 8u;
+    if (const char* forced = std::getenv("CKV_DECODE_WAVES")) {
+        const long v = std::strtol(forced, nullptr, 10);
+        if (v >= 1 && v <= (long)limit)
+            return (uint32_t)v;
+    }
+    return limit;
+}
+
 template <int G>
 hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
-                       const void* q, uint32_t q_heads, float scale_log2, void* out,
-                       float* partials, bool f16)
+                       const void* q, uint32_t q_heads, float scale_log2, void* out, bool f16)
 {
-    const dim3 grid(m.n_items * p.kv_heads), block(64);
+    const uint32_t units = m.rows * p.kv_heads;
+    const uint32_t waves = fast_waves(G);
+    const dim3 grid(units), block(64 * waves);
+    const size_t lds = (size_t)waves * G * (128 + 2) * sizeof(float);
     const auto qq = static_cast<const uint16_t*>(q);
     const auto oo = static_cast<uint16_t*>(out);
     if (f16)
-        decode_d128_kernel<G, true><<<grid, block, 0, s>>>(p, m, layer, qq, q_heads, scale_log2, oo,
-                                                           partials);
+        decode_wg_kernel<G, true><<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo);
     else
-        decode_d128_kernel<G, false><<<grid, block, 0, s>>>(p, m, layer, qq, q_heads, scale_log2,
-                                                            oo, partials);
+        decode_wg_kernel<G, false><<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2,
+                                                            oo);
     return hipGetLastError();
 }
 
@@ -442,28 +493,33 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
 bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads)
 {
     const uint32_t G = q_heads / p.kv_heads;
-    return p.dtype != CKV_F32 && p.head_dim == 128 && p.block_size % 4 == 0
+    return p.dtype != CKV_F32 && p.head_dim == 128 && p.block_size == 16
         && (G == 1 || G == 2 || G == 4 || G == 8) && aligned16(p.keys) && aligned16(p.values);
+}
+
+bool decode_fast_applies(const pool_view& p, uint32_t q_heads, const void* q, const void* out)
+{
+    return decode_uses_fast_path(p, q_heads) && aligned16(q) && aligned16(out);
 }
 
 hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                          const void* q, uint32_t q_heads, float scale, void* out,
-                         float* partials)
+                         float* partials, int cu_count)
 {
-    if (!m.n_items)
+    if (!m.rows)
         return hipSuccess;
     const float scale_log2 = scale * log2e;
-    if (decode_uses_fast_path(p, q_heads) && aligned16(q) && aligned16(out)) {
+    if (decode_fast_applies(p, q_heads, q, out)) {
         const bool f16 = p.dtype == CKV_F16;
         switch (q_heads / p.kv_heads) {
         case 1:
-            return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, partials, f16);
+            return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16);
         case 2:
-            return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, partials, f16);
+            return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16);
         case 4:
-            return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, partials, f16);
+            return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16);
         default:
-            return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, partials, f16);
+            return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16);
         }
     }
     if (p.head_dim > 64u * generic_max_features_per_lane)

@@ -84,6 +84,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-fuse", action="store_true",
+                    help="append and decode as two launches instead of ckv_append_decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -155,8 +157,12 @@ def main():
                  for s, p in enumerate(positions)]
         pool.upload(flat, offsets, owned, positions, slots)
         for layer in range(LAYERS):
-            pool.append(layer, k_new[layer], v_new[layer])
-            pool.decode(layer, q[layer], Q_HEADS, scale, out[layer])
+            if args.no_fuse:
+                pool.append(layer, k_new[layer], v_new[layer])
+                pool.decode(layer, q[layer], Q_HEADS, scale, out[layer])
+            else:
+                pool.append_decode(layer, k_new[layer], v_new[layer], q[layer], Q_HEADS, scale,
+                                   out[layer])
         attended = positions + 1
         lengths[:] = attended
         return int(attended.sum()), int(sum(math.ceil(a / BLOCK) for a in attended))
@@ -177,7 +183,8 @@ def main():
         pages_read += pages
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    decode_ms, decode_n = ctx.profile_query("paged_attention_decode")
+    dominant = "paged_attention_decode" if args.no_fuse else "append_decode"
+    decode_ms, decode_n = ctx.profile_query(dominant)
     merge_ms, merge_n = ctx.profile_query("paged_attention_merge")
     store_ms, store_n = ctx.profile_query("store_kv")
     ctx.profile(False)
@@ -187,10 +194,11 @@ def main():
     kv_bytes = LAYERS * tokens_attended * kv_row_bytes
     value = kv_bytes / elapsed / 1e9
     ms_per_step = elapsed * 1e3 / args.steps
-    # algorithmic bytes of one decode launch (one layer): KV of every attended
-    # token + Q + O + the table entries read
+    # algorithmic bytes of one launch (one layer): KV of every attended token,
+    # Q and O, the table entries read, and (fused) the new K/V rows written
+    appended = 0 if args.no_fuse else BATCH * kv_row_bytes
     per_launch = (tokens_attended * kv_row_bytes + pages_read * 4
-                  + args.steps * 2 * BATCH * Q_HEADS * HEAD_DIM * 2) / args.steps
+                  + args.steps * (2 * BATCH * Q_HEADS * HEAD_DIM * 2 + appended)) / args.steps
     decode_avg_s = decode_ms / decode_n / 1e3
     achieved = per_launch / decode_avg_s / 1e9
     result = {
@@ -209,6 +217,8 @@ def main():
         "config": {
             "workload": "config3: 28-layer decode step (append 1 token/seq/layer + paged GQA "
                         "decode attention), batch 128, context U[1024,8192] growing 1/step",
+            "launches": "two per layer (ckv_append, ckv_decode_attention)" if args.no_fuse
+                        else "one per layer (ckv_append_decode)",
             "layers": LAYERS, "batch": BATCH, "kv_heads": KV_HEADS, "q_heads": Q_HEADS,
             "head_dim": HEAD_DIM, "block_size": BLOCK, "pool_pages": n_pool,
             "kv_pool_gb": round(kv_gb, 2),
@@ -217,12 +227,12 @@ def main():
         "tokens_per_s": round(BATCH * args.steps / elapsed, 1),
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "kernels_ms_per_step": {
-            "paged_attention_decode": round(decode_ms / args.steps, 4),
+            dominant: round(decode_ms / args.steps, 4),
             "paged_attention_merge": round(merge_ms / args.steps, 4),
             "store_kv": round(store_ms / args.steps, 4),
         },
         "roofline": {
-            "kernel": "paged_attention_decode",
+            "kernel": dominant,
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,

@@ -51,6 +51,7 @@ _SIGNATURES = [
     ("ckv_append", _i, [_vp, _sz, _vp, _vp, _sz]),
     ("ckv_gather", _i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp]),
     ("ckv_decode_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
+    ("ckv_append_decode", _i, [_vp, _sz, _vp, _vp, _vp, _sz, C.c_float, _vp, _sz]),
     ("ckv_prefill_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
     ("ckv_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
     ("ckv_copy_blocks", _i, [_vp, _u32p, _u32p, _sz]),
@@ -237,6 +238,13 @@ class Pool:
 
     def decode(self, layer, queries, q_heads, scale, output, rows=None) -> None:
         self._attend(load().ckv_decode_attention, layer, queries, q_heads, scale, output, rows)
+
+    def append_decode(self, layer, keys, values, queries, q_heads, scale, output,
+                      rows=None) -> None:
+        rows = queries.shape[0] if rows is None else rows
+        self.ctx.check(load().ckv_append_decode(self.handle, layer, _ptr(keys), _ptr(values),
+                                                _ptr(queries), q_heads, scale, _ptr(output),
+                                                rows))
 
     def prefill(self, layer, queries, q_heads, scale, output, rows=None) -> None:
         self._attend(load().ckv_prefill_attention, layer, queries, q_heads, scale, output, rows)

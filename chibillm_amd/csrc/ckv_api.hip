@@ -693,6 +693,18 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
         r += n;
     }
 
+    // append + decode can run as one launch when every row appends the token at
+    // its own position and no two rows attend through the same table range
+    bool fusable = slots != nullptr;
+    if (fusable) {
+        std::unordered_set<uint32_t> ranges;
+        for (size_t r = 0; r < rows && fusable; ++r) {
+            const uint64_t own = (uint64_t)block_table[offsets[r] + positions[r] / bs] * bs
+                + positions[r] % bs;
+            fusable = own == slots[r] && ranges.insert(offsets[r]).second;
+        }
+    }
+
     // rows by decreasing position: the decode kernel dispatches the longest work first
     std::vector<uint32_t> order(rows);
     for (size_t r = 0; r < rows; ++r)
@@ -775,6 +787,7 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     pool->order = std::move(order);
     pool->chunk = chunk;
     pool->shared_tile = shared;
+    pool->fusable = fusable;
     pool->uploaded = true;
     return CKV_OK;
 }
@@ -857,6 +870,36 @@ int ckv_decode_attention(ckv_pool* pool, size_t layer, const void* queries, size
         return CKV_E_INVALID_ARGUMENT;
     const int status = check_attention(pool, layer, queries, q_heads, output, rows);
     if (status || !rows)
+        return status;
+    return run_decode(pool, layer, queries, q_heads, scale, output);
+}
+
+int ckv_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+                      const void* queries, size_t q_heads, float scale, void* output, size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if (rows && (!keys || !values))
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "keys and values are required");
+    if (!pool->uploaded || !pool->has_slots)
+        return set_error(ctx, CKV_E_NO_TABLES, "append before slots were uploaded");
+    if (rows != pool->slots.size())
+        return set_error(ctx, CKV_E_CACHE_SLOT_COUNT_MISMATCH, "rows != uploaded slots");
+    int status = check_attention(pool, layer, queries, q_heads, output, rows);
+    if (status || !rows)
+        return status;
+    const pool_view view = view_of(pool);
+    const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (pool->fusable && decode_fast_applies(view, (uint32_t)q_heads, queries, output)
+        && aligned(keys) && aligned(values)) {
+        return run_kernel(ctx, "append_decode", [&] {
+            return launch_append_decode(ctx->stream, view, pool->meta, (uint32_t)layer, keys,
+                                        values, queries, (uint32_t)q_heads, scale, output);
+        });
+    }
+    status = ckv_append(pool, layer, keys, values, rows);
+    if (status)
         return status;
     return run_decode(pool, layer, queries, q_heads, scale, output);
 }

@@ -99,6 +99,7 @@ struct ckv_pool {
     std::vector<uint32_t> items, row_first, row_count, tiles, order;
     uint32_t chunk = 0;
     bool shared_tile = false;
+    bool fusable = false; // slots are the rows' own positions, one row per table range
 
     // device copies
     uint32_t* d_meta = nullptr;
@@ -134,6 +135,12 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
                          const void* q, uint32_t q_heads, float scale, void* out,
                          float* partials, int cu_count);
 bool decode_fast_applies(const pool_view& p, uint32_t q_heads, const void* q, const void* out);
+// store_kv + fast decode in one launch; the caller has checked
+// decode_fast_applies, 16-byte aligned inputs, and that every row's slot is
+// its position's slot with no two rows on one table range.
+hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_view& m,
+                                uint32_t layer, const void* k_in, const void* v_in, const void* q,
+                                uint32_t q_heads, float scale, void* out);
 hipError_t launch_merge(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t q_heads,
                         void* out, const float* partials);
 bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads);

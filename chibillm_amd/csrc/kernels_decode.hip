@@ -114,7 +114,10 @@ __host__ __device__ constexpr uint32_t record_floats(uint32_t head_dim)
     return head_dim + 4;
 }
 
-// Fast path, one workgroup per (row, kv_head), W waves. Wave w walks pages
+// Fast path, one workgroup per (row, kv_head), W waves. With FUSED, the row's
+// new token (position = the row's last) is taken from k_in/v_in rows instead
+// of the cache and stored into its slot by the wave that owns the last page:
+// the append of store_kv and the attention in one pass. Wave w walks pages
 // w, w+W, w+2W, ... of the row (16-token pages, one scalar table read per
 // page); the next page's K/V loads are issued before the current page is
 // processed. Lane 16*group + part reads features 8*part..8*part+7 of token
@@ -122,11 +125,11 @@ __host__ __device__ constexpr uint32_t record_floats(uint32_t head_dim)
 // four for V. The wave's four row-group softmax states are merged with
 // shuffles, the W wave states through LDS, and the workgroup writes the
 // normalised output of the group's q heads.
-template <int G, bool F16>
-__global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg_kernel(pool_view p, meta_view m, uint32_t layer,
-                                                        const uint16_t* __restrict__ q,
-                                                        uint32_t q_heads, float scale_log2,
-                                                        uint16_t* __restrict__ out)
+template <int G, bool F16, bool FUSED>
+__global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg_kernel(
+    pool_view p, meta_view m, uint32_t layer, const uint16_t* __restrict__ q, uint32_t q_heads,
+    float scale_log2, uint16_t* __restrict__ out, const char* __restrict__ k_in,
+    const char* __restrict__ v_in)
 {
     using ops = half2_ops<F16>;
     constexpr uint32_t D = 128;
@@ -167,22 +170,37 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
     }
 
     // rows past the row's last token re-read that token (in bounds, written)
+    const uint64_t in_row = (uint64_t)row * row_bytes + head_off;
     auto load_page = [&](uint32_t pg, uint4* k, uint4* v) {
         const uint64_t base = (uint64_t)tbl[pg] * page_bytes;
         const char* kb = kl + base;
         const char* vb = vl + base;
-        const uint32_t last = pg == n_pages - 1 ? last_in_page : BS - 1;
+        const bool last_page = pg == n_pages - 1;
+        const uint32_t last = last_page ? last_in_page : BS - 1;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t r = min(4u * j + group, last);
             const uint32_t off = r * row_bytes + head_off;
-            k[j] = *reinterpret_cast<const uint4*>(kb + off);
-            v[j] = *reinterpret_cast<const uint4*>(vb + off);
+            const bool fresh = FUSED && last_page && r == last_in_page;
+            k[j] = *reinterpret_cast<const uint4*>(fresh ? k_in + in_row : kb + off);
+            v[j] = *reinterpret_cast<const uint4*>(fresh ? v_in + in_row : vb + off);
         }
     };
 
     auto process = [&](const uint4* k, const uint4* v, uint32_t pg) {
         const uint32_t valid = pg == n_pages - 1 ? last_in_page + 1 : BS;
+        if (FUSED && pg == n_pages - 1) {
+            // append: the lanes holding the new token write it into its slot
+            const uint64_t base = (uint64_t)tbl[pg] * page_bytes;
+            const uint32_t off = last_in_page * row_bytes + head_off;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (4u * j + group == last_in_page) {
+                    *reinterpret_cast<uint4*>(const_cast<char*>(kl) + base + off) = k[j];
+                    *reinterpret_cast<uint4*>(const_cast<char*>(vl) + base + off) = v[j];
+                }
+            }
+        }
         bool ok[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -472,7 +490,8 @@ uint32_t fast_waves(uint32_t group)
 
 template <int G>
 hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
-                       const void* q, uint32_t q_heads, float scale_log2, void* out, bool f16)
+                       const void* q, uint32_t q_heads, float scale_log2, void* out, bool f16,
+                       const void* k_in, const void* v_in)
 {
     const uint32_t units = m.rows * p.kv_heads;
     const uint32_t waves = fast_waves(G);
@@ -480,11 +499,23 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
     const size_t lds = (size_t)waves * G * (128 + 2) * sizeof(float);
     const auto qq = static_cast<const uint16_t*>(q);
     const auto oo = static_cast<uint16_t*>(out);
-    if (f16)
-        decode_wg_kernel<G, true><<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo);
-    else
-        decode_wg_kernel<G, false><<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2,
-                                                            oo);
+    const auto ki = static_cast<const char*>(k_in);
+    const auto vi = static_cast<const char*>(v_in);
+    if (k_in) {
+        if (f16)
+            decode_wg_kernel<G, true, true>
+                <<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo, ki, vi);
+        else
+            decode_wg_kernel<G, false, true>
+                <<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo, ki, vi);
+    } else {
+        if (f16)
+            decode_wg_kernel<G, true, false>
+                <<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo, ki, vi);
+        else
+            decode_wg_kernel<G, false, false>
+                <<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo, ki, vi);
+    }
     return hipGetLastError();
 }
 
@@ -513,13 +544,17 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
         const bool f16 = p.dtype == CKV_F16;
         switch (q_heads / p.kv_heads) {
         case 1:
-            return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16);
+            return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
+                                  nullptr);
         case 2:
-            return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16);
+            return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
+                                  nullptr);
         case 4:
-            return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16);
+            return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
+                                  nullptr);
         default:
-            return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16);
+            return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
+                                  nullptr);
         }
     }
     if (p.head_dim > 64u * generic_max_features_per_lane)
@@ -540,6 +575,26 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
         break;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_view& m,
+                                uint32_t layer, const void* k_in, const void* v_in, const void* q,
+                                uint32_t q_heads, float scale, void* out)
+{
+    if (!m.rows)
+        return hipSuccess;
+    const float scale_log2 = scale * log2e;
+    const bool f16 = p.dtype == CKV_F16;
+    switch (q_heads / p.kv_heads) {
+    case 1:
+        return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in);
+    case 2:
+        return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in);
+    case 4:
+        return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in);
+    default:
+        return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in);
+    }
 }
 
 hipError_t launch_merge(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t q_heads,

@@ -119,7 +119,7 @@ int ckv_sync(ckv_context* ctx);
  * (src/metal/metal_context.mm:94-169): when enabled, every launch is bracketed
  * by HIP events on the launch stream and its duration is added under the
  * kernel's name. Query synchronises the stream. Names: "store_kv",
- * "gather_kv", "paged_attention_decode", "paged_attention_merge",
+ * "gather_kv", "paged_attention_decode", "paged_attention_merge", "append_decode",
  * "paged_attention_prefill", "copy_blocks", "checkpoint_pack",
  * "checkpoint_unpack", "tables_patch". */
 int ckv_profile_enable(ckv_context* ctx, int enabled);
@@ -195,6 +195,16 @@ int ckv_gather(ckv_pool* pool, size_t layer, size_t table_offset, size_t table_l
  * cache_layer_out_of_range, position_count_mismatch (rows != uploaded rows). */
 int ckv_decode_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
                          float scale, void* output, size_t rows);
+/* store_kv followed by the decode form, in one launch where possible: the
+ * `run_attention` pair of src/qwen/qwen_layer.cc:32-50 (store_kv, then
+ * paged_attention). Each workgroup reads its row's new token from keys/values,
+ * writes it into the row's slot and attends to it in the same pass, which
+ * applies when every uploaded slot is the slot of its row's position and no
+ * two rows share a table range (a decode batch); otherwise ckv_append then
+ * ckv_decode_attention run. Results are those of the two calls in sequence.
+ * Checks: those of ckv_append, then those of ckv_decode_attention. */
+int ckv_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+                      const void* queries, size_t q_heads, float scale, void* output, size_t rows);
 /* Prefill form (paged_flash_attention_prefill_f32,
  * src/metal/kernels/attention.metal:246-444): query tiles of consecutive
  * positions of one sequence share every K/V tile; QK^T and PV run on MFMA

@@ -429,3 +429,65 @@ def test_table_patch_equals_reupload(ctx):
         pool.patch([0], [65536])
     assert e.value.name == "tensor_op.cache_block_out_of_range"
     pool.close()
+
+
+# ---- fused append + decode ------------------------------------------------------------------
+
+def test_append_decode_equals_append_then_decode(ctx):
+    lengths, tables, ks, vs, q = config2_inputs(seed=5, batch=12)
+    geom = (2, 65536, 16, 8, 128)
+    pools = []
+    for _ in range(2):
+        pool, keys, values = new_pool(ctx, geom, orc.BF16)
+        # every token but the last is already cached
+        fill_by_append(pool, [n - 1 for n in lengths], tables,
+                       [k[:-1] for k in ks], [v[:-1] for v in vs], layer=1)
+        pools.append((pool, keys, values))
+    flat = np.concatenate(tables)
+    offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
+    positions = [n - 1 for n in lengths]
+    slots = [orc.slot(t, p, 16) for t, p in zip(tables, positions)]
+    k_new = to_dev(np.stack([k[-1] for k in ks]), orc.BF16)
+    v_new = to_dev(np.stack([v[-1] for v in vs]), orc.BF16)
+    qd = to_dev(q, orc.BF16)
+    scale = float(np.float32(1 / math.sqrt(128)))
+    outs = []
+    for i, (pool, _, _) in enumerate(pools):
+        pool.upload(flat, offsets, [len(t) for t in tables], positions, slots)
+        out = torch.empty(len(lengths), 16 * 128, dtype=torch.bfloat16, device="cuda")
+        if i == 0:
+            pool.append_decode(1, k_new, v_new, qd, 16, scale, out)
+        else:
+            pool.append(1, k_new, v_new)
+            pool.decode(1, qd, 16, scale, out)
+        outs.append(out)
+    ctx.sync()
+    assert torch.equal(pools[0][1], pools[1][1]) and torch.equal(pools[0][2], pools[1][2])
+    assert torch.equal(outs[0], outs[1])
+    expected = compact_oracle((8, 128), lengths, tables, ks, vs, q, 16)
+    assert_close(to_f32(outs[0]), expected, what="append_decode vs oracle")
+    for pool, _, _ in pools:
+        pool.close()
+
+
+def test_append_decode_falls_back_when_rows_share_a_sequence(ctx):
+    # two rows of one sequence (positions 40 and 41) cannot be fused: the
+    # second row attends to the token the first row appends
+    rng = orc.Mt64(13)
+    geom = (1, 8, 16, 8, 128)
+    F = 1024
+    table = [5, 2, 7]
+    k = rng.normal(42 * F, orc.BF16).reshape(42, F)
+    v = rng.normal(42 * F, orc.BF16).reshape(42, F)
+    q = rng.normal(2 * 2048, orc.BF16).reshape(2, 2048)
+    pool, _, _ = new_pool(ctx, geom, orc.BF16)
+    fill_by_append(pool, [40], [np.array(table, np.uint32)], [k[:40]], [v[:40]])
+    pool.upload(table, [0, 0], [3, 3], [40, 41], [orc.slot(table, 40, 16), orc.slot(table, 41, 16)])
+    out = torch.empty(2, 2048, dtype=torch.bfloat16, device="cuda")
+    pool.append_decode(0, to_dev(k[40:], orc.BF16), to_dev(v[40:], orc.BF16),
+                       to_dev(q, orc.BF16), 16, float(np.float32(1 / math.sqrt(128))), out)
+    expected = compact_oracle((8, 128), [41, 42], [np.array(table, np.uint32)] * 2, [k[:41], k],
+                              [v[:41], v], q, 16)
+    assert_close(to_f32(out), expected, what="append_decode fallback")
+    ctx.sync()
+    pool.close()

@@ -25,12 +25,26 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+# HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE /
+# WRITE_SIZE passes scaled by a known-size copy (written by those passes)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "append_decode_config3_traffic.json")
 LAYERS, BATCH, KV_HEADS, Q_HEADS, HEAD_DIM, BLOCK = 28, 128, 8, 16, 128, 16
 CTX_LO, CTX_HI = 1024, 8192
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def traffic_bytes(kernel):
+    """Measured HBM bytes per launch of `kernel` if a counter summary exists."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            data = json.load(fh)
+    except OSError:
+        return None
+    entry = data.get("kernels", {}).get(kernel)
+    return None if entry is None else int(entry["hbm_bytes_per_launch"])
 
 
 def cpu_baseline(threads):
@@ -84,6 +98,9 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run one ckv_copy_blocks of 1024 pages (64 MiB read + 64 MiB "
+                         "written), the known-size copy the HBM counters are scaled by")
     ap.add_argument("--no-fuse", action="store_true",
                     help="append and decode as two launches instead of ckv_append_decode")
     args = ap.parse_args()
@@ -128,6 +145,12 @@ def main():
     log(f"pool {n_pool} pages x {LAYERS} layers = {kv_gb:.1f} GB K+V; "
         f"context tokens {int(lengths.sum())}")
     ctx = ckv.Context(0, stream=torch.cuda.current_stream())
+    if args.calibrate_copy:
+        calib = ckv.Pool(ctx, 1, 2048, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16)
+        calib.copy_blocks(np.arange(1024), np.arange(1024, 2048))
+        ctx.sync()
+        calib.close()
+        log("calibration copy: 1024 pages x 32 KiB, keys + values = 64 MiB read, 64 MiB written")
     elems = LAYERS * n_pool * BLOCK * F
     keys = torch.empty(elems, dtype=torch.bfloat16, device=device)
     values = torch.empty(elems, dtype=torch.bfloat16, device=device)
@@ -238,7 +261,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_bytes(dominant),
             "avg_launch_us": round(decode_avg_s * 1e6, 2),
             "algorithmic_bytes_per_launch": int(per_launch),
         },

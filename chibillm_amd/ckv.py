@@ -38,6 +38,10 @@ _SIGNATURES = [
     ("ckv_context_stream", _vp, [_vp]),
     ("ckv_context_own_stream", _vp, [_vp]),
     ("ckv_sync", _i, [_vp]),
+    ("ckv_device_alloc", _i, [_vp, _sz, C.POINTER(_vp)]),
+    ("ckv_device_free", _i, [_vp, _vp]),
+    ("ckv_copy_to_device", _i, [_vp, _vp, _vp, _sz]),
+    ("ckv_copy_to_host", _i, [_vp, _vp, _vp, _sz]),
     ("ckv_profile_enable", _i, [_vp, _i]),
     ("ckv_profile_query", _i, [_vp, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
     ("ckv_profile_reset", _i, [_vp]),

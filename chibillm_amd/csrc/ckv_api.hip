@@ -513,6 +513,58 @@ int ckv_sync(ckv_context* ctx)
     return CKV_OK;
 }
 
+int ckv_device_alloc(ckv_context* ctx, size_t bytes, void** out)
+{
+    if (!ctx || !out)
+        return CKV_E_INVALID_ARGUMENT;
+    *out = nullptr;
+    (void)hipSetDevice(ctx->device);
+    const hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return hip_error(ctx, e, "device buffer allocation");
+    }
+    return CKV_OK;
+}
+
+int ckv_device_free(ckv_context* ctx, void* ptr)
+{
+    if (!ctx)
+        return CKV_E_INVALID_ARGUMENT;
+    if (!ptr)
+        return CKV_OK;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess)
+        e = hipFree(ptr);
+    if (e != hipSuccess)
+        return hip_error(ctx, e, "device buffer free");
+    return CKV_OK;
+}
+
+int ckv_copy_to_device(ckv_context* ctx, void* device_dst, const void* host_src, size_t bytes)
+{
+    if (!ctx || (bytes && (!device_dst || !host_src)))
+        return CKV_E_INVALID_ARGUMENT;
+    hipError_t e = hipMemcpyAsync(device_dst, host_src, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess)
+        return hip_error(ctx, e, "copy to device");
+    return CKV_OK;
+}
+
+int ckv_copy_to_host(ckv_context* ctx, void* host_dst, const void* device_src, size_t bytes)
+{
+    if (!ctx || (bytes && (!host_dst || !device_src)))
+        return CKV_E_INVALID_ARGUMENT;
+    hipError_t e = hipMemcpyAsync(host_dst, device_src, bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess)
+        return hip_error(ctx, e, "copy to host");
+    return CKV_OK;
+}
+
 int ckv_profile_enable(ckv_context* ctx, int enabled)
 {
     if (!ctx)

@@ -1,0 +1,116 @@
+// The KV-path ops of the tensor layer (src/tensor/tensor_ops.h:160-178,
+// src/tensor/attention.h:6-78) over non-owning device tensor views, with the
+// reference's validation order (all ranks, then dtypes, then shapes, then
+// bounds; src/tensor/validation.h:15-28) and error codes. Batch metadata is
+// uploaded once per step (upload_attention_metadata) and used by every layer.
+#pragma once
+
+#include <cstdint>
+#include <span>
+#include <vector>
+
+#include "hip_kv_cache.h"
+
+namespace chibillm {
+
+// src/tensor/types.h:90-95, plus f16
+enum class dtype : std::uint8_t {
+    f32,
+    bf16,
+    i32,
+    u32,
+    f16,
+};
+
+// A device array with a shape; does not own its memory.
+struct device_tensor {
+    void* data = nullptr;
+    dtype type = dtype::f32;
+    std::vector<std::size_t> dims;
+
+    std::size_t rank() const noexcept { return dims.size(); }
+    std::size_t element_count() const noexcept
+    {
+        std::size_t n = 1;
+        for (std::size_t d : dims)
+            n *= d;
+        return n;
+    }
+};
+
+enum class tensor_op_errc : std::uint8_t {
+    tensor_creation_failed,
+    allocation_failed,
+    empty_tokens,
+    empty_logits_indices,
+    invalid_hidden_states,
+    logits_index_out_of_range,
+    token_id_overflow,
+    invalid_rank,
+    unsupported_dtype,
+    input_shape_mismatch,
+    inner_dimension_mismatch,
+    output_shape_mismatch,
+    token_out_of_range,
+    invalid_epsilon,
+    position_count_mismatch,
+    invalid_head_count,
+    invalid_head_dimension,
+    invalid_rope_theta,
+    cache_slot_count_mismatch,
+    cache_feature_count_mismatch,
+    cache_layer_out_of_range,
+    cache_slot_out_of_range,
+    block_table_metadata_count_mismatch,
+    block_table_range_out_of_bounds,
+    cache_block_out_of_range,
+    cache_head_dimension_mismatch,
+    invalid_kv_head_mapping,
+    backend_failure,
+    unsupported_aliasing,
+};
+
+[[nodiscard]] inline std::string_view
+error_name(tensor_op_errc code) noexcept
+{
+    // the ckv status of code c is c + 100 and carries the same name
+    const char* name = ckv_error_name(static_cast<int>(code) + 100);
+    return std::string_view(name).starts_with("tensor_op.") ? name : "tensor_op.unknown_error";
+}
+
+using tensor_op_error = error<tensor_op_errc>;
+
+// The five arrays of attention_metadata (src/tensor/attention.h:6-12).
+struct attention_metadata {
+    std::span<const std::uint32_t> positions;
+    std::span<const std::uint32_t> slots; // may be empty when no append follows
+    std::span<const std::uint32_t> block_table;
+    std::span<const std::uint32_t> block_table_offsets;
+    std::span<const std::uint32_t> block_table_lengths;
+};
+
+// Validates on the host and uploads (src/tensor/attention.cc:8-29, :110-137).
+result<void, tensor_op_error> upload_attention_metadata(hip_kv_cache& cache,
+                                                        attention_metadata metadata);
+
+// keys/values: [rows, kv_heads * head_dim] of the cache dtype (src/tensor/tensor_ops.cc:412-463).
+result<void, tensor_op_error> store_kv(hip_kv_cache& cache, const device_tensor& keys,
+                                       const device_tensor& values, std::size_t layer);
+
+// queries/output: [rows, q_heads * head_dim] of the cache dtype; scale
+// 1/sqrt(head_dim) (src/tensor/attention.cc:188-254). Selection as the
+// reference: query tiles (prefill form) when a run of rows shares a tile.
+result<void, tensor_op_error> paged_attention(hip_kv_cache& cache, const device_tensor& queries,
+                                              std::size_t layer, std::size_t query_head_count,
+                                              device_tensor& output);
+
+// store_kv then paged_attention of decode rows in one pass where possible
+// (ckv_append_decode): the pair run_attention issues per layer
+// (src/qwen/qwen_layer.cc:32-50).
+result<void, tensor_op_error> store_kv_and_attend(hip_kv_cache& cache, const device_tensor& keys,
+                                                  const device_tensor& values,
+                                                  const device_tensor& queries, std::size_t layer,
+                                                  std::size_t query_head_count,
+                                                  device_tensor& output);
+
+} // namespace chibillm

@@ -115,6 +115,15 @@ void* ckv_context_own_stream(const ckv_context* ctx);
 /* Waits for all work enqueued on the context's stream. */
 int ckv_sync(ckv_context* ctx);
 
+/* Device buffers for callers without their own HIP binding (the role of
+ * metal_context::make_shared_buffer, src/metal/metal_context.h:87-120, but
+ * device memory: the host reaches it only through the copies below).
+ * The copies are synchronous with respect to the context stream. */
+int ckv_device_alloc(ckv_context* ctx, size_t bytes, void** out);
+int ckv_device_free(ckv_context* ctx, void* ptr);
+int ckv_copy_to_device(ckv_context* ctx, void* device_dst, const void* host_src, size_t bytes);
+int ckv_copy_to_host(ckv_context* ctx, void* host_dst, const void* device_src, size_t bytes);
+
 /* Per-kernel GPU timing, the role of CHIBILLM_PROFILE
  * (src/metal/metal_context.mm:94-169): when enabled, every launch is bracketed
  * by HIP events on the launch stream and its duration is added under the

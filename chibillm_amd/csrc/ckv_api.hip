@@ -965,7 +965,7 @@ int ckv_prefill_attention(ckv_pool* pool, size_t layer, const void* queries, siz
     if (status || !rows)
         return status;
     const pool_view view = view_of(pool);
-    if (!prefill_supported(view, (uint32_t)q_heads))
+    if (!prefill_supported(view, (uint32_t)q_heads, queries, output))
         return run_decode(pool, layer, queries, q_heads, scale, output);
     ckv_context* ctx = pool->ctx;
     return run_kernel(ctx, "paged_attention_prefill", [&] {

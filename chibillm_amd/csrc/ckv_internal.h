@@ -47,8 +47,9 @@ struct meta_view {
     uint32_t n_tiles;
 };
 
-// Largest query tile of the prefill kernel, in rows (positions).
-constexpr uint32_t prefill_tile_rows = 64;
+// Largest query tile, in rows (positions): the prefill kernel covers a tile
+// with G workgroups of 256/G rows for GQA group size G.
+constexpr uint32_t prefill_tile_rows = 256;
 
 struct pending_timing {
     const char* name;
@@ -148,7 +149,9 @@ bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads);
 uint32_t partial_record_floats(uint32_t head_dim);
 
 // ---- launchers (kernels_prefill.hip) ------------------------------------------
-bool prefill_supported(const pool_view& p, uint32_t q_heads);
+// MFMA prefill: 16-bit K/V, head_dim 128, 16-token pages, GQA group 1/2/4/8,
+// 16-byte aligned pools, queries and output.
+bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, const void* out);
 hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                           const void* q, uint32_t q_heads, float scale, void* out);
 

@@ -1,0 +1,156 @@
+"""Chunked-prefill attention on the matrix cores (ckv_prefill_attention /
+ckv_attention with query tiles) against the CPU oracle: causal attention of
+each chunk row over its sequence's prefix + chunk through the block table,
+within 2e-2 abs + 1e-2 rel (bf16/fp16 storage, fp32 accumulation).
+
+The shared-prefix case follows config 4's shape at a reduced batch: sequences
+share the prefix's full pages, each takes a copy-on-write copy of a partial
+tail page, appends its chunk and attends over prefix + chunk."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from tests.gpu_util import assert_close, new_context, new_pool, to_dev, to_f32, to_host
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = new_context()
+    yield c
+    c.sync()
+    c.close()
+
+
+def scale():
+    return float(np.float32(1 / math.sqrt(D)))
+
+
+def pages_for(tokens):
+    return -(-tokens // 16)
+
+
+@pytest.mark.parametrize("prefix", [2000, 2008])
+def test_shared_prefix_chunks_with_copy_on_write_tail(ctx, prefix):
+    print(f"shared prefix {prefix}", flush=True)
+    H, Hq, S, C = 8, 16, 3, 300
+    F = H * D
+    rng = orc.Mt64(40 + prefix)
+    prefix_pages = pages_for(prefix)
+    partial = prefix % 16 != 0
+    full = prefix // 16
+    own = pages_for(prefix + C) - full  # each sequence's private pages (tail copy first)
+    blocks = prefix_pages + S * own + 5
+    geom = (1, blocks, 16, H, D)
+    pool, kd, vd = new_pool(ctx, geom, orc.BF16)
+    slot_count = blocks * 16
+    kc = np.zeros(slot_count * F, np.uint16)
+    vc = np.zeros_like(kc)
+
+    # the prefix, written once through the append path
+    prefix_table = np.arange(prefix_pages, dtype=np.uint32)
+    pk = rng.normal(prefix * F, orc.BF16).reshape(prefix, F)
+    pv = rng.normal(prefix * F, orc.BF16).reshape(prefix, F)
+    slots = [orc.slot(prefix_table, p, 16) for p in range(prefix)]
+    pool.upload(prefix_table, [0] * prefix, [prefix_pages] * prefix, list(range(prefix)), slots)
+    pool.append(0, to_dev(pk, orc.BF16), to_dev(pv, orc.BF16))
+    orc.store_kv(kc, vc, pk, pv, slots, 0, slot_count)
+
+    # per-sequence tables: shared full pages, then private pages
+    tables = []
+    for s in range(S):
+        mine = prefix_pages + s * own + np.arange(own, dtype=np.uint32)
+        tables.append(np.concatenate([prefix_table[:full], mine]).astype(np.uint32))
+    if partial:  # copy-on-write of the shared tail page into each sequence's first own page
+        src = [int(prefix_table[full])] * S
+        dst = [int(t[full]) for t in tables]
+        pool.copy_blocks(src, dst)
+        orc.copy_blocks(kc, vc, geom, src, dst)
+
+    # each sequence appends its chunk, then attends
+    positions, offsets, lengths, slots, ks, vs = [], [], [], [], [], []
+    flat = np.concatenate(tables)
+    at = 0
+    for t in tables:
+        positions += list(range(prefix, prefix + C))
+        offsets += [at] * C
+        lengths += [len(t)] * C
+        slots += [orc.slot(t, p, 16) for p in range(prefix, prefix + C)]
+        at += len(t)
+        ks.append(rng.normal(C * F, orc.BF16).reshape(C, F))
+        vs.append(rng.normal(C * F, orc.BF16).reshape(C, F))
+    ks, vs = np.concatenate(ks), np.concatenate(vs)
+    q = rng.normal(S * C * Hq * D, orc.BF16).reshape(S * C, Hq * D)
+    pool.upload(flat, offsets, lengths, positions, slots)
+    pool.append(0, to_dev(ks, orc.BF16), to_dev(vs, orc.BF16))
+    orc.store_kv(kc, vc, ks, vs, slots, 0, slot_count)
+    ctx.sync()
+    assert np.array_equal(to_host(kd, orc.BF16), kc)
+    assert np.array_equal(to_host(vd, orc.BF16), vc)
+
+    expected = orc.Attention(geom, kc, vc, orc.BF16, q, orc.BF16, positions, flat, offsets,
+                             lengths, Hq, 0, scale()).online_threads(8)
+    qd = to_dev(q, orc.BF16)
+    for name in ("attention", "prefill"):
+        out = torch.full_like(qd, float("nan"))
+        getattr(pool, name)(0, qd, Hq, scale(), out)
+        ctx.sync()
+        assert_close(to_f32(out), expected, what=f"{name}, prefix {prefix}")
+    pool.close()
+
+
+# (first position, rows) per sequence: single rows, rows across page and
+# 32-key block edges, tiles longer than one workgroup's share, a chunk
+# starting mid-page, and decode rows of other sequences in the same batch
+RAGGED = [(0, 1), (0, 40), (5, 300), (100, 33), (16, 257), (1000, 64), (700, 1), (63, 2)]
+
+
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_ragged_tiles_every_group_size(ctx, group, code):
+    print(f"ragged tiles group {group} dtype {code}", flush=True)
+    H = 2
+    Hq = H * group
+    F = H * D
+    rng = orc.Mt64(7 * group + code)
+    lengths_tok = [start + n for start, n in RAGGED]
+    total_pages = sum(pages_for(n) for n in lengths_tok)
+    blocks = total_pages + 7
+    perm = rng.permutation(blocks)
+    geom = (2, blocks, 16, H, D)
+    slot_count = blocks * 16
+    kc = rng.normal(2 * slot_count * F, code)  # every slot finite, layer 1 used
+    vc = rng.normal(2 * slot_count * F, code)
+    tables, at = [], 0
+    for n in lengths_tok:
+        tables.append(perm[at:at + pages_for(n)])
+        at += pages_for(n)
+    flat = np.concatenate(tables)
+    positions, offsets, lengths = [], [], []
+    at = 0
+    for (start, n), t in zip(RAGGED, tables):
+        positions += list(range(start, start + n))
+        offsets += [at] * n
+        lengths += [len(t)] * n
+        at += len(t)
+    rows = len(positions)
+    q = rng.normal(rows * Hq * D, code).reshape(rows, Hq * D)
+    pool, kd, vd = new_pool(ctx, geom, code)
+    kd.copy_(to_dev(kc, code))
+    vd.copy_(to_dev(vc, code))
+    pool.upload(flat, offsets, lengths, positions)
+    expected = orc.Attention(geom, kc, vc, code, q, code, positions, flat, offsets, lengths, Hq,
+                             1, scale()).online_threads(8)
+    qd = to_dev(q, code)
+    for name in ("attention", "prefill", "decode"):
+        out = torch.full_like(qd, float("nan"))
+        getattr(pool, name)(1, qd, Hq, scale(), out)
+        ctx.sync()
+        assert_close(to_f32(out), expected, what=f"{name}, group {group}")
+    pool.close()

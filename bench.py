@@ -90,25 +90,7 @@ def cpu_baseline(threads):
     }
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=0)
-    ap.add_argument("--calibrate-copy", action="store_true",
-                    help="first run one ckv_copy_blocks of 1024 pages (64 MiB read + 64 MiB "
-                         "written), the known-size copy the HBM counters are scaled by")
-    ap.add_argument("--no-fuse", action="store_true",
-                    help="append and decode as two launches instead of ckv_append_decode")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(run with --gpus 1)", file=sys.stderr)
-        sys.exit(2)
-
+def bench_config3(args):
     import torch
 
     from chibillm_amd import ckv
@@ -274,6 +256,208 @@ def main():
         threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
         log(f"CPU baseline on {threads} threads")
         result["cpu_baseline"] = cpu_baseline(threads)
+    return result
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
+PREFILL_SEQS, PREFILL_CHUNK = 64, 512
+
+
+def prefill_flops(prefix, chunk, seqs):
+    """Causal attention FLOPs of one layer: QK^T and PV, 2 FLOPs per MAC each,
+    over the keys each row attends (prefix + its own position + 1)."""
+    keys = sum(prefix + i + 1 for i in range(chunk))
+    return 4 * HEAD_DIM * Q_HEADS * seqs * keys
+
+
+def prefill_cpu_baseline(threads, prefix):
+    """Oracle causal attention (restated paged_flash_attention_prefill_f32 maths,
+    fp32) on a bounded sample: 4 sequences x 256 chunk rows of one layer."""
+    from oracle import oracle as orc
+
+    gen = np.random.default_rng(2)
+    seqs, rows = 4, 256
+    F = KV_HEADS * HEAD_DIM
+    pages = math.ceil((prefix + rows) / BLOCK)
+    n_pages = pages * seqs
+    kc = orc.from_f32(gen.standard_normal(n_pages * BLOCK * F, np.float32), orc.BF16)
+    vc = orc.from_f32(gen.standard_normal(n_pages * BLOCK * F, np.float32), orc.BF16)
+    q = orc.from_f32(gen.standard_normal((seqs * rows, Q_HEADS * HEAD_DIM), np.float32),
+                     orc.BF16)
+    table = gen.permutation(n_pages).astype(np.uint32)
+    positions = [prefix + i for _ in range(seqs) for i in range(rows)]
+    offsets = [s * pages for s in range(seqs) for _ in range(rows)]
+    att = orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, orc.BF16, q, orc.BF16,
+                        positions, table, offsets, [pages] * len(positions), Q_HEADS, 0,
+                        1 / math.sqrt(HEAD_DIM))
+    t0 = time.perf_counter()
+    att.online_threads(threads)
+    dt = time.perf_counter() - t0
+    flops = prefill_flops(prefix, rows, seqs)
+    return {
+        "value": round(flops / dt / 1e9, 3),
+        "unit": "GFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle/oracle.c causal attention over paged bf16 K/V, fp32 accumulate: "
+                   f"1 layer x {seqs} sequences x {rows} rows at positions {prefix}.."
+                   f"{prefix + rows - 1} ({flops / 1e9:.1f} GFLOP) in {dt:.2f} s on "
+                   f"{threads} threads"),
+    }
+
+
+def bench_config4(args):
+    """64 sequences share one prefix held once as pages; each step restores it
+    for every sequence (shared full pages; a copy-on-write copy of a partial
+    tail page, all layers, one ckv_copy_blocks), uploads the chunk's metadata,
+    then per layer appends the 512-row chunks and runs the MFMA prefill."""
+    import torch
+
+    from chibillm_amd import ckv
+    from oracle import oracle as orc  # seeded page order only
+
+    device = torch.device("cuda:0")
+    prefix, S, C = args.prefix, PREFILL_SEQS, PREFILL_CHUNK
+    F = KV_HEADS * HEAD_DIM
+    full = prefix // BLOCK
+    partial = prefix % BLOCK != 0
+    prefix_pages = math.ceil(prefix / BLOCK)
+    own = math.ceil((prefix + C) / BLOCK) - full
+    n_pool = prefix_pages + S * own + 16
+    perm = orc.Mt64(args.seed).permutation(n_pool)
+    prefix_table = perm[:prefix_pages]
+    tables = [np.concatenate([prefix_table[:full],
+                              perm[prefix_pages + s * own:prefix_pages + (s + 1) * own]])
+              for s in range(S)]
+    flat = np.concatenate(tables).astype(np.uint32)
+    positions = np.tile(np.arange(prefix, prefix + C, dtype=np.uint32), S)
+    offsets = np.repeat(np.arange(S, dtype=np.uint32) * len(tables[0]), C)
+    lengths = np.full(S * C, len(tables[0]), np.uint32)
+    slots = np.array([int(t[p // BLOCK]) * BLOCK + p % BLOCK
+                      for t in tables for p in range(prefix, prefix + C)], np.uint32)
+    cow_src = [int(prefix_table[full])] * S if partial else []
+    cow_dst = [int(t[full]) for t in tables] if partial else []
+
+    ctx = ckv.Context(0, stream=torch.cuda.current_stream())
+    elems = LAYERS * n_pool * BLOCK * F
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed)
+    keys = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=gen)
+    values = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=gen)
+    pool = ckv.Pool(ctx, LAYERS, n_pool, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16, keys, values)
+    rows = S * C
+    q = torch.randn(LAYERS, rows, Q_HEADS * HEAD_DIM, generator=gen, device=device).to(torch.bfloat16)
+    k_new = torch.randn(LAYERS, rows, F, generator=gen, device=device).to(torch.bfloat16)
+    v_new = torch.randn(LAYERS, rows, F, generator=gen, device=device).to(torch.bfloat16)
+    out = torch.empty(LAYERS, rows, Q_HEADS * HEAD_DIM, dtype=torch.bfloat16, device=device)
+    scale = 1.0 / math.sqrt(HEAD_DIM)
+    log(f"config4: prefix {prefix} ({prefix_pages} shared pages, tail copy: {partial}), "
+        f"{S} x {C}-row chunks, pool {n_pool} pages x {LAYERS} layers")
+
+    def one_step():
+        if partial:
+            pool.copy_blocks(cow_src, cow_dst)
+        pool.upload(flat, offsets, lengths, positions, slots)
+        for layer in range(LAYERS):
+            pool.append(layer, k_new[layer], v_new[layer])
+            pool.prefill(layer, q[layer], Q_HEADS, scale, out[layer])
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    ctx.profile(True)
+    ctx.profile_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kernels = {}
+    for name in ("paged_attention_prefill", "store_kv", "copy_blocks"):
+        ms, n = ctx.profile_query(name)
+        kernels[name] = (ms, n)
+    ctx.profile(False)
+    prefill_ms, prefill_n = kernels["paged_attention_prefill"]
+    avg_s = prefill_ms / prefill_n / 1e3
+    flops = prefill_flops(prefix, C, S)
+    achieved = flops / avg_s / 1e12
+    ms_per_step = elapsed * 1e3 / args.steps
+    result = {
+        "metric": "chunked-prefill attention TFLOP/s (MFMA) + tokens/s, Qwen3-0.6B KV, "
+                  "64 sequences x 512-token chunks over a shared prefix",
+        "value": round(LAYERS * flops * args.steps / elapsed / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) K/V/Q, seeded page order",
+        "config": {
+            "workload": f"config4: {S} sequences share a {prefix}-token prefix (refcounted "
+                        f"pages, copy-on-write tail: {partial}); each appends and prefills a "
+                        f"{C}-row causal chunk over prefix + chunk, {LAYERS} layers per step",
+            "layers": LAYERS, "sequences": S, "chunk": C, "prefix": prefix,
+            "kv_heads": KV_HEADS, "q_heads": Q_HEADS, "head_dim": HEAD_DIM,
+            "block_size": BLOCK, "pool_pages": n_pool,
+        },
+        "tokens_per_s": round(S * C * args.steps / elapsed, 1),
+        "kernels_ms_per_step": {k: round(v[0] / args.steps, 4) for k, v in kernels.items()},
+        "roofline": {
+            "kernel": "paged_attention_prefill",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "avg_launch_us": round(avg_s * 1e6, 2),
+            "algorithmic_flops_per_launch": flops,
+        },
+        "cpu_baseline": None,
+    }
+    pool.close()
+    del keys, values, q, k_new, v_new, out
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
+        log(f"CPU baseline on {threads} threads")
+        result["cpu_baseline"] = prefill_cpu_baseline(threads, prefix)
+    return result
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run one ckv_copy_blocks of 1024 pages (64 MiB read + 64 MiB "
+                         "written), the known-size copy the HBM counters are scaled by")
+    ap.add_argument("--no-fuse", action="store_true",
+                    help="append and decode as two launches instead of ckv_append_decode")
+    ap.add_argument("--workload", choices=["config3", "config4"], default="config3",
+                    help="config3 (default): the headline decode step; config4: chunked "
+                         "prefill of 64 sequences over a shared prefix (MFMA tiles)")
+    ap.add_argument("--prefix", type=int, default=2008,
+                    help="config4 shared prefix tokens (2008 leaves a partial tail page, "
+                         "so every sequence copies it on write; 2000 does not)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    if args.workload == "config4":
+        result = bench_config4(args)
+    else:
+        result = bench_config3(args)
     print(json.dumps(result), flush=True)
 
 

@@ -91,28 +91,38 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi)
         return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-// One q-block's online-softmax step over the 16 scores this lane holds.
-// Scores are raw q.k; c = scale * log2(e) so every exponential is one exp2.
-// Returns the factor the accumulator must be multiplied by.
-__device__ __forceinline__ float softmax_step(f32x16_t& s, float& m, float& l, float c)
+// Growth of the running maximum (log2 units) that forces a rescale. Below it
+// the probabilities keep using the older, smaller maximum and may reach
+// 2^rescale_log2 (exact in fp32 and in the 16-bit P operand's exponent
+// range); the final division by the denominator, accumulated with the same
+// maximum, removes the offset exactly. Skipping the rescale of 128 fp32
+// accumulators per block matters because on random data some lane of a
+// 32-query block sees a new maximum in most key blocks.
+constexpr float rescale_log2 = 8.0f;
+
+// Row maximum of the 16 scores a lane holds and its partner lane's 16.
+__device__ __forceinline__ float block_max(const f32x16_t& s)
 {
     float mx = s[0];
 #pragma unroll
     for (int r = 1; r < 16; ++r)
         mx = fmaxf(mx, s[r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx);
-    const float mc = m_new * c;
+    return fmaxf(mx, __shfl_xor(mx, 32));
+}
+
+// Probabilities of one q-block against the running maximum m (raw q.k
+// units; c = scale * log2(e) so every exponential is one exp2), added to
+// this lane's share of the denominator.
+__device__ __forceinline__ void exponentiate(f32x16_t& s, float m, float& l, float c)
+{
+    const float mc = m * c;
     float sum = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         s[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -mc));
         sum += s[r];
     }
-    const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c); // m = -inf at the start: 0
-    l = l * alpha + sum;
-    m = m_new;
-    return alpha;
+    l += sum;
 }
 
 template <int G, bool F16>
@@ -151,7 +161,7 @@ __global__ __launch_bounds__(threads, 1) void prefill_kernel(pool_view p, meta_v
     uint32_t head[2], qpos[2];
     size_t qoff[2];
     bool valid[2];
-    uint32_t row_lo = ~0u, row_hi = 0;
+    uint32_t row_lo = ~0u;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         const uint32_t b = 2 * wave + s;
@@ -162,11 +172,9 @@ __global__ __launch_bounds__(threads, 1) void prefill_kernel(pool_view p, meta_v
         qpos[s] = pos0 + min(row, nrows - 1);
         qoff[s] = (size_t)(row0 + min(row, nrows - 1)) * q_stride + (size_t)head[s] * dim;
         row_lo = min(row_lo, rb * 32);
-        row_hi = max(row_hi, rb * 32 + 31);
     }
     const bool active = row_lo < nrows;
     const uint32_t pos_lo = pos0 + row_lo;
-    const uint32_t pos_hi = pos0 + min(row_hi, nrows - 1);
 
     // Q^T operands: lane (n, g) holds features 16*ks + 8*g .. +7 of its query
     uint4 qr[2][8];
@@ -226,73 +234,113 @@ __global__ __launch_bounds__(threads, 1) void prefill_kernel(pool_view p, meta_v
 
     f32x16_t o[2][4];
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
-            o[s][mt] = f32x16_t {};
+            o[sb][mt] = f32x16_t {};
     float m[2] = { -__builtin_inff(), -__builtin_inff() };
     float l[2] = { 0.0f, 0.0f };
+
+    // S^T of one block for both q-blocks, causal mask applied; the block's
+    // V^T operands are requested here too so their latency overlaps the
+    // softmax. Every wave computes every block: blocks past a wave's last
+    // row are fully masked (P = 0), and each wave has its own SIMD.
+    f32x16_t sc[2];
+    uint4 va[4][2];
+    auto scores = [&](uint32_t kb) {
+        const uint8_t* st = lds + (kb & 1) * stage_bytes;
+        const uint32_t key0 = kb * block_keys;
+        const uint8_t* krow = st + n * k_row_bytes + g * 16;
+        uint4 ka[8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+            ka[ks] = *reinterpret_cast<const uint4*>(krow + ks * 32);
+        sc[0] = f32x16_t {};
+        sc[1] = f32x16_t {};
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            sc[0] = mfma<F16>(ka[ks], qr[0][ks], sc[0]);
+            sc[1] = mfma<F16>(ka[ks], qr[1][ks], sc[1]);
+        }
+        const uint8_t* vt = st + k_bytes + g * 16;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                va[mt][h] = *reinterpret_cast<const uint4*>(
+                    vt + vt_row(32 * mt + n) * vt_row_bytes + h * 32);
+        if (key0 + block_keys - 1 > pos_lo) { // the causal diagonal crosses this block
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t kpos = key0 + 16 * (r >> 3) + 8 * g + (r & 7);
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb)
+                    if (kpos > qpos[sb])
+                        sc[sb][r] = -__builtin_inff();
+            }
+        }
+    };
+    // P = exp2 against the running maxima, O^T += V^T P^T, then stage the
+    // next block and synchronise.
+    auto finish = [&](uint32_t kb) {
+        uint4 pt[2][2];
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            exponentiate(sc[sb], m[sb], l[sb], c);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                pt[sb][h] = make_uint4(pack2<F16>(sc[sb][8 * h + 0], sc[sb][8 * h + 1]),
+                                       pack2<F16>(sc[sb][8 * h + 2], sc[sb][8 * h + 3]),
+                                       pack2<F16>(sc[sb][8 * h + 4], sc[sb][8 * h + 5]),
+                                       pack2<F16>(sc[sb][8 * h + 6], sc[sb][8 * h + 7]));
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                o[0][mt] = mfma<F16>(va[mt][h], pt[0][h], o[0][mt]);
+                o[1][mt] = mfma<F16>(va[mt][h], pt[1][h], o[1][mt]);
+            }
+        if (kb + 1 < n_blocks)
+            store_block(lds + ((kb + 1) & 1) * stage_bytes);
+        __syncthreads();
+    };
 
     load_block(0);
     store_block(lds);
     __syncthreads();
 
-    for (uint32_t kb = 0; kb < n_blocks; ++kb) {
-        const bool more = kb + 1 < n_blocks;
-        if (more)
-            load_block(kb + 1);
-        const uint8_t* st = lds + (kb & 1) * stage_bytes;
-        const uint32_t key0 = kb * block_keys;
-        if (active && key0 <= pos_hi) {
-            f32x16_t sc[2] = { f32x16_t {}, f32x16_t {} };
-            const uint8_t* krow = st + n * k_row_bytes + g * 16;
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                const uint4 a = *reinterpret_cast<const uint4*>(krow + ks * 32);
-                sc[0] = mfma<F16>(a, qr[0][ks], sc[0]);
-                sc[1] = mfma<F16>(a, qr[1][ks], sc[1]);
-            }
-            if (key0 + block_keys - 1 > pos_lo) { // the causal diagonal crosses this block
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint32_t kpos = key0 + 16 * (r >> 3) + 8 * g + (r & 7);
-#pragma unroll
-                    for (int s = 0; s < 2; ++s)
-                        if (kpos > qpos[s])
-                            sc[s][r] = -__builtin_inff();
-                }
-            }
-            uint4 pt[2][2];
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const float alpha = softmax_step(sc[s], m[s], l[s], c);
-                if (__any(alpha != 1.0f)) {
-#pragma unroll
-                    for (int mt = 0; mt < 4; ++mt)
-                        o[s][mt] *= alpha;
-                }
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-                    pt[s][h] = make_uint4(pack2<F16>(sc[s][8 * h + 0], sc[s][8 * h + 1]),
-                                          pack2<F16>(sc[s][8 * h + 2], sc[s][8 * h + 3]),
-                                          pack2<F16>(sc[s][8 * h + 4], sc[s][8 * h + 5]),
-                                          pack2<F16>(sc[s][8 * h + 6], sc[s][8 * h + 7]));
-            }
-            const uint8_t* vt = st + k_bytes + g * 16;
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const uint8_t* vrow = vt + vt_row(32 * mt + n) * vt_row_bytes;
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint4 a = *reinterpret_cast<const uint4*>(vrow + h * 32);
-                    o[0][mt] = mfma<F16>(a, pt[0][h], o[0][mt]);
-                    o[1][mt] = mfma<F16>(a, pt[1][h], o[1][mt]);
-                }
-            }
+    // The hot loop never touches the accumulators outside the matrix
+    // products; a block whose maximum grows past the threshold leaves it,
+    // rescales, finishes and re-enters.
+    uint32_t kb = 0;
+    while (kb < n_blocks) {
+        float mx[2];
+        for (; kb < n_blocks; ++kb) {
+            if (kb + 1 < n_blocks)
+                load_block(kb + 1);
+            scores(kb);
+            mx[0] = block_max(sc[0]);
+            mx[1] = block_max(sc[1]);
+            // m = -inf before the first block, so it always leaves there
+            if (__any((mx[0] - m[0]) * c > rescale_log2 || (mx[1] - m[1]) * c > rescale_log2))
+                break;
+            finish(kb);
         }
-        if (more)
-            store_block(lds + ((kb + 1) & 1) * stage_bytes);
-        __syncthreads();
+        if (kb == n_blocks)
+            break;
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            const float m_new = fmaxf(m[sb], mx[sb]);
+            const float alpha = __builtin_amdgcn_exp2f((m[sb] - m_new) * c); // 0 at the start
+            l[sb] *= alpha;
+            m[sb] = m_new;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+                o[sb][mt] *= alpha;
+        }
+        finish(kb);
+        ++kb;
     }
 
     if (!active)

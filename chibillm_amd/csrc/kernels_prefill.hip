@@ -48,7 +48,6 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr uint32_t dim = 128;
 constexpr uint32_t page_tokens = 16;
 constexpr uint32_t block_keys = 32;
-constexpr uint32_t threads = 256;
 constexpr uint32_t k_row_bytes = 272;  // 256 + 16: rows 0..7 start in distinct 16-byte bank groups
 constexpr uint32_t vt_row_bytes = 80;  // 64 + 16: likewise for 8 consecutive feature rows
 constexpr uint32_t k_bytes = block_keys * k_row_bytes;
@@ -125,12 +124,16 @@ __device__ __forceinline__ void exponentiate(f32x16_t& s, float m, float& l, flo
     l += sum;
 }
 
-template <int G, bool F16>
-__global__ __launch_bounds__(threads, 1) void prefill_kernel(pool_view p, meta_view md,
-                                                             uint32_t layer,
-                                                             const uint16_t* __restrict__ q,
-                                                             uint16_t* __restrict__ out,
-                                                             uint32_t q_heads, float c)
+// QB q-blocks (32 queries each) per wave: QB = 2 runs four waves of 64
+// queries, one wave per SIMD; QB = 1 runs eight waves of 32 queries, two
+// per SIMD, so one wave's softmax overlaps the other's matrix products.
+template <int QB>
+constexpr uint32_t wg_threads = 64 * (8 / QB);
+
+template <int G, int QB, bool F16>
+__global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kernel(
+    pool_view p, meta_view md, uint32_t layer, const uint16_t* __restrict__ q,
+    uint16_t* __restrict__ out, uint32_t q_heads, float c)
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * stage_bytes];
     constexpr uint32_t tile_rows = 256 / G;
@@ -157,95 +160,135 @@ __global__ __launch_bounds__(threads, 1) void prefill_kernel(pool_view p, meta_v
     const uint32_t F = p.features;
     const size_t q_stride = (size_t)q_heads * dim;
 
-    // this wave's two q-blocks
-    uint32_t head[2], qpos[2];
-    size_t qoff[2];
-    bool valid[2];
+    // this wave's q-blocks
+    uint32_t qpos[QB];
+    size_t qoff[QB];
+    bool valid[QB];
     uint32_t row_lo = ~0u;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        const uint32_t b = 2 * wave + s;
+    for (int sb = 0; sb < QB; ++sb) {
+        const uint32_t b = QB * wave + sb;
         const uint32_t rb = b / G;
-        head[s] = kvh * G + b % G;
+        const uint32_t head = kvh * G + b % G;
         const uint32_t row = rb * 32 + n;
-        valid[s] = row < nrows;
-        qpos[s] = pos0 + min(row, nrows - 1);
-        qoff[s] = (size_t)(row0 + min(row, nrows - 1)) * q_stride + (size_t)head[s] * dim;
+        valid[sb] = row < nrows;
+        qpos[sb] = pos0 + min(row, nrows - 1);
+        qoff[sb] = (size_t)(row0 + min(row, nrows - 1)) * q_stride + (size_t)head * dim;
         row_lo = min(row_lo, rb * 32);
     }
     const bool active = row_lo < nrows;
     const uint32_t pos_lo = pos0 + row_lo;
 
     // Q^T operands: lane (n, g) holds features 16*ks + 8*g .. +7 of its query
-    uint4 qr[2][8];
+    uint4 qr[QB][8];
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int sb = 0; sb < QB; ++sb)
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks)
-            qr[s][ks] = valid[s] && active
-                ? *reinterpret_cast<const uint4*>(q + qoff[s] + ks * 16 + g * 8)
+            qr[sb][ks] = valid[sb] && active
+                ? *reinterpret_cast<const uint4*>(q + qoff[sb] + ks * 16 + g * 8)
                 : make_uint4(0, 0, 0, 0);
 
     const uint16_t* kbase = static_cast<const uint16_t*>(p.keys) + layer * p.layer_elems + kvh * dim;
     const uint16_t* vbase = static_cast<const uint16_t*>(p.values) + layer * p.layer_elems + kvh * dim;
-    // staging roles: K row t/16 (+16), chunk t%16; V key pair t/16, chunk t%16
-    const uint32_t srow = tid >> 4, chunk = tid & 15;
+    // Staging roles over 256 threads: K rows t/16 and 16 + t/16, chunk t%16;
+    // V key pair t/16, chunk t%16. With 512 threads the first 256 stage V
+    // and the other 256 stage K (wave-uniform).
+    const uint32_t st_tid = tid & 255;
+    const bool k_role = QB == 2 || tid >= 256;
+    const bool v_role = QB == 2 || tid < 256;
+    const uint32_t srow = st_tid >> 4, chunk = st_tid & 15;
 
+    // Loads are unconditional so the compiler can keep them in flight across
+    // the block's compute: a key past the tile's last position is read from a
+    // slot of the block's first page (always in the table) and replaced by
+    // zero when staged.
     uint4 kr[2], vr[2];
+    // The block table entries of a block are read one block before its K/V
+    // loads are issued, so that dependent load never stalls the wave.
+    uint32_t key0_next = 0;
+    uint32_t page_a = 0, page_b = 0; // pages of the next block to load
+    auto fetch_pages = [&](uint32_t kb) {
+        if (kb < n_blocks) {
+            const uint32_t key0 = kb * block_keys;
+            page_a = __builtin_amdgcn_readfirstlane(table[2 * kb]);
+            page_b = key0 + page_tokens <= pos_last
+                ? __builtin_amdgcn_readfirstlane(table[2 * kb + 1])
+                : page_a;
+        }
+    };
     auto load_block = [&](uint32_t kb) {
         const uint32_t key0 = kb * block_keys;
-        const uint32_t pg0 = table[2 * kb];
-        const uint32_t pg1 = key0 + page_tokens <= pos_last ? table[2 * kb + 1] : 0;
+        key0_next = key0;
+        const uint32_t pg0 = page_a, pg1 = page_b;
+        fetch_pages(kb + 1);
+        if (k_role) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t key = 16 * i + srow;
-            const size_t slot = (size_t)(i ? pg1 : pg0) * page_tokens + srow;
-            kr[i] = key0 + key <= pos_last
-                ? *reinterpret_cast<const uint4*>(kbase + slot * F + chunk * 8)
-                : make_uint4(0, 0, 0, 0);
+            for (int i = 0; i < 2; ++i) {
+                const size_t slot = (size_t)(i ? pg1 : pg0) * page_tokens + srow;
+                kr[i] = *reinterpret_cast<const uint4*>(kbase + slot * F + chunk * 8);
+            }
         }
-        const uint32_t vpg = srow < 8 ? pg0 : pg1;
-        const uint32_t vtok = (2 * srow) & 15;
+        if (v_role) {
+            const uint32_t vpg = srow < 8 ? pg0 : pg1;
+            const uint32_t vtok = (2 * srow) & 15;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const size_t slot = (size_t)vpg * page_tokens + vtok + i;
-            vr[i] = key0 + 2 * srow + i <= pos_last
-                ? *reinterpret_cast<const uint4*>(vbase + slot * F + chunk * 8)
-                : make_uint4(0, 0, 0, 0);
+            for (int i = 0; i < 2; ++i) {
+                const size_t slot = (size_t)vpg * page_tokens + vtok + i;
+                vr[i] = *reinterpret_cast<const uint4*>(vbase + slot * F + chunk * 8);
+            }
         }
     };
+    // all-ones when `keep`, else zero (element-wise masks keep the staging
+    // registers out of private memory, which a select of whole vectors does not)
+    auto masked = [](const uint4& v, bool keep) {
+        const uint32_t k = keep ? ~0u : 0u;
+        return make_uint4(v.x & k, v.y & k, v.z & k, v.w & k);
+    };
     auto store_block = [&](uint8_t* st) {
+        if (k_role) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            *reinterpret_cast<uint4*>(st + key_row(16 * i + srow) * k_row_bytes + chunk * 16) = kr[i];
-        uint8_t* vt = st + k_bytes;
-        const uint32_t w0[4] = { vr[0].x, vr[0].y, vr[0].z, vr[0].w };
-        const uint32_t w1[4] = { vr[1].x, vr[1].y, vr[1].z, vr[1].w };
+            for (int i = 0; i < 2; ++i)
+                *reinterpret_cast<uint4*>(st + key_row(16 * i + srow) * k_row_bytes + chunk * 16) =
+                    masked(kr[i], key0_next + 16 * i + srow <= pos_last);
+        }
+        if (v_role) {
+            uint8_t* vt = st + k_bytes;
+            const uint4 v0 = masked(vr[0], key0_next + 2 * srow <= pos_last);
+            const uint4 v1 = masked(vr[1], key0_next + 2 * srow + 1 <= pos_last);
+            const uint32_t w0[4] = { v0.x, v0.y, v0.z, v0.w };
+            const uint32_t w1[4] = { v1.x, v1.y, v1.z, v1.w };
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            // features 8*chunk + 2d (low halves) and + 2d + 1 (high halves), keys (2*srow, +1)
-            const uint32_t even = __builtin_amdgcn_perm(w1[d], w0[d], 0x05040100u);
-            const uint32_t odd = __builtin_amdgcn_perm(w1[d], w0[d], 0x07060302u);
-            const uint32_t f = 8 * chunk + 2 * d;
-            *reinterpret_cast<uint32_t*>(vt + vt_row(f) * vt_row_bytes + 4 * srow) = even;
-            *reinterpret_cast<uint32_t*>(vt + vt_row(f + 1) * vt_row_bytes + 4 * srow) = odd;
+            for (int d = 0; d < 4; ++d) {
+                // features 8*chunk + 2d (low halves) and + 2d + 1 (high halves), keys (2*srow, +1)
+                const uint32_t even = __builtin_amdgcn_perm(w1[d], w0[d], 0x05040100u);
+                const uint32_t odd = __builtin_amdgcn_perm(w1[d], w0[d], 0x07060302u);
+                const uint32_t f = 8 * chunk + 2 * d;
+                *reinterpret_cast<uint32_t*>(vt + vt_row(f) * vt_row_bytes + 4 * srow) = even;
+                *reinterpret_cast<uint32_t*>(vt + vt_row(f + 1) * vt_row_bytes + 4 * srow) = odd;
+            }
         }
     };
 
-    f32x16_t o[2][4];
+    f32x16_t o[QB][4];
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
+    for (int sb = 0; sb < QB; ++sb)
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
             o[sb][mt] = f32x16_t {};
-    float m[2] = { -__builtin_inff(), -__builtin_inff() };
-    float l[2] = { 0.0f, 0.0f };
+    float m[QB], l[QB];
+#pragma unroll
+    for (int sb = 0; sb < QB; ++sb) {
+        m[sb] = -__builtin_inff();
+        l[sb] = 0.0f;
+    }
 
-    // S^T of one block for both q-blocks, causal mask applied; the block's
-    // V^T operands are requested here too so their latency overlaps the
-    // softmax. Every wave computes every block: blocks past a wave's last
-    // row are fully masked (P = 0), and each wave has its own SIMD.
-    f32x16_t sc[2];
+    // S^T of one block for the wave's q-blocks, causal mask applied; the
+    // block's V^T operands are requested here too so their latency overlaps
+    // the softmax. Every wave computes every block: blocks past a wave's last
+    // row are fully masked (P = 0), and a branch here would turn the
+    // accumulators into a loop phi.
+    f32x16_t sc[QB];
     uint4 va[4][2];
     auto scores = [&](uint32_t kb) {
         const uint8_t* st = lds + (kb & 1) * stage_bytes;
@@ -255,13 +298,14 @@ __global__ __launch_bounds__(threads, 1) void prefill_kernel(pool_view p, meta_v
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks)
             ka[ks] = *reinterpret_cast<const uint4*>(krow + ks * 32);
-        sc[0] = f32x16_t {};
-        sc[1] = f32x16_t {};
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            sc[0] = mfma<F16>(ka[ks], qr[0][ks], sc[0]);
-            sc[1] = mfma<F16>(ka[ks], qr[1][ks], sc[1]);
-        }
+        for (int sb = 0; sb < QB; ++sb)
+            sc[sb] = f32x16_t {};
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+            for (int sb = 0; sb < QB; ++sb)
+                sc[sb] = mfma<F16>(ka[ks], qr[sb][ks], sc[sb]);
         const uint8_t* vt = st + k_bytes + g * 16;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
@@ -274,7 +318,7 @@ __global__ __launch_bounds__(threads, 1) void prefill_kernel(pool_view p, meta_v
             for (int r = 0; r < 16; ++r) {
                 const uint32_t kpos = key0 + 16 * (r >> 3) + 8 * g + (r & 7);
 #pragma unroll
-                for (int sb = 0; sb < 2; ++sb)
+                for (int sb = 0; sb < QB; ++sb)
                     if (kpos > qpos[sb])
                         sc[sb][r] = -__builtin_inff();
             }
@@ -283,29 +327,28 @@ __global__ __launch_bounds__(threads, 1) void prefill_kernel(pool_view p, meta_v
     // P = exp2 against the running maxima, O^T += V^T P^T, then stage the
     // next block and synchronise.
     auto finish = [&](uint32_t kb) {
-        uint4 pt[2][2];
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
+        for (int sb = 0; sb < QB; ++sb) {
             exponentiate(sc[sb], m[sb], l[sb], c);
+            uint4 pt[2];
 #pragma unroll
             for (int h = 0; h < 2; ++h)
-                pt[sb][h] = make_uint4(pack2<F16>(sc[sb][8 * h + 0], sc[sb][8 * h + 1]),
-                                       pack2<F16>(sc[sb][8 * h + 2], sc[sb][8 * h + 3]),
-                                       pack2<F16>(sc[sb][8 * h + 4], sc[sb][8 * h + 5]),
-                                       pack2<F16>(sc[sb][8 * h + 6], sc[sb][8 * h + 7]));
+                pt[h] = make_uint4(pack2<F16>(sc[sb][8 * h + 0], sc[sb][8 * h + 1]),
+                                   pack2<F16>(sc[sb][8 * h + 2], sc[sb][8 * h + 3]),
+                                   pack2<F16>(sc[sb][8 * h + 4], sc[sb][8 * h + 5]),
+                                   pack2<F16>(sc[sb][8 * h + 6], sc[sb][8 * h + 7]));
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+                    o[sb][mt] = mfma<F16>(va[mt][h], pt[h], o[sb][mt]);
         }
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                o[0][mt] = mfma<F16>(va[mt][h], pt[0][h], o[0][mt]);
-                o[1][mt] = mfma<F16>(va[mt][h], pt[1][h], o[1][mt]);
-            }
         if (kb + 1 < n_blocks)
             store_block(lds + ((kb + 1) & 1) * stage_bytes);
         __syncthreads();
     };
 
+    fetch_pages(0);
     load_block(0);
     store_block(lds);
     __syncthreads();
@@ -315,22 +358,26 @@ __global__ __launch_bounds__(threads, 1) void prefill_kernel(pool_view p, meta_v
     // rescales, finishes and re-enters.
     uint32_t kb = 0;
     while (kb < n_blocks) {
-        float mx[2];
+        float mx[QB];
         for (; kb < n_blocks; ++kb) {
             if (kb + 1 < n_blocks)
                 load_block(kb + 1);
             scores(kb);
-            mx[0] = block_max(sc[0]);
-            mx[1] = block_max(sc[1]);
+            bool grow = false;
+#pragma unroll
+            for (int sb = 0; sb < QB; ++sb) {
+                mx[sb] = block_max(sc[sb]);
+                grow = grow || (mx[sb] - m[sb]) * c > rescale_log2;
+            }
             // m = -inf before the first block, so it always leaves there
-            if (__any((mx[0] - m[0]) * c > rescale_log2 || (mx[1] - m[1]) * c > rescale_log2))
+            if (__any(grow))
                 break;
             finish(kb);
         }
         if (kb == n_blocks)
             break;
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
+        for (int sb = 0; sb < QB; ++sb) {
             const float m_new = fmaxf(m[sb], mx[sb]);
             const float alpha = __builtin_amdgcn_exp2f((m[sb] - m_new) * c); // 0 at the start
             l[sb] *= alpha;
@@ -346,17 +393,17 @@ __global__ __launch_bounds__(threads, 1) void prefill_kernel(pool_view p, meta_v
     if (!active)
         return;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        const float inv = 1.0f / (l[s] + __shfl_xor(l[s], 32));
-        if (!valid[s])
+    for (int sb = 0; sb < QB; ++sb) {
+        const float inv = 1.0f / (l[sb] + __shfl_xor(l[sb], 32));
+        if (!valid[sb])
             continue;
-        uint16_t* dst = out + qoff[s];
+        uint16_t* dst = out + qoff[sb];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
             for (int quad = 0; quad < 4; ++quad) {
                 const uint32_t f = 32 * mt + 8 * quad + 4 * g;
-                const f32x16_t& acc = o[s][mt];
+                const f32x16_t& acc = o[sb][mt];
                 *reinterpret_cast<uint2*>(dst + f) =
                     make_uint2(pack2<F16>(acc[4 * quad] * inv, acc[4 * quad + 1] * inv),
                                pack2<F16>(acc[4 * quad + 2] * inv, acc[4 * quad + 3] * inv));
@@ -364,18 +411,23 @@ __global__ __launch_bounds__(threads, 1) void prefill_kernel(pool_view p, meta_v
     }
 }
 
+#ifndef CKV_PREFILL_QB
+#define CKV_PREFILL_QB 1
+#endif
+
 template <int G>
 hipError_t launch_g(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                     const void* q, uint32_t q_heads, float c, void* out, uint32_t grid)
 {
+    constexpr int QB = CKV_PREFILL_QB;
     const auto* qq = static_cast<const uint16_t*>(q);
     auto* oo = static_cast<uint16_t*>(out);
     if (p.dtype == CKV_F16)
-        hipLaunchKernelGGL((prefill_kernel<G, true>), dim3(grid), dim3(threads), 0, s, p, m, layer,
-                           qq, oo, q_heads, c);
+        hipLaunchKernelGGL((prefill_kernel<G, QB, true>), dim3(grid), dim3(wg_threads<QB>), 0, s,
+                           p, m, layer, qq, oo, q_heads, c);
     else
-        hipLaunchKernelGGL((prefill_kernel<G, false>), dim3(grid), dim3(threads), 0, s, p, m,
-                           layer, qq, oo, q_heads, c);
+        hipLaunchKernelGGL((prefill_kernel<G, QB, false>), dim3(grid), dim3(wg_threads<QB>), 0, s,
+                           p, m, layer, qq, oo, q_heads, c);
     return hipGetLastError();
 }
 

@@ -429,6 +429,81 @@ def bench_config4(args):
     return result
 
 
+CHURN_STEPS = 5000
+
+
+def bench_config5(args):
+    """The churn trace runs in the C++ driver (chibillm_amd/bin/churn): the
+    scheduler, refcounted pages and a 160 GB device pool, one engine step per
+    scheduler step. --steps sets the trace length (default 5000 when the
+    default 20 is given); warmup does not apply to a trace."""
+    import subprocess
+
+    steps = CHURN_STEPS if args.steps == 20 else args.steps
+    driver = os.path.join(ROOT, "chibillm_amd", "bin", "churn")
+    if not os.path.exists(driver):
+        raise SystemExit(f"{driver} is not built: run __graft_entry__.build()")
+    cmd = [driver, "--steps", str(steps), "--seed", str(args.seed), "--profile"]
+    log("config5: " + " ".join(cmd))
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    sys.stderr.write(proc.stderr)
+    if proc.returncode != 0:
+        raise SystemExit(f"churn driver failed ({proc.returncode})")
+    trace = json.loads(proc.stdout.strip().splitlines()[-1])
+    decode_ms, decode_n = trace["kernels_ms"]["append_decode"]
+    decode_s = decode_ms / 1e3
+    achieved = trace["decode_step_bytes"] / decode_s / 1e9 if decode_s else 0.0
+    result = {
+        "metric": "continuous-batching churn: tokens/s, steps/s and HBM fraction, Qwen3-0.6B KV, "
+                  "28 layers, 160 GB page pool, live batch <= 512",
+        "value": trace["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": 0,
+        "ms_per_step": round(trace["seconds"] * 1e3 / steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) K/V/Q rows; seeded Poisson(8) arrivals, lognormal prompt "
+                "(median 512, sigma 1, [16, 16384]) and output (median 256, sigma 1, [1, 4096])",
+        "config": {
+            "workload": "config5: churn trace through the C++ scheduler and page allocator; each "
+                        "step uploads the batch tables and runs append + paged attention for 28 "
+                        "layers (prefill tiles or fused decode)",
+            "pool_pages": trace["pool_pages"], "max_live": 512, "max_batch_tokens": 2048,
+            "prefill_chunk": 512,
+        },
+        "steps_per_s": trace["steps_per_s"],
+        "hbm_frac": trace["hbm_frac"],
+        "hbm_gbs": trace["hbm_gbs"],
+        "trace": {k: trace[k] for k in ("prefill_tokens", "decode_tokens", "prefill_steps",
+                                        "decode_steps", "arrived", "admitted", "finished",
+                                        "pending_at_end", "peak_live")},
+        "kernels_ms_per_step": {k: round(v[0] / steps, 4) for k, v in trace["kernels_ms"].items()},
+        "roofline": {
+            "kernel": "append_decode",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(decode_ms * 1e3 / max(decode_n, 1), 2),
+            "algorithmic_bytes_per_launch": int(trace["decode_step_bytes"] / max(decode_n, 1)),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
+        log(f"CPU baseline on {threads} threads")
+        base = cpu_baseline(threads)
+        base["sample"] = "decode attention, the dominant work of the trace: " + base["sample"]
+        result["cpu_baseline"] = base
+    return result
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -442,9 +517,10 @@ def main():
                          "written), the known-size copy the HBM counters are scaled by")
     ap.add_argument("--no-fuse", action="store_true",
                     help="append and decode as two launches instead of ckv_append_decode")
-    ap.add_argument("--workload", choices=["config3", "config4"], default="config3",
+    ap.add_argument("--workload", choices=["config3", "config4", "config5"], default="config3",
                     help="config3 (default): the headline decode step; config4: chunked "
-                         "prefill of 64 sequences over a shared prefix (MFMA tiles)")
+                         "prefill of 64 sequences over a shared prefix (MFMA tiles); config5: "
+                         "the continuous-batching churn trace (C++ scheduler driver)")
     ap.add_argument("--prefix", type=int, default=2008,
                     help="config4 shared prefix tokens (2008 leaves a partial tail page, "
                          "so every sequence copies it on write; 2000 does not)")
@@ -456,6 +532,8 @@ def main():
 
     if args.workload == "config4":
         result = bench_config4(args)
+    elif args.workload == "config5":
+        result = bench_config5(args)
     else:
         result = bench_config3(args)
     print(json.dumps(result), flush=True)

@@ -12,7 +12,7 @@
  * Metal. Where only a Metal kernel exists, the kernel's arithmetic is written
  * out as scalar C with fp32 accumulation, in the kernel's own order.
  *
- * Pinning (tests/test_oracle_*.py): every function below is checked against
+ * Pinning (tests/test_oracle.py): every function below is checked against
  * the reference's own known-answer tests, a closed form, a brute-force
  * double-precision computation, or an exhaustive enumeration.
  */

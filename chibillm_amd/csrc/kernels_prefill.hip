@@ -135,7 +135,7 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
     pool_view p, meta_view md, uint32_t layer, const uint16_t* __restrict__ q,
     uint16_t* __restrict__ out, uint32_t q_heads, float c)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * stage_bytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[3 * stage_bytes];
     constexpr uint32_t tile_rows = 256 / G;
 
     const uint32_t kv_heads = p.kv_heads;
@@ -283,21 +283,18 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
         l[sb] = 0.0f;
     }
 
-    // S^T of one block for the wave's q-blocks, causal mask applied; the
-    // block's V^T operands are requested here too so their latency overlaps
-    // the softmax. Every wave computes every block: blocks past a wave's last
-    // row are fully masked (P = 0), and a branch here would turn the
-    // accumulators into a loop phi.
-    f32x16_t sc[QB];
-    uint4 va[4][2];
-    auto scores = [&](uint32_t kb) {
-        const uint8_t* st = lds + (kb & 1) * stage_bytes;
-        const uint32_t key0 = kb * block_keys;
-        const uint8_t* krow = st + n * k_row_bytes + g * 16;
-        uint4 ka[8];
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks)
-            ka[ks] = *reinterpret_cast<const uint4*>(krow + ks * 32);
+    // Software pipeline over key blocks, three LDS stages (block kb in stage
+    // kb % 3). Iteration kb issues S(kb) = K(kb) Q^T on the matrix core while
+    // the vector ALU turns S(kb-1) into probabilities, then P.V(kb-1) on the
+    // matrix core while the vector ALU masks S(kb) and takes its maxima and
+    // the next block is staged. The two halves of each iteration have no
+    // dependence between their matrix and vector work, so one wave keeps
+    // both units busy.
+    auto stage_of = [&](uint32_t kb) { return lds + (kb % 3) * stage_bytes; };
+    f32x16_t sc[QB];      // S^T(kb), written by the matrix core
+    f32x16_t sp[QB];      // S^T(kb - 1), its maxima taken, awaiting exponentials
+    float mx[QB];
+    auto qk = [&](uint32_t kb, const uint4 (&ka)[8]) {
 #pragma unroll
         for (int sb = 0; sb < QB; ++sb)
             sc[sb] = f32x16_t {};
@@ -306,13 +303,47 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
 #pragma unroll
             for (int sb = 0; sb < QB; ++sb)
                 sc[sb] = mfma<F16>(ka[ks], qr[sb][ks], sc[sb]);
-        const uint8_t* vt = st + k_bytes + g * 16;
+    };
+    auto read_k = [&](uint32_t kb, uint4 (&ka)[8]) {
+        const uint8_t* krow = stage_of(kb) + n * k_row_bytes + g * 16;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+            ka[ks] = *reinterpret_cast<const uint4*>(krow + ks * 32);
+    };
+    auto read_v = [&](uint32_t kb, uint4 (&va)[4][2]) {
+        const uint8_t* vt = stage_of(kb) + k_bytes + g * 16;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
                 va[mt][h] = *reinterpret_cast<const uint4*>(
                     vt + vt_row(32 * mt + n) * vt_row_bytes + h * 32);
+    };
+    auto probabilities = [&](uint4 (&pt)[QB][2]) {
+#pragma unroll
+        for (int sb = 0; sb < QB; ++sb) {
+            exponentiate(sp[sb], m[sb], l[sb], c);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                pt[sb][h] = make_uint4(pack2<F16>(sp[sb][8 * h + 0], sp[sb][8 * h + 1]),
+                                       pack2<F16>(sp[sb][8 * h + 2], sp[sb][8 * h + 3]),
+                                       pack2<F16>(sp[sb][8 * h + 4], sp[sb][8 * h + 5]),
+                                       pack2<F16>(sp[sb][8 * h + 6], sp[sb][8 * h + 7]));
+        }
+    };
+    auto pv = [&](const uint4 (&va)[4][2], const uint4 (&pt)[QB][2]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int sb = 0; sb < QB; ++sb)
+                    o[sb][mt] = mfma<F16>(va[mt][h], pt[sb][h], o[sb][mt]);
+    };
+    // causal mask and maxima of S(kb); moves it to sp; true when some lane's
+    // maximum grew past the rescale threshold (m = -inf before block 0)
+    auto stats = [&](uint32_t kb) {
+        const uint32_t key0 = kb * block_keys;
         if (key0 + block_keys - 1 > pos_lo) { // the causal diagonal crosses this block
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -323,59 +354,16 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
                         sc[sb][r] = -__builtin_inff();
             }
         }
-    };
-    // P = exp2 against the running maxima, O^T += V^T P^T, then stage the
-    // next block and synchronise.
-    auto finish = [&](uint32_t kb) {
+        bool grow = false;
 #pragma unroll
         for (int sb = 0; sb < QB; ++sb) {
-            exponentiate(sc[sb], m[sb], l[sb], c);
-            uint4 pt[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-                pt[h] = make_uint4(pack2<F16>(sc[sb][8 * h + 0], sc[sb][8 * h + 1]),
-                                   pack2<F16>(sc[sb][8 * h + 2], sc[sb][8 * h + 3]),
-                                   pack2<F16>(sc[sb][8 * h + 4], sc[sb][8 * h + 5]),
-                                   pack2<F16>(sc[sb][8 * h + 6], sc[sb][8 * h + 7]));
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int mt = 0; mt < 4; ++mt)
-                    o[sb][mt] = mfma<F16>(va[mt][h], pt[h], o[sb][mt]);
+            sp[sb] = sc[sb];
+            mx[sb] = block_max(sp[sb]);
+            grow = grow || (mx[sb] - m[sb]) * c > rescale_log2;
         }
-        if (kb + 1 < n_blocks)
-            store_block(lds + ((kb + 1) & 1) * stage_bytes);
-        __syncthreads();
+        return __any(grow);
     };
-
-    fetch_pages(0);
-    load_block(0);
-    store_block(lds);
-    __syncthreads();
-
-    // The hot loop never touches the accumulators outside the matrix
-    // products; a block whose maximum grows past the threshold leaves it,
-    // rescales, finishes and re-enters.
-    uint32_t kb = 0;
-    while (kb < n_blocks) {
-        float mx[QB];
-        for (; kb < n_blocks; ++kb) {
-            if (kb + 1 < n_blocks)
-                load_block(kb + 1);
-            scores(kb);
-            bool grow = false;
-#pragma unroll
-            for (int sb = 0; sb < QB; ++sb) {
-                mx[sb] = block_max(sc[sb]);
-                grow = grow || (mx[sb] - m[sb]) * c > rescale_log2;
-            }
-            // m = -inf before the first block, so it always leaves there
-            if (__any(grow))
-                break;
-            finish(kb);
-        }
-        if (kb == n_blocks)
-            break;
+    auto rescale = [&]() {
 #pragma unroll
         for (int sb = 0; sb < QB; ++sb) {
             const float m_new = fmaxf(m[sb], mx[sb]);
@@ -386,8 +374,58 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
             for (int mt = 0; mt < 4; ++mt)
                 o[sb][mt] *= alpha;
         }
-        finish(kb);
+    };
+
+    fetch_pages(0);
+    load_block(0);
+    store_block(stage_of(0));
+    __syncthreads();
+    // block 0: its scores and maxima (the first block always sets the maxima)
+    {
+        if (1 < n_blocks)
+            load_block(1);
+        uint4 ka[8];
+        read_k(0, ka);
+        qk(0, ka);
+        stats(0);
+        if (1 < n_blocks)
+            store_block(stage_of(1));
+        __syncthreads();
+        rescale();
+    }
+    // steady state: iteration kb finishes block kb - 1 and scores block kb
+    uint32_t kb = 1;
+    while (kb < n_blocks) {
+        bool grew = false;
+        for (; kb < n_blocks; ++kb) {
+            if (kb + 1 < n_blocks)
+                load_block(kb + 1);
+            uint4 ka[8], va[4][2];
+            uint4 pt[QB][2];
+            read_k(kb, ka);
+            probabilities(pt); // vector: block kb - 1
+            qk(kb, ka);        // matrix: block kb
+            read_v(kb - 1, va);
+            pv(va, pt);        // matrix: block kb - 1
+            grew = stats(kb);  // vector: block kb
+            if (kb + 1 < n_blocks)
+                store_block(stage_of(kb + 1));
+            __syncthreads();
+            if (grew)
+                break;
+        }
+        if (!grew)
+            break;
+        rescale(); // before block kb's probabilities are formed
         ++kb;
+    }
+    // the last block's probabilities and product
+    {
+        uint4 va[4][2];
+        uint4 pt[QB][2];
+        probabilities(pt);
+        read_v(n_blocks - 1, va);
+        pv(va, pt);
     }
 
     if (!active)

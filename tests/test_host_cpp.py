@@ -30,3 +30,22 @@ def test_host_layer_cpu():
 @pytest.mark.gpu
 def test_host_layer_gpu():
     _run("host_gpu_tests", 100)
+
+
+@pytest.mark.gpu
+def test_churn_driver_runs_a_short_trace():
+    """The config-5 driver end to end at a small size: the scheduler admits,
+    runs and retires sequences over the device KV path without errors."""
+    import json
+
+    path = os.path.join(BIN, "churn")
+    if not os.path.exists(path):
+        pytest.fail(f"{path} is not built: run __graft_entry__.build()")
+    proc = subprocess.run([path, "--steps", "300", "--pool-gb", "4", "--layers", "2",
+                           "--max-live", "64"], capture_output=True, text=True, timeout=100)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    trace = json.loads(proc.stdout.strip().splitlines()[-1])
+    assert trace["prefill_steps"] > 0 and trace["decode_steps"] > 0
+    assert trace["finished"] > 0 and trace["rejected"] == 0
+    assert trace["peak_live"] <= 64
+    assert trace["prefill_tokens"] + trace["decode_tokens"] > 0

@@ -58,6 +58,8 @@ _SIGNATURES = [
     ("ckv_append_decode", _i, [_vp, _sz, _vp, _vp, _vp, _sz, C.c_float, _vp, _sz]),
     ("ckv_prefill_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
     ("ckv_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
+    ("ckv_rope", _i, [_vp, _vp, _vp, _sz, C.c_float, _sz, _sz]),
+    ("ckv_rope_append", _i, [_vp, _sz, _vp, _vp, C.c_float, _sz, _sz]),
     ("ckv_copy_blocks", _i, [_vp, _u32p, _u32p, _sz]),
     ("ckv_checkpoint_pack", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
     ("ckv_checkpoint_unpack", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
@@ -255,6 +257,18 @@ class Pool:
 
     def attention(self, layer, queries, q_heads, scale, output, rows=None) -> None:
         self._attend(load().ckv_attention, layer, queries, q_heads, scale, output, rows)
+
+    def rope(self, inputs, outputs, heads: int, theta: float, rotary_dim: int = 0,
+             rows: Optional[int] = None) -> None:
+        rows = inputs.shape[0] if rows is None else rows
+        self.ctx.check(load().ckv_rope(self.handle, _ptr(inputs), _ptr(outputs), heads, theta,
+                                       rotary_dim, rows))
+
+    def rope_append(self, layer: int, keys, values, theta: float, rotary_dim: int = 0,
+                    rows: Optional[int] = None) -> None:
+        rows = keys.shape[0] if rows is None else rows
+        self.ctx.check(load().ckv_rope_append(self.handle, layer, _ptr(keys), _ptr(values),
+                                              theta, rotary_dim, rows))
 
     def copy_blocks(self, src, dst) -> None:
         s, d = _u32(src), _u32(dst)

@@ -6,6 +6,8 @@
 // host-to-device copy per call.
 #include "ckv_internal.h"
 
+#include <cmath>
+
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -889,6 +891,81 @@ int ckv_append(ckv_pool* pool, size_t layer, const void* keys, const void* value
     return run_kernel(ctx, "store_kv", [&] {
         return launch_store_kv(ctx->stream, view, pool->meta, (uint32_t)layer, keys, values,
                                (uint32_t)rows);
+    });
+}
+
+namespace {
+
+// Host checks of rope (src/tensor/tensor_ops.cc:375-399) after the row count;
+// fills the frequency table and the effective rotary width.
+int check_rope(ckv_pool* pool, size_t heads, float theta, size_t rotary_dim,
+               ckv::rope_table& freq, uint32_t& rotary)
+{
+    ckv_context* ctx = pool->ctx;
+    if (heads == 0)
+        return set_error(ctx, CKV_E_INVALID_HEAD_COUNT, "heads == 0");
+    const size_t head_dim = pool->head_dim;
+    if (rotary_dim == 0)
+        rotary_dim = head_dim;
+    if (head_dim % 2 != 0 || rotary_dim % 2 != 0 || rotary_dim > head_dim)
+        return set_error(ctx, CKV_E_INVALID_HEAD_DIMENSION,
+                         "head_dim and rotary_dim must be even, rotary_dim <= head_dim");
+    if (!std::isfinite(theta) || theta <= 0.0f)
+        return set_error(ctx, CKV_E_INVALID_ROPE_THETA, "theta must be positive and finite");
+    if ((uint64_t)heads * head_dim > UINT32_MAX)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "row too wide");
+    rotary = (uint32_t)rotary_dim;
+    ckv::rope_frequencies(theta, rotary, freq);
+    return CKV_OK;
+}
+
+} // namespace
+
+int ckv_rope(ckv_pool* pool, const void* input, void* output, size_t heads, float theta,
+             size_t rotary_dim, size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if (rows && (!input || !output))
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "input and output are required");
+    if (!pool->uploaded)
+        return set_error(ctx, CKV_E_NO_TABLES, "rope before ckv_tables_upload");
+    if (rows != pool->positions.size())
+        return set_error(ctx, CKV_E_POSITION_COUNT_MISMATCH, "rows != uploaded positions");
+    ckv::rope_table freq;
+    uint32_t rotary = 0;
+    if (const int status = check_rope(pool, heads, theta, rotary_dim, freq, rotary))
+        return status;
+    const pool_view view = view_of(pool);
+    return run_kernel(ctx, "rope", [&] {
+        return launch_rope(ctx->stream, view, pool->meta, input, output, (uint32_t)rows,
+                           (uint32_t)heads, rotary, freq);
+    });
+}
+
+int ckv_rope_append(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+                    float theta, size_t rotary_dim, size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if (rows && (!keys || !values))
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "keys and values are required");
+    if (!pool->uploaded || !pool->has_slots)
+        return set_error(ctx, CKV_E_NO_TABLES, "append before slots were uploaded");
+    if (rows != pool->slots.size())
+        return set_error(ctx, CKV_E_CACHE_SLOT_COUNT_MISMATCH, "rows != uploaded slots");
+    if (layer >= pool->layers)
+        return set_error(ctx, CKV_E_CACHE_LAYER_OUT_OF_RANGE, "layer >= layers");
+    ckv::rope_table freq;
+    uint32_t rotary = 0;
+    if (const int status = check_rope(pool, pool->kv_heads, theta, rotary_dim, freq, rotary))
+        return status;
+    const pool_view view = view_of(pool);
+    return run_kernel(ctx, "rope_append", [&] {
+        return launch_rope_append(ctx->stream, view, pool->meta, (uint32_t)layer, keys, values,
+                                  (uint32_t)rows, rotary, freq);
     });
 }
 

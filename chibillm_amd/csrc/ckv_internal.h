@@ -51,6 +51,13 @@ struct meta_view {
 // with G workgroups of 256/G rows for GQA group size G.
 constexpr uint32_t prefill_tile_rows = 256;
 
+// Inverse RoPE frequencies of one (theta, rotary width), by value as a kernel
+// argument; head_dim is at most 1024, so rotary/2 <= 512.
+constexpr uint32_t max_rope_pairs = 512;
+struct rope_table {
+    float inv_freq[max_rope_pairs];
+};
+
 struct pending_timing {
     const char* name;
     hipEvent_t start;
@@ -61,6 +68,18 @@ struct profile_total {
     double ms = 0.0;
     uint64_t launches = 0;
 };
+
+// ---- launchers (kernels_rope.hip) --------------------------------------------------
+// theta^(-2j/rotary) in float for j < rotary/2 (src/metal/metal_kernels.mm:186-191)
+void rope_frequencies(float theta, uint32_t rotary, rope_table& out);
+// rows of `heads` heads of the pool's head_dim and dtype, at the uploaded positions
+hipError_t launch_rope(hipStream_t s, const pool_view& p, const meta_view& m, const void* in,
+                       void* out, uint32_t rows, uint32_t heads, uint32_t rotary,
+                       const rope_table& freq);
+// rotated key rows and the value rows into the uploaded slots of `layer`
+hipError_t launch_rope_append(hipStream_t s, const pool_view& p, const meta_view& m,
+                              uint32_t layer, const void* keys, const void* values, uint32_t rows,
+                              uint32_t rotary, const rope_table& freq);
 
 } // namespace ckv
 
@@ -154,5 +173,17 @@ uint32_t partial_record_floats(uint32_t head_dim);
 bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, const void* out);
 hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                           const void* q, uint32_t q_heads, float scale, void* out);
+
+// ---- launchers (kernels_rope.hip) --------------------------------------------------
+// theta^(-2j/rotary) in float for j < rotary/2 (src/metal/metal_kernels.mm:186-191)
+void rope_frequencies(float theta, uint32_t rotary, rope_table& out);
+// rows of `heads` heads of the pool's head_dim and dtype, at the uploaded positions
+hipError_t launch_rope(hipStream_t s, const pool_view& p, const meta_view& m, const void* in,
+                       void* out, uint32_t rows, uint32_t heads, uint32_t rotary,
+                       const rope_table& freq);
+// rotated key rows and the value rows into the uploaded slots of `layer`
+hipError_t launch_rope_append(hipStream_t s, const pool_view& p, const meta_view& m,
+                              uint32_t layer, const void* keys, const void* values, uint32_t rows,
+                              uint32_t rotary, const rope_table& freq);
 
 } // namespace ckv

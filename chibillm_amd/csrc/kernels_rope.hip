@@ -1,0 +1,170 @@
+// Rotary position embedding over device rows, and its fusion with the KV
+// append.
+//
+// rope_f32 (src/metal/kernels/tensor_ops.metal:158-195): within each head of
+// a row at position p, pair j < rotary/2 rotates elements j and j + rotary/2
+// by the angle float(p) * inv_freq[j]; elements past the rotary width are
+// copied. inv_freq is theta^(-2j/rotary) in float, computed on the host as
+// src/metal/metal_kernels.mm:186-191 does. The angle is reduced by the
+// device library's sincosf (positions reach 10^4..10^5 radians).
+//
+// The fused form rotates the key rows and scatters them, with the value
+// rows, straight into their pages: the apply_rope + store_kv pair of
+// src/qwen/qwen_layer.cc:20-30, :43 without the rotated keys' round trip
+// through HBM. One thread per (row, head, pair) touches both elements of its
+// pair, so consecutive threads read and write consecutive elements.
+#include "ckv_internal.h"
+
+#include <cmath>
+
+namespace ckv {
+namespace {
+
+constexpr uint32_t block_threads = 256;
+
+template <int DT>
+struct element;
+
+template <>
+struct element<CKV_F32> {
+    using type = float;
+    static __device__ __forceinline__ float load(type v) { return v; }
+    static __device__ __forceinline__ type store(float v) { return v; }
+};
+
+template <>
+struct element<CKV_BF16> {
+    using type = uint16_t;
+    static __device__ __forceinline__ float load(type v)
+    {
+        return __builtin_bit_cast(float, static_cast<uint32_t>(v) << 16);
+    }
+    // round to nearest even, NaN quieted (src/tensor/types.h:60-75)
+    static __device__ __forceinline__ type store(float v)
+    {
+        uint32_t b = __builtin_bit_cast(uint32_t, v);
+        if ((b & 0x7FFFFFFFu) > 0x7F800000u)
+            return static_cast<type>((b >> 16) | 0x40u);
+        b += 0x7FFFu + ((b >> 16) & 1u);
+        return static_cast<type>(b >> 16);
+    }
+};
+
+template <>
+struct element<CKV_F16> {
+    using type = uint16_t;
+    static __device__ __forceinline__ float load(type v)
+    {
+        return static_cast<float>(__builtin_bit_cast(_Float16, v));
+    }
+    static __device__ __forceinline__ type store(float v)
+    {
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+    }
+};
+
+// Grid: x covers the row's (head, pair) threads, y strides over rows.
+// APPEND: `out` is ignored; rotated keys and the values go to the rows'
+// slots of `layer`.
+template <int DT, bool APPEND>
+__global__ __launch_bounds__(block_threads) void rope_kernel(
+    const void* in, void* out, uint32_t rows, uint32_t heads,
+    uint32_t head_dim, uint32_t rotary, rope_table freq, const uint32_t* __restrict__ positions,
+    pool_view p, const uint32_t* __restrict__ slots, uint32_t layer,
+    const void* __restrict__ values)
+{
+    using E = element<DT>;
+    using T = typename E::type;
+    const uint32_t half_dim = head_dim / 2, half = rotary / 2;
+    const uint32_t t = blockIdx.x * block_threads + threadIdx.x;
+    if (t >= heads * half_dim)
+        return;
+    const uint32_t head = t / half_dim, pair = t % half_dim;
+    const uint64_t width = (uint64_t)heads * head_dim;
+    // the pair's two elements within the head
+    const uint32_t a = pair < half ? pair : rotary + 2 * (pair - half);
+    const uint32_t b = pair < half ? pair + half : a + 1;
+    for (uint32_t row = blockIdx.y; row < rows; row += gridDim.y) {
+        const T* src = static_cast<const T*>(in) + row * width + head * head_dim;
+        float x1 = E::load(src[a]), x2 = E::load(src[b]);
+        if (pair < half) {
+            const float angle = static_cast<float>(positions[row]) * freq.inv_freq[pair];
+            float sine, cosine;
+            sincosf(angle, &sine, &cosine);
+            const float r1 = x1 * cosine - x2 * sine;
+            const float r2 = x2 * cosine + x1 * sine;
+            x1 = r1;
+            x2 = r2;
+        }
+        if constexpr (APPEND) {
+            const uint64_t dst = layer * p.layer_elems + (uint64_t)slots[row] * p.features
+                + head * head_dim;
+            T* kc = static_cast<T*>(p.keys) + dst;
+            T* vc = static_cast<T*>(p.values) + dst;
+            const T* vs = static_cast<const T*>(values) + row * width + head * head_dim;
+            kc[a] = E::store(x1);
+            kc[b] = E::store(x2);
+            vc[a] = vs[a];
+            vc[b] = vs[b];
+        } else {
+            T* dst = static_cast<T*>(out) + row * width + head * head_dim;
+            dst[a] = E::store(x1);
+            dst[b] = E::store(x2);
+        }
+    }
+}
+
+template <bool APPEND>
+hipError_t launch(hipStream_t s, int dtype, const void* in, void* out, uint32_t rows,
+                  uint32_t heads, uint32_t head_dim, uint32_t rotary, const rope_table& freq,
+                  const uint32_t* positions, const pool_view& p, const uint32_t* slots,
+                  uint32_t layer, const void* values)
+{
+    if (!rows)
+        return hipSuccess;
+    const uint32_t threads = heads * (head_dim / 2);
+    const dim3 grid((threads + block_threads - 1) / block_threads, rows < 65535 ? rows : 65535);
+    switch (dtype) {
+    case CKV_F32:
+        rope_kernel<CKV_F32, APPEND><<<grid, block_threads, 0, s>>>(
+            in, out, rows, heads, head_dim, rotary, freq, positions, p, slots, layer, values);
+        break;
+    case CKV_BF16:
+        rope_kernel<CKV_BF16, APPEND><<<grid, block_threads, 0, s>>>(
+            in, out, rows, heads, head_dim, rotary, freq, positions, p, slots, layer, values);
+        break;
+    default:
+        rope_kernel<CKV_F16, APPEND><<<grid, block_threads, 0, s>>>(
+            in, out, rows, heads, head_dim, rotary, freq, positions, p, slots, layer, values);
+        break;
+    }
+    return hipGetLastError();
+}
+
+} // namespace
+
+void rope_frequencies(float theta, uint32_t rotary, rope_table& out)
+{
+    for (uint32_t pair = 0; pair < rotary / 2; ++pair) {
+        const float exponent = -2.0f * static_cast<float>(pair) / static_cast<float>(rotary);
+        out.inv_freq[pair] = std::pow(theta, exponent);
+    }
+}
+
+hipError_t launch_rope(hipStream_t s, const pool_view& p, const meta_view& m, const void* in,
+                       void* out, uint32_t rows, uint32_t heads, uint32_t rotary,
+                       const rope_table& freq)
+{
+    return launch<false>(s, p.dtype, in, out, rows, heads, p.head_dim, rotary, freq,
+                         m.positions, p, nullptr, 0, nullptr);
+}
+
+hipError_t launch_rope_append(hipStream_t s, const pool_view& p, const meta_view& m,
+                              uint32_t layer, const void* keys, const void* values, uint32_t rows,
+                              uint32_t rotary, const rope_table& freq)
+{
+    return launch<true>(s, p.dtype, keys, nullptr, rows, p.kv_heads, p.head_dim, rotary, freq,
+                        m.positions, p, m.slots, layer, values);
+}
+
+} // namespace ckv

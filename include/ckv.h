@@ -58,6 +58,7 @@ enum ckv_status {
     CKV_E_POSITION_COUNT_MISMATCH = 114,
     CKV_E_INVALID_HEAD_COUNT = 115,
     CKV_E_INVALID_HEAD_DIMENSION = 116,
+    CKV_E_INVALID_ROPE_THETA = 117,
     CKV_E_CACHE_SLOT_COUNT_MISMATCH = 118,
     CKV_E_CACHE_FEATURE_COUNT_MISMATCH = 119,
     CKV_E_CACHE_LAYER_OUT_OF_RANGE = 120,
@@ -130,7 +131,7 @@ int ckv_copy_to_host(ckv_context* ctx, void* host_dst, const void* device_src, s
  * kernel's name. Query synchronises the stream. Names: "store_kv",
  * "gather_kv", "paged_attention_decode", "paged_attention_merge", "append_decode",
  * "paged_attention_prefill", "copy_blocks", "checkpoint_pack",
- * "checkpoint_unpack", "tables_patch". */
+ * "checkpoint_unpack", "tables_patch", "rope", "rope_append". */
 int ckv_profile_enable(ckv_context* ctx, int enabled);
 int ckv_profile_query(ckv_context* ctx, const char* kernel, double* total_ms,
                       uint64_t* launches);
@@ -225,6 +226,27 @@ int ckv_prefill_attention(ckv_pool* pool, size_t layer, const void* queries, siz
  * the prefill form when some query tile has more than one row, else decode. */
 int ckv_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
                   float scale, void* output, size_t rows);
+
+/* ---- Rotary position embedding ------------------------------------------------------ */
+/* rope (src/tensor/tensor_ops.cc:356-410; kernel rope_f32,
+ * src/metal/kernels/tensor_ops.metal:158-195) on device rows
+ * [rows, heads*head_dim] of the pool dtype and head_dim, each at its uploaded
+ * position: within every head, pair j < rotary_dim/2 rotates elements j and
+ * j + rotary_dim/2 by position * theta^(-2j/rotary_dim); the rest is copied.
+ * rotary_dim 0 means head_dim. input may equal output (in place). Checks, in
+ * the reference's order: position_count_mismatch (rows != uploaded rows),
+ * invalid_head_count, invalid_head_dimension (odd head_dim or rotary_dim, or
+ * rotary_dim > head_dim), invalid_rope_theta (not positive and finite). */
+int ckv_rope(ckv_pool* pool, const void* input, void* output, size_t heads, float theta,
+             size_t rotary_dim, size_t rows);
+/* rope of the key rows fused with ckv_append: the apply_rope + store_kv pair
+ * of src/qwen/qwen_layer.cc:20-30, :43 in one pass. keys/values are device
+ * [rows, kv_heads*head_dim] rows of the pool dtype; keys are read unrotated
+ * and are not modified; the rotated keys and the values land in the
+ * uploaded slots of `layer`. Checks: those of ckv_append, then those of
+ * ckv_rope. */
+int ckv_rope_append(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+                    float theta, size_t rotary_dim, size_t rows);
 
 /* ---- Pages: copy-on-write and checkpoints ------------------------------------------ */
 /* For every layer, keys and values: page dst[i] := page src[i]. The copy-on-write

@@ -722,6 +722,64 @@ void orc_copy_blocks(void* key_cache, void* value_cache, const orc_geometry* g,
     }
 }
 
+/* ---- Rotary position embedding ---------------------------------------------- */
+
+void orc_rope_frequencies(float theta, size_t rotary_dim, float* out)
+{
+    for (size_t pair = 0; pair < rotary_dim / 2; ++pair) {
+        const float exponent = -2.0f * (float)pair / (float)rotary_dim;
+        out[pair] = powf(theta, exponent);
+    }
+}
+
+int orc_rope(const void* in, void* out, int dtype, size_t rows, size_t heads, size_t head_dim,
+             const uint32_t* positions, float theta, size_t rotary_dim)
+{
+    if (rotary_dim == 0)
+        rotary_dim = head_dim;
+    if (head_dim % 2 || rotary_dim % 2 || rotary_dim > head_dim || !isfinite(theta)
+        || theta <= 0.0f)
+        return -1;
+    const size_t width = heads * head_dim;
+    float* x = malloc(rows * width * sizeof(float));
+    float* y = malloc(rows * width * sizeof(float));
+    float* freq = malloc((rotary_dim / 2 + 1) * sizeof(float));
+    if (!x || !y || !freq) {
+        free(x);
+        free(y);
+        free(freq);
+        return -1;
+    }
+    orc_convert_to_f32(in, x, rows * width, dtype);
+    orc_rope_frequencies(theta, rotary_dim, freq);
+    const size_t half = rotary_dim / 2;
+    for (size_t row = 0; row < rows; ++row) {
+        for (size_t head = 0; head < heads; ++head) {
+            const size_t base = row * width + head * head_dim;
+            for (size_t pair = 0; pair < head_dim / 2; ++pair) {
+                if (pair >= half) { /* the unrotated tail, two elements per pair */
+                    const size_t tail = base + rotary_dim + 2 * (pair - half);
+                    y[tail] = x[tail];
+                    y[tail + 1] = x[tail + 1];
+                    continue;
+                }
+                const float angle = (float)positions[row] * freq[pair];
+                const float cosine = cosf(angle);
+                const float sine = sinf(angle);
+                const float first = x[base + pair];
+                const float second = x[base + pair + half];
+                y[base + pair] = first * cosine - second * sine;
+                y[base + pair + half] = second * cosine + first * sine;
+            }
+        }
+    }
+    orc_convert_from_f32(y, out, rows * width, dtype);
+    free(x);
+    free(y);
+    free(freq);
+    return 0;
+}
+
 /* ---- Threaded CPU baseline -------------------------------------------------- */
 
 typedef struct {

@@ -97,6 +97,9 @@ def lib() -> C.CDLL:
                                       C.c_int]
         L.orc_copy_blocks.argtypes = [_vp, _vp, C.POINTER(Geometry), _u32p, _u32p, _size_t,
                                       _size_t]
+        L.orc_rope_frequencies.argtypes = [C.c_float, _size_t, _vp]
+        L.orc_rope.argtypes = [_vp, _vp, C.c_int, _size_t, _size_t, _size_t, _u32p, C.c_float,
+                               _size_t]
         _lib = L
     return _lib
 
@@ -246,6 +249,27 @@ def copy_blocks(key_cache, value_cache, geom: tuple, src, dst) -> None:
     g = Geometry(*geom)
     lib().orc_copy_blocks(key_cache.ctypes.data, value_cache.ctypes.data, C.byref(g), _p32(s),
                           _p32(d), s.size, key_cache.dtype.itemsize)
+
+
+# ---- rotary position embedding ---------------------------------------------------
+
+def rope_frequencies(theta: float, rotary_dim: int) -> np.ndarray:
+    out = np.empty(max(rotary_dim // 2, 1), dtype=np.float32)
+    lib().orc_rope_frequencies(theta, rotary_dim, out.ctypes.data)
+    return out[:rotary_dim // 2]
+
+
+def rope(rows_in: np.ndarray, dtype: int, heads: int, positions, theta: float,
+         rotary_dim: int = 0) -> np.ndarray:
+    """rope_f32 on [rows, heads*head_dim] rows of `dtype` (float32 or 16-bit bit patterns)."""
+    x = np.ascontiguousarray(rows_in)
+    rows, width = x.shape
+    out = np.empty_like(x)
+    p = _u32(positions)
+    if lib().orc_rope(x.ctypes.data, out.ctypes.data, dtype, rows, heads, width // heads,
+                      _p32(p), theta, rotary_dim):
+        raise ValueError("invalid rope arguments")
+    return out
 
 
 # ---- attention -------------------------------------------------------------------

@@ -451,3 +451,66 @@ def test_copy_blocks_duplicates_pages_bit_for_bit():
     assert np.array_equal(vc.reshape(3, 10, -1)[:, 7], v0.reshape(3, 10, -1)[:, 1])
     others = [b for b in range(10) if b not in (7, 2)]
     assert np.array_equal(kv[:, others], k0v[:, others])
+
+
+# ---- rotary position embedding ---------------------------------------------------------
+
+def test_rope_rotates_split_half_pairs_known_answer():
+    # tests/tensor_ops_test.cc:426-469: two heads of 4, positions {0, 1}, theta 1e4
+    x = np.tile(np.arange(1, 9, dtype=np.float32), (2, 1))
+    out = orc.rope(x, orc.F32, 2, [0, 1], 10000.0)
+    fc, fs, sc, ss = math.cos(1.0), math.sin(1.0), math.cos(0.01), math.sin(0.01)
+    expected = [1, 2, 3, 4, 5, 6, 7, 8,
+                1 * fc - 3 * fs, 2 * sc - 4 * ss, 3 * fc + 1 * fs, 4 * sc + 2 * ss,
+                5 * fc - 7 * fs, 6 * sc - 8 * ss, 7 * fc + 5 * fs, 8 * sc + 6 * ss]
+    assert approx(out.ravel(), expected, 1e-5)
+
+
+def test_partial_rope_rotates_only_the_prefix():
+    # tests/tensor_ops_test.cc:471-511: rotary widths 8 and 4 of 8-wide heads, theta 100
+    values = (np.arange(32, dtype=np.float32) - 8).reshape(2, 16)
+    for rotary in (8, 4, 8, 4):
+        expected = values.copy()
+        for row in range(2):
+            for head in range(2):
+                for pair in range(rotary // 2):
+                    a = head * 8 + pair
+                    b = a + rotary // 2
+                    angle = np.float32(1 + row * 2) * np.float32(100.0) ** np.float32(
+                        -2.0 * pair / rotary)
+                    expected[row, a] = values[row, a] * math.cos(angle) - values[row, b] * math.sin(angle)
+                    expected[row, b] = values[row, b] * math.cos(angle) + values[row, a] * math.sin(angle)
+        assert approx(orc.rope(values, orc.F32, 2, [1, 3], 100.0, rotary), expected, 1e-5)
+    for invalid in (3, 10):
+        with pytest.raises(ValueError):
+            orc.rope(values, orc.F32, 2, [1, 3], 100.0, invalid)
+    for theta in (0.0, -1.0, float("inf"), float("nan")):
+        with pytest.raises(ValueError):
+            orc.rope(values, orc.F32, 2, [1, 3], theta)
+
+
+def test_rope_frequencies_and_invariants():
+    # inverse frequencies theta^(-2p/rotary) in float (src/metal/metal_kernels.mm:186-191)
+    f = orc.rope_frequencies(1e6, 128)
+    assert f[0] == 1.0 and f.size == 64
+    assert np.allclose(f, 1e6 ** (-2.0 * np.arange(64) / 128), rtol=1e-6)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 4 * 128)).astype(np.float32)
+    # position 0 is the identity; every pair keeps its length; a rotation by
+    # p followed by the inverse angle returns the input
+    assert np.array_equal(orc.rope(x, orc.F32, 4, [0] * 5, 1e6), x)
+    pos = [1, 17, 300, 4096, 16383]
+    y = orc.rope(x, orc.F32, 4, pos, 1e6)
+    xr, yr = x.reshape(5, 4, 2, 64), y.reshape(5, 4, 2, 64)
+    assert np.allclose(np.hypot(xr[:, :, 0], xr[:, :, 1]), np.hypot(yr[:, :, 0], yr[:, :, 1]),
+                       rtol=1e-5, atol=1e-6)
+    angles = np.float32(np.array(pos, np.float32)[:, None]) * f[None, :]
+    c, s = np.cos(angles)[:, None, :], np.sin(angles)[:, None, :]
+    back0 = yr[:, :, 0] * c + yr[:, :, 1] * s
+    back1 = yr[:, :, 1] * c - yr[:, :, 0] * s
+    assert np.allclose(back0, xr[:, :, 0], atol=1e-4) and np.allclose(back1, xr[:, :, 1], atol=1e-4)
+    # 16-bit rows: rotate in float, round to nearest even (bf16 of the f32 result)
+    xb = orc.from_f32(x, orc.BF16)
+    yb = orc.rope(xb, orc.BF16, 4, pos, 1e6)
+    assert np.array_equal(yb, orc.from_f32(orc.rope(orc.to_f32(xb, orc.BF16), orc.F32, 4, pos,
+                                                    1e6), orc.BF16))

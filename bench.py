@@ -268,6 +268,7 @@ def bench_config3(args):
     return result
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
+ROPE_THETA = 1e6  # Qwen3-0.6B rope_theta
 PREFILL_SEQS, PREFILL_CHUNK = 64, 512
 
 
@@ -367,7 +368,11 @@ def bench_config4(args):
             pool.copy_blocks(cow_src, cow_dst)
         pool.upload(flat, offsets, lengths, positions, slots)
         for layer in range(LAYERS):
-            pool.append(layer, k_new[layer], v_new[layer])
+            if args.rope:
+                pool.rope(q[layer], q[layer], Q_HEADS, ROPE_THETA)
+                pool.rope_append(layer, k_new[layer], v_new[layer], ROPE_THETA)
+            else:
+                pool.append(layer, k_new[layer], v_new[layer])
             pool.prefill(layer, q[layer], Q_HEADS, scale, out[layer])
 
     for _ in range(args.warmup):
@@ -382,7 +387,7 @@ def bench_config4(args):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     kernels = {}
-    for name in ("paged_attention_prefill", "store_kv", "copy_blocks"):
+    for name in ("paged_attention_prefill", "store_kv", "copy_blocks", "rope", "rope_append"):
         ms, n = ctx.profile_query(name)
         kernels[name] = (ms, n)
     ctx.profile(False)
@@ -428,6 +433,15 @@ def bench_config4(args):
         },
         "cpu_baseline": None,
     }
+    if args.rope:
+        # the fused append's algorithmic bytes: key and value rows read, page
+        # rows written, positions and slots
+        ms, n = kernels["rope_append"]
+        per = rows * (4 * F * 2 + 8)
+        result["rope_append"] = {"avg_launch_us": round(ms / n * 1e3, 2),
+                                 "bytes_per_launch": per,
+                                 "achieved_gbs": round(per / (ms / n / 1e3) / 1e9, 2)}
+        result["config"]["workload"] += "; keys rotated inside the append, queries by ckv_rope"
     pool.close()
     del keys, values, q, k_new, v_new, out
     torch.cuda.empty_cache()
@@ -530,6 +544,9 @@ def main():
                     help="config3 (default): the headline decode step; config4: chunked "
                          "prefill of 64 sequences over a shared prefix (MFMA tiles); config5: "
                          "the continuous-batching churn trace (C++ scheduler driver)")
+    ap.add_argument("--rope", action="store_true",
+                    help="config4: rotate the chunk's keys inside the append (ckv_rope_append) "
+                         "and the queries in place (ckv_rope), Qwen3 theta 1e6")
     ap.add_argument("--prefix", type=int, default=2008,
                     help="config4 shared prefix tokens (2008 leaves a partial tail page, "
                          "so every sequence copies it on write; 2000 does not)")

@@ -107,11 +107,13 @@ def test_rope_validation_codes(ctx):
     pool.close()
 
 
-@pytest.mark.parametrize("code", [orc.BF16, orc.F16, orc.F32])
-def test_rope_append_matches_rope_then_store(ctx, code):
+@pytest.mark.parametrize("code,rotary", [(orc.BF16, 0), (orc.F16, 0), (orc.F32, 0),
+                                         (orc.BF16, 64)])
+def test_rope_append_matches_rope_then_store(ctx, code, rotary):
     """Qwen3-0.6B KV rows (8 heads x 128, theta 1e6) at positions up to 16 K,
-    scattered through a permuted table."""
-    print(f"rope_append dtype {code}", flush=True)
+    scattered through a permuted table; full width (the 128-bit path for
+    16-bit rows) and a partial rotary width (the per-pair path)."""
+    print(f"rope_append dtype {code} rotary {rotary}", flush=True)
     rng = orc.Mt64(17 + code)
     H, D, bs, B = 8, 128, 16, 96
     F = H * D
@@ -128,12 +130,12 @@ def test_rope_append_matches_rope_then_store(ctx, code):
     # (valid page ids, repeated) covers every position
     table = np.arange(1024) % B
     pool.upload(table, [0] * rows, [1024] * rows, positions, slots)
-    pool.rope_append(1, to_dev(k, code), to_dev(v, code), 1e6)
+    pool.rope_append(1, to_dev(k, code), to_dev(v, code), 1e6, rotary)
     ctx.sync()
     got_k, got_v = to_host(kd, code), to_host(vd, code)
 
     # oracle: rope the key rows, then store_kv
-    rk = orc.rope(k, code, H, positions, 1e6)
+    rk = orc.rope(k, code, H, positions, 1e6, rotary)
     kc = np.zeros_like(got_k)
     vc = np.zeros_like(got_v)
     orc.store_kv(kc, vc, rk, v, slots, 1, B * bs)
@@ -149,7 +151,7 @@ def test_rope_append_matches_rope_then_store(ctx, code):
     pool2, kd2, vd2 = new_pool(ctx, (2, B, bs, H, D), code, fill=0.0)
     pool2.upload(table, [0] * rows, [1024] * rows, positions, slots)
     kr = to_dev(k, code)
-    pool2.rope(kr, kr, H, 1e6)
+    pool2.rope(kr, kr, H, 1e6, rotary)
     pool2.append(1, kr, to_dev(v, code))
     ctx.sync()
     assert np.array_equal(to_host(kd2, code), got_k)
@@ -158,9 +160,9 @@ def test_rope_append_matches_rope_then_store(ctx, code):
     # queries: 16 heads through ckv_rope against the oracle
     qd = to_dev(q, code)
     qo = torch.empty_like(qd)
-    pool.rope(qd, qo, 16, 1e6)
+    pool.rope(qd, qo, 16, 1e6, rotary)
     ctx.sync()
-    rq = orc.rope(q, code, 16, positions, 1e6)
+    rq = orc.rope(q, code, 16, positions, 1e6, rotary)
     if code == orc.F32:
         assert_close(to_host(qo, code), rq, atol=1e-5, rtol=1e-5, what="rotated queries (f32)")
     else:

@@ -155,4 +155,38 @@ store_kv_and_attend(hip_kv_cache& cache, const device_tensor& keys, const device
     return {};
 }
 
+result<void, tensor_op_error>
+rope(hip_kv_cache& cache, const device_tensor& input, std::size_t head_count, float theta,
+     device_tensor& output, std::size_t rotary_dimension)
+{
+    const dtype t = cache_dtype(cache);
+    CL_TRY(validate_layouts({ { input, 2, t }, { output, 2, t } }));
+    if (output.dims != input.dims)
+        return fail(tensor_op_errc::output_shape_mismatch);
+    if (head_count && input.dims[1] != head_count * cache.head_dimension())
+        return fail(tensor_op_errc::invalid_head_dimension);
+    // position count, head count, rotary width and theta are checked by
+    // libckv; the output shape and feature count (which it cannot see) are
+    // checked here first, so when several are wrong at once the shape error
+    // wins where the reference would report the count
+    const int rc = ckv_rope(cache.pool(), input.data, output.data, head_count, theta,
+                            rotary_dimension, input.dims[0]);
+    if (rc)
+        return from_ckv(cache, rc);
+    return {};
+}
+
+result<void, tensor_op_error>
+store_kv_rotated(hip_kv_cache& cache, const device_tensor& keys, const device_tensor& values,
+                 std::size_t layer, float theta, std::size_t rotary_dimension)
+{
+    std::size_t rows = 0;
+    CL_TRY_ASSIGN(rows, validate_store(cache, keys, values, layer));
+    const int rc = ckv_rope_append(cache.pool(), layer, keys.data, values.data, theta,
+                                   rotary_dimension, rows);
+    if (rc)
+        return from_ckv(cache, rc);
+    return {};
+}
+
 } // namespace chibillm

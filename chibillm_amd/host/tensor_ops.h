@@ -113,4 +113,17 @@ result<void, tensor_op_error> store_kv_and_attend(hip_kv_cache& cache, const dev
                                                   std::size_t query_head_count,
                                                   device_tensor& output);
 
+// rope (src/tensor/tensor_ops.cc:356-410) on [rows, heads * head_dim] rows of
+// the cache dtype and head dimension at the uploaded positions; input may be
+// output. rotary_dimension 0 means the whole head.
+result<void, tensor_op_error> rope(hip_kv_cache& cache, const device_tensor& input,
+                                   std::size_t head_count, float theta, device_tensor& output,
+                                   std::size_t rotary_dimension = 0);
+
+// rope of the key rows fused into store_kv (ckv_rope_append): the
+// apply_rope + store_kv pair of src/qwen/qwen_layer.cc:20-30, :43.
+result<void, tensor_op_error> store_kv_rotated(hip_kv_cache& cache, const device_tensor& keys,
+                                               const device_tensor& values, std::size_t layer,
+                                               float theta, std::size_t rotary_dimension = 0);
+
 } // namespace chibillm

@@ -52,6 +52,9 @@ _SIGNATURES = [
     ("ckv_element_offset", _i, [_vp, _sz, _sz, _sz, _sz, _sz, C.POINTER(_sz)]),
     ("ckv_tables_upload", _i, [_vp, _u32p, _sz, _u32p, _u32p, _u32p, _u32p, _sz]),
     ("ckv_tables_patch", _i, [_vp, _u32p, _u32p, _sz]),
+    ("ckv_seq_tables_reserve", _i, [_vp, _sz, _sz]),
+    ("ckv_seq_tables_update", _i, [_vp, _u32p, _u32p, _u32p, _sz, _u32p, _u32p, _sz]),
+    ("ckv_batch_upload", _i, [_vp, _u32p, _u32p, _u32p, _sz, _i]),
     ("ckv_append", _i, [_vp, _sz, _vp, _vp, _sz]),
     ("ckv_gather", _i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp]),
     ("ckv_decode_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
@@ -228,6 +231,24 @@ class Pool:
     def patch(self, idx, val) -> None:
         i, v = _u32(idx), _u32(val)
         self.ctx.check(load().ckv_tables_patch(self.handle, _p(i), _p(v), i.size))
+
+    def reserve_sequences(self, max_sequences: int, pages_per_sequence: int) -> None:
+        """Device arena of per-sequence block tables (ckv_seq_tables_reserve)."""
+        self.ctx.check(load().ckv_seq_tables_reserve(self.handle, max_sequences,
+                                                     pages_per_sequence))
+
+    def update_sequences(self, seq=(), index=(), block=(), len_seq=(), length=()) -> None:
+        """entry (seq[i], index[i]) = block[i]; table length of len_seq[j] = length[j]."""
+        s, i, b, ls, ln = (_u32(seq), _u32(index), _u32(block), _u32(len_seq), _u32(length))
+        self.ctx.check(load().ckv_seq_tables_update(self.handle, _p(s), _p(i), _p(b), s.size,
+                                                    _p(ls), _p(ln), ls.size))
+
+    def upload_batch(self, seq, first_position, token_count, with_slots: bool = True) -> None:
+        """Batch of items (sequence, first position, token count) over the
+        sequence tables; rows are expanded on the device (ckv_batch_upload)."""
+        s, f, c = _u32(seq), _u32(first_position), _u32(token_count)
+        self.ctx.check(load().ckv_batch_upload(self.handle, _p(s), _p(f), _p(c), s.size,
+                                               1 if with_slots else 0))
 
     def append(self, layer: int, keys, values, rows: Optional[int] = None) -> None:
         rows = keys.shape[0] if rows is None else rows

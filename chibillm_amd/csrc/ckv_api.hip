@@ -85,40 +85,44 @@ int run_kernel(ckv_context* ctx, const char* name, Launch&& launch)
     return CKV_OK;
 }
 
-// Returns pinned staging memory of at least `bytes`, after the previous
-// upload from it has completed.
+// Returns pinned staging memory of at least `bytes`: the ring's next slot,
+// after the copy last made from it has completed. upload_staged copies from
+// this slot and advances the ring.
 int stage(ckv_context* ctx, size_t bytes, void** host)
 {
-    if (ctx->staging_pending) {
-        const hipError_t e = hipEventSynchronize(ctx->staging_done);
+    auto& slot = ctx->staging[ctx->staging_next];
+    if (slot.pending) {
+        const hipError_t e = hipEventSynchronize(slot.done);
         if (e != hipSuccess)
             return hip_error(ctx, e, "staging wait");
-        ctx->staging_pending = false;
+        slot.pending = false;
     }
-    if (bytes > ctx->pinned_bytes) {
-        if (ctx->pinned)
-            (void)hipHostFree(ctx->pinned);
-        ctx->pinned = nullptr;
-        ctx->pinned_bytes = 0;
+    if (bytes > slot.bytes) {
+        if (slot.pinned)
+            (void)hipHostFree(slot.pinned);
+        slot.pinned = nullptr;
+        slot.bytes = 0;
         const size_t size = std::max<size_t>(bytes, 1 << 20);
-        const hipError_t e = hipHostMalloc(&ctx->pinned, size, hipHostMallocDefault);
+        const hipError_t e = hipHostMalloc(&slot.pinned, size, hipHostMallocDefault);
         if (e != hipSuccess)
             return hip_error(ctx, e, "pinned staging allocation");
-        ctx->pinned_bytes = size;
+        slot.bytes = size;
     }
-    *host = ctx->pinned;
+    *host = slot.pinned;
     return CKV_OK;
 }
 
 int upload_staged(ckv_context* ctx, void* device, size_t bytes)
 {
-    hipError_t e = hipMemcpyAsync(device, ctx->pinned, bytes, hipMemcpyHostToDevice, ctx->stream);
+    auto& slot = ctx->staging[ctx->staging_next];
+    hipError_t e = hipMemcpyAsync(device, slot.pinned, bytes, hipMemcpyHostToDevice, ctx->stream);
     if (e != hipSuccess)
         return hip_error(ctx, e, "metadata upload");
-    e = hipEventRecord(ctx->staging_done, ctx->stream);
+    e = hipEventRecord(slot.done, ctx->stream);
     if (e != hipSuccess)
         return hip_error(ctx, e, "metadata upload event");
-    ctx->staging_pending = true;
+    slot.pending = true;
+    ctx->staging_next = (ctx->staging_next + 1) % ckv_context::staging_slots;
     return CKV_OK;
 }
 
@@ -128,13 +132,15 @@ int ensure_device(ckv_context* ctx, T** ptr, size_t* capacity, size_t needed, co
 {
     if (needed <= *capacity)
         return CKV_OK;
+    // grow by half again at least: a batch a little larger than the last
+    // must not reallocate (and drain the stream) every step
+    const size_t count = std::max({ needed, *capacity + *capacity / 2, (size_t)1024 });
     if (*ptr) {
         (void)hipStreamSynchronize(ctx->stream);
         (void)hipFree(*ptr);
         *ptr = nullptr;
         *capacity = 0;
     }
-    const size_t count = std::max(needed, (size_t)1024);
     const hipError_t e = hipMalloc(reinterpret_cast<void**>(ptr), count * sizeof(T));
     if (e != hipSuccess)
         return hip_error(ctx, e, what);
@@ -183,6 +189,119 @@ int check_attention(const ckv_pool* pool, size_t layer, const void* queries, siz
     return CKV_OK;
 }
 
+// Rows by decreasing position, ties in row order: the decode kernel
+// dispatches the longest work first. Sorted as 64-bit keys (inverted
+// position above the row), which needs no comparator indirection.
+void decode_order(const std::vector<uint32_t>& positions, std::vector<uint64_t>& keys,
+                  uint32_t* order)
+{
+    const size_t rows = positions.size();
+    keys.resize(rows);
+    for (size_t r = 0; r < rows; ++r)
+        keys[r] = ((uint64_t)(UINT32_MAX - positions[r]) << 32) | r;
+    std::sort(keys.begin(), keys.end());
+    for (size_t r = 0; r < rows; ++r)
+        order[r] = (uint32_t)keys[r];
+}
+
+// Whether keys[0..n) (each < bound) are distinct: a generation-stamped
+// table, cleared only when the generation counter wraps.
+bool all_distinct(ckv_pool* pool, const uint32_t* keys, size_t n, size_t bound)
+{
+    if (pool->stamp.size() < bound)
+        pool->stamp.assign(bound, 0);
+    if (++pool->stamp_generation == 0) {
+        std::fill(pool->stamp.begin(), pool->stamp.end(), 0);
+        pool->stamp_generation = 1;
+    }
+    const uint32_t g = pool->stamp_generation;
+    for (size_t i = 0; i < n; ++i) {
+        if (pool->stamp[keys[i]] == g)
+            return false;
+        pool->stamp[keys[i]] = g;
+    }
+    return true;
+}
+
+// The row order of a batch uploaded without it (one served by the prefill
+// kernel), at its first decode launch.
+int ensure_order(ckv_pool* pool)
+{
+    if (pool->order_ready)
+        return CKV_OK;
+    ckv_context* ctx = pool->ctx;
+    const size_t rows = pool->positions.size();
+    void* host = nullptr;
+    int status = stage(ctx, std::max<size_t>(rows, 4) * sizeof(uint32_t), &host);
+    if (status)
+        return status;
+    decode_order(pool->positions, pool->sort_keys, static_cast<uint32_t*>(host));
+    status = ensure_device(ctx, &pool->d_order, &pool->d_order_words, std::max<size_t>(rows, 4),
+                           "row order");
+    if (status)
+        return status;
+    status = upload_staged(ctx, pool->d_order, rows * sizeof(uint32_t));
+    if (status)
+        return status;
+    pool->meta.order = pool->d_order;
+    pool->order_ready = true;
+    return CKV_OK;
+}
+
+// The split-KV work list, at the batch's first split decode launch: each
+// row's range 0..position cut into chunks of `chunk` tokens, (row, chunk)
+// pairs, plus each row's first item and item count.
+int ensure_work(ckv_pool* pool)
+{
+    if (pool->work_ready)
+        return CKV_OK;
+    ckv_context* ctx = pool->ctx;
+    const std::vector<uint32_t>& positions = pool->positions;
+    const size_t rows = positions.size();
+    uint64_t token_heads = 0, n_items = 0;
+    for (const uint32_t p : positions)
+        token_heads += ((uint64_t)p + 1) * pool->kv_heads;
+    const uint32_t chunk = choose_chunk(token_heads, ctx->cu_count);
+    for (const uint32_t p : positions)
+        n_items += p / chunk + 1;
+    if (n_items > UINT32_MAX / pool->kv_heads)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "too many decode work items");
+    const size_t s_first = round4(2 * n_items);
+    const size_t s_count = s_first + round4(rows);
+    const size_t words = std::max<size_t>(s_count + rows, 4);
+    void* host = nullptr;
+    int status = stage(ctx, words * sizeof(uint32_t), &host);
+    if (status)
+        return status;
+    auto* w = static_cast<uint32_t*>(host);
+    bool multi = false;
+    for (size_t r = 0, item = 0; r < rows; ++r) {
+        const uint32_t n = positions[r] / chunk + 1;
+        w[s_first + r] = (uint32_t)item;
+        w[s_count + r] = n;
+        multi = multi || n > 1;
+        for (uint32_t c = 0; c < n; ++c, ++item) {
+            w[2 * item] = (uint32_t)r;
+            w[2 * item + 1] = c;
+        }
+    }
+    status = ensure_device(ctx, &pool->d_work, &pool->d_work_words, words, "decode work list");
+    if (status)
+        return status;
+    status = upload_staged(ctx, pool->d_work, words * sizeof(uint32_t));
+    if (status)
+        return status;
+    meta_view& m = pool->meta;
+    m.items = pool->d_work;
+    m.row_first = pool->d_work + s_first;
+    m.row_count = pool->d_work + s_count;
+    m.n_items = (uint32_t)n_items;
+    m.chunk = chunk;
+    pool->work_multi = multi;
+    pool->work_ready = true;
+    return CKV_OK;
+}
+
 int run_decode(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads, float scale,
                void* output)
 {
@@ -190,21 +309,22 @@ int run_decode(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads
     const pool_view view = view_of(pool);
     float* partials = nullptr;
     const bool fast = decode_fast_applies(view, (uint32_t)q_heads, queries, output);
-    const bool needs_merge = !fast
-        && std::any_of(pool->row_count.begin(), pool->row_count.end(),
-                       [](uint32_t c) { return c > 1; });
+    int status = fast ? ensure_order(pool) : ensure_work(pool);
+    if (status)
+        return status;
+    const bool needs_merge = !fast && pool->work_multi;
     if (needs_merge) {
         size_t capacity_floats = pool->d_partials_bytes / sizeof(float);
-        const size_t needed = (pool->items.size() / 2) * q_heads
+        const size_t needed = (size_t)pool->meta.n_items * q_heads
             * partial_record_floats((uint32_t)pool->head_dim);
-        int status = ensure_device(ctx, &pool->d_partials, &capacity_floats, needed,
-                                   "decode partials");
+        status = ensure_device(ctx, &pool->d_partials, &capacity_floats, needed,
+                               "decode partials");
         if (status)
             return status;
         pool->d_partials_bytes = capacity_floats * sizeof(float);
         partials = pool->d_partials;
     }
-    int status = run_kernel(ctx, "paged_attention_decode", [&] {
+    status = run_kernel(ctx, "paged_attention_decode", [&] {
         return launch_decode(ctx->stream, view, pool->meta, (uint32_t)layer, queries,
                              (uint32_t)q_heads, scale, output, partials, ctx->cu_count);
     });
@@ -452,9 +572,13 @@ int ckv_context_create(int device, ckv_context** out)
         e = hipGetDeviceProperties(&props, device);
     if (e == hipSuccess)
         e = hipStreamCreate(&ctx->own_stream);
-    if (e == hipSuccess)
-        e = hipEventCreateWithFlags(&ctx->staging_done, hipEventDisableTiming);
+    for (auto& slot : ctx->staging)
+        if (e == hipSuccess)
+            e = hipEventCreateWithFlags(&slot.done, hipEventDisableTiming);
     if (e != hipSuccess) {
+        for (auto& slot : ctx->staging)
+            if (slot.done)
+                (void)hipEventDestroy(slot.done);
         if (ctx->own_stream)
             (void)hipStreamDestroy(ctx->own_stream);
         delete ctx;
@@ -477,9 +601,11 @@ int ckv_context_destroy(ckv_context* ctx)
     }
     for (auto e : ctx->spare_events)
         (void)hipEventDestroy(e);
-    if (ctx->pinned)
-        (void)hipHostFree(ctx->pinned);
-    (void)hipEventDestroy(ctx->staging_done);
+    for (auto& slot : ctx->staging) {
+        if (slot.pinned)
+            (void)hipHostFree(slot.pinned);
+        (void)hipEventDestroy(slot.done);
+    }
     (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
     return CKV_OK;
@@ -644,6 +770,12 @@ int ckv_pool_destroy(ckv_pool* pool)
         (void)hipFree(pool->d_partials);
     if (pool->d_pairs)
         (void)hipFree(pool->d_pairs);
+    if (pool->d_seq)
+        (void)hipFree(pool->d_seq);
+    if (pool->d_order)
+        (void)hipFree(pool->d_order);
+    if (pool->d_work)
+        (void)hipFree(pool->d_work);
     delete pool;
     return CKV_OK;
 }
@@ -683,6 +815,34 @@ int ckv_element_offset(const ckv_pool* pool, size_t layer, size_t block, size_t 
     return CKV_OK;
 }
 
+namespace {
+
+// The host state of a batch just uploaded; the work list (and, unless it
+// was uploaded, the row order) are derived on first use.
+void adopt_batch(ckv_pool* pool, size_t rows, size_t n_entries, bool with_slots, bool shared,
+                 bool fusable, bool order_uploaded, bool device_tables)
+{
+    meta_view& m = pool->meta;
+    m.n_entries = (uint32_t)n_entries;
+    m.rows = (uint32_t)rows;
+    m.items = m.row_first = m.row_count = nullptr;
+    m.n_items = 0;
+    m.chunk = 0;
+    if (!order_uploaded)
+        m.order = nullptr;
+    pool->has_slots = with_slots;
+    pool->slot_rows = with_slots ? rows : 0;
+    pool->n_entries = n_entries;
+    pool->device_tables = device_tables;
+    pool->shared_tile = shared;
+    pool->fusable = fusable;
+    pool->order_ready = order_uploaded;
+    pool->work_ready = false;
+    pool->uploaded = true;
+}
+
+} // namespace
+
 int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entries,
                       const uint32_t* offsets, const uint32_t* lengths,
                       const uint32_t* positions, const uint32_t* slots, size_t rows)
@@ -715,26 +875,10 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
                 return set_error(ctx, CKV_E_CACHE_SLOT_OUT_OF_RANGE,
                                  "slot of row " + std::to_string(r));
 
-    // decode work list
-    uint64_t token_heads = 0;
-    for (size_t r = 0; r < rows; ++r)
-        token_heads += ((uint64_t)positions[r] + 1) * pool->kv_heads;
-    const uint32_t chunk = choose_chunk(token_heads, ctx->cu_count);
-    std::vector<uint32_t> items, row_first(rows), row_count(rows);
-    for (size_t r = 0; r < rows; ++r) {
-        const uint32_t n = positions[r] / chunk + 1;
-        row_first[r] = (uint32_t)(items.size() / 2);
-        row_count[r] = n;
-        for (uint32_t c = 0; c < n; ++c) {
-            items.push_back((uint32_t)r);
-            items.push_back(c);
-        }
-    }
-    if (items.size() / 2 > UINT32_MAX / pool->kv_heads)
-        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "too many decode work items");
     // query tiles: runs of consecutive positions sharing a table range
     // (src/tensor/attention.cc:142-167), up to prefill_tile_rows rows
-    std::vector<uint32_t> tiles;
+    std::vector<uint32_t>& tiles = pool->scratch;
+    tiles.clear();
     bool shared = false;
     for (size_t r = 0; r < rows;) {
         size_t n = 1;
@@ -750,41 +894,31 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     // append + decode can run as one launch when every row appends the token at
     // its own position and no two rows attend through the same table range
     bool fusable = slots != nullptr;
-    if (fusable) {
-        std::unordered_set<uint32_t> ranges;
-        for (size_t r = 0; r < rows && fusable; ++r) {
-            const uint64_t own = (uint64_t)block_table[offsets[r] + positions[r] / bs] * bs
-                + positions[r] % bs;
-            fusable = own == slots[r] && ranges.insert(offsets[r]).second;
-        }
+    for (size_t r = 0; r < rows && fusable; ++r) {
+        const uint64_t own = (uint64_t)block_table[offsets[r] + positions[r] / bs] * bs
+            + positions[r] % bs;
+        fusable = own == slots[r];
     }
+    fusable = fusable && all_distinct(pool, offsets, rows, n_entries + 1);
+    pool->positions.assign(positions, positions + rows);
+    // a batch of single-row tiles goes to the decode kernel: its row order
+    // goes up now
+    const bool with_order = !shared;
 
-    // rows by decreasing position: the decode kernel dispatches the longest work first
-    std::vector<uint32_t> order(rows);
-    for (size_t r = 0; r < rows; ++r)
-        order[r] = (uint32_t)r;
-    std::stable_sort(order.begin(), order.end(),
-                     [&](uint32_t a, uint32_t b) { return positions[a] > positions[b]; });
-
-    // pack: table | offsets | lengths | positions | slots | items | row_first | row_count |
-    // tiles | order
+    // pack: table | offsets | lengths | positions | slots | tiles | order
     const size_t s_table = 0;
     const size_t s_offsets = s_table + round4(n_entries);
     const size_t s_lengths = s_offsets + round4(rows);
     const size_t s_positions = s_lengths + round4(rows);
     const size_t s_slots = s_positions + round4(rows);
-    const size_t s_items = s_slots + round4(rows);
-    const size_t s_first = s_items + round4(items.size());
-    const size_t s_count = s_first + round4(rows);
-    const size_t s_tiles = s_count + round4(rows);
+    const size_t s_tiles = s_slots + round4(rows);
     const size_t s_order = s_tiles + round4(tiles.size());
-    const size_t words = s_order + round4(rows);
+    const size_t words = std::max<size_t>(s_order + (with_order ? rows : 0), 4);
     void* host = nullptr;
-    int status = stage(ctx, std::max<size_t>(words, 4) * sizeof(uint32_t), &host);
+    int status = stage(ctx, words * sizeof(uint32_t), &host);
     if (status)
         return status;
     auto* w = static_cast<uint32_t*>(host);
-    std::memset(w, 0, words * sizeof(uint32_t));
     auto put = [&](size_t at, const uint32_t* src, size_t n) {
         if (n)
             std::memcpy(w + at, src, n * sizeof(uint32_t));
@@ -795,13 +929,10 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     put(s_positions, positions, rows);
     if (slots)
         put(s_slots, slots, rows);
-    put(s_items, items.data(), items.size());
-    put(s_first, row_first.data(), rows);
-    put(s_count, row_count.data(), rows);
     put(s_tiles, tiles.data(), tiles.size());
-    put(s_order, order.data(), rows);
-    status = ensure_device(ctx, &pool->d_meta, &pool->d_meta_words, std::max<size_t>(words, 4),
-                           "metadata buffer");
+    if (with_order)
+        decode_order(pool->positions, pool->sort_keys, w + s_order);
+    status = ensure_device(ctx, &pool->d_meta, &pool->d_meta_words, words, "metadata buffer");
     if (status)
         return status;
     status = upload_staged(ctx, pool->d_meta, words * sizeof(uint32_t));
@@ -814,35 +945,10 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     m.lengths = pool->d_meta + s_lengths;
     m.positions = pool->d_meta + s_positions;
     m.slots = pool->d_meta + s_slots;
-    m.items = pool->d_meta + s_items;
-    m.row_first = pool->d_meta + s_first;
-    m.row_count = pool->d_meta + s_count;
     m.tiles = pool->d_meta + s_tiles;
     m.order = pool->d_meta + s_order;
-    m.n_entries = (uint32_t)n_entries;
-    m.rows = (uint32_t)rows;
-    m.n_items = (uint32_t)(items.size() / 2);
-    m.chunk = chunk;
     m.n_tiles = (uint32_t)(tiles.size() / 2);
-
-    pool->table.assign(block_table, block_table + n_entries);
-    pool->offsets.assign(offsets, offsets + rows);
-    pool->lengths.assign(lengths, lengths + rows);
-    pool->positions.assign(positions, positions + rows);
-    pool->has_slots = slots != nullptr;
-    if (slots)
-        pool->slots.assign(slots, slots + rows);
-    else
-        pool->slots.clear();
-    pool->items = std::move(items);
-    pool->row_first = std::move(row_first);
-    pool->row_count = std::move(row_count);
-    pool->tiles = std::move(tiles);
-    pool->order = std::move(order);
-    pool->chunk = chunk;
-    pool->shared_tile = shared;
-    pool->fusable = fusable;
-    pool->uploaded = true;
+    adopt_batch(pool, rows, n_entries, slots != nullptr, shared, fusable, with_order, false);
     return CKV_OK;
 }
 
@@ -857,8 +963,11 @@ int ckv_tables_patch(ckv_pool* pool, const uint32_t* idx, const uint32_t* val, s
         return set_error(ctx, CKV_E_INVALID_ARGUMENT, "patch arrays are required");
     if (!pool->uploaded)
         return set_error(ctx, CKV_E_NO_TABLES, "patch before ckv_tables_upload");
+    if (pool->device_tables)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT,
+                         "the batch indexes the sequence tables: use ckv_seq_tables_update");
     for (size_t i = 0; i < n; ++i) {
-        if (idx[i] >= pool->table.size())
+        if (idx[i] >= pool->n_entries)
             return set_error(ctx, CKV_E_BLOCK_TABLE_RANGE_OUT_OF_BOUNDS, "patch index");
         if (val[i] >= pool->blocks)
             return set_error(ctx, CKV_E_CACHE_BLOCK_OUT_OF_RANGE, "patch value");
@@ -866,12 +975,211 @@ int ckv_tables_patch(ckv_pool* pool, const uint32_t* idx, const uint32_t* val, s
     int status = stage_pairs(pool, idx, val, n);
     if (status)
         return status;
-    for (size_t i = 0; i < n; ++i)
-        pool->table[idx[i]] = val[i];
     uint32_t* table = pool->d_meta; // the table section starts the metadata block
     return run_kernel(ctx, "tables_patch", [&] {
         return launch_table_patch(ctx->stream, table, pool->d_pairs, (uint32_t)n);
     });
+}
+
+int ckv_seq_tables_reserve(ckv_pool* pool, size_t max_sequences, size_t pages_per_sequence)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if (!max_sequences || !pages_per_sequence
+        || (uint64_t)max_sequences * pages_per_sequence > UINT32_MAX)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "sequence table arena size");
+    const size_t words = max_sequences * pages_per_sequence;
+    int status = ensure_device(ctx, &pool->d_seq, &pool->d_seq_words, words, "sequence tables");
+    if (status)
+        return status;
+    // every entry starts as page 0: a valid page id, whatever a range reads
+    uint32_t* arena = pool->d_seq;
+    status = run_kernel(ctx, "tables_fill",
+                        [&] { return launch_fill(ctx->stream, arena, 0, (uint32_t)words); });
+    if (status)
+        return status;
+    pool->seq_max = max_sequences;
+    pool->seq_cap = pages_per_sequence;
+    pool->seq_len.assign(max_sequences, 0);
+    pool->seq_host.assign(words, 0);
+    pool->seq_dirty.assign(words, 0);
+    pool->dirty.clear();
+    if (pool->device_tables)
+        pool->uploaded = false; // the batch indexed the old arena
+    return CKV_OK;
+}
+
+int ckv_seq_tables_update(ckv_pool* pool, const uint32_t* seq, const uint32_t* index,
+                          const uint32_t* block, size_t n, const uint32_t* len_seq,
+                          const uint32_t* length, size_t m)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if ((n && (!seq || !index || !block)) || (m && (!len_seq || !length)))
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "update arrays are required");
+    if (!pool->d_seq)
+        return set_error(ctx, CKV_E_NO_TABLES, "update before ckv_seq_tables_reserve");
+    for (size_t i = 0; i < n; ++i) {
+        if (seq[i] >= pool->seq_max || index[i] >= pool->seq_cap)
+            return set_error(ctx, CKV_E_BLOCK_TABLE_RANGE_OUT_OF_BOUNDS,
+                             "entry " + std::to_string(i) + " outside the arena");
+        if (block[i] >= pool->blocks)
+            return set_error(ctx, CKV_E_CACHE_BLOCK_OUT_OF_RANGE,
+                             "entry " + std::to_string(i) + " page id");
+    }
+    for (size_t j = 0; j < m; ++j)
+        if (len_seq[j] >= pool->seq_max || length[j] > pool->seq_cap)
+            return set_error(ctx, CKV_E_BLOCK_TABLE_RANGE_OUT_OF_BOUNDS,
+                             "length " + std::to_string(j) + " outside the arena");
+    // pending until the next batch upload; a later write of an entry wins
+    for (size_t i = 0; i < n; ++i) {
+        const size_t at = (size_t)seq[i] * pool->seq_cap + index[i];
+        pool->seq_host[at] = block[i];
+        if (!pool->seq_dirty[at]) {
+            pool->seq_dirty[at] = 1;
+            pool->dirty.push_back((uint32_t)at);
+        }
+    }
+    for (size_t j = 0; j < m; ++j)
+        pool->seq_len[len_seq[j]] = length[j];
+    return CKV_OK;
+}
+
+int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_position,
+                     const uint32_t* token_count, size_t n_items, int with_slots)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if (n_items && (!seq || !first_position || !token_count))
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "item arrays are required");
+    if (!pool->d_seq)
+        return set_error(ctx, CKV_E_NO_TABLES, "batch upload before ckv_seq_tables_reserve");
+    const size_t bs = pool->block_size;
+    // rows, and the checks of prepared_attention_batch::make
+    // (src/tensor/attention.cc:110-137) against the sequences' table lengths
+    uint64_t rows = 0;
+    for (size_t i = 0; i < n_items; ++i) {
+        if (!token_count[i])
+            return set_error(ctx, CKV_E_INVALID_ARGUMENT, "item with no tokens");
+        const uint64_t last = (uint64_t)first_position[i] + token_count[i] - 1;
+        if (seq[i] >= pool->seq_max || last > UINT32_MAX
+            || last / bs >= pool->seq_len[seq[i]])
+            return set_error(ctx, CKV_E_BLOCK_TABLE_RANGE_OUT_OF_BOUNDS,
+                             "item " + std::to_string(i) + " table range");
+        rows += token_count[i];
+    }
+    if (rows > UINT32_MAX || n_items > UINT32_MAX)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "batch exceeds u32 counts");
+
+    // query tiles: items of one sequence at consecutive positions, up to
+    // prefill_tile_rows rows (the rule of src/tensor/attention.cc:142-167)
+    std::vector<uint32_t>& tiles = pool->scratch;
+    tiles.clear();
+    bool shared = false;
+    for (size_t i = 0, first_row = 0; i < n_items;) {
+        size_t end = i + 1, span = token_count[i]; // items [i, end) continue one another
+        while (end < n_items && seq[end] == seq[i]
+               && first_position[end] == first_position[end - 1] + token_count[end - 1])
+            span += token_count[end++];
+        for (size_t at = 0; at < span; at += prefill_tile_rows) {
+            const size_t n = std::min<size_t>(prefill_tile_rows, span - at);
+            tiles.push_back((uint32_t)(first_row + at));
+            tiles.push_back((uint32_t)n);
+            shared = shared || n > 1;
+        }
+        first_row += span;
+        i = end;
+    }
+    // one decode row per sequence at its own position's slot: fusable
+    bool fusable = with_slots != 0 && rows == n_items; // every item a single row
+    fusable = fusable && all_distinct(pool, seq, n_items, pool->seq_max);
+    std::vector<uint32_t>& positions = pool->positions;
+    positions.resize(rows);
+    for (size_t i = 0, r = 0; i < n_items; ++i)
+        for (uint32_t j = 0; j < token_count[i]; ++j)
+            positions[r++] = first_position[i] + j;
+    const bool with_order = !shared;
+
+    // d_meta: offsets | lengths | positions | slots (written by the expand
+    // kernel) | pending (index, block) pairs | items (5 sections) | tiles | order;
+    // the upload starts at the pairs
+    const size_t n_pairs = pool->dirty.size();
+    const size_t s_offsets = 0;
+    const size_t s_lengths = s_offsets + round4(rows);
+    const size_t s_positions = s_lengths + round4(rows);
+    const size_t s_slots = s_positions + round4(rows);
+    const size_t s_pairs = s_slots + round4(rows);
+    const size_t s_batch = s_pairs + round4(2 * n_pairs);
+    const size_t s_tiles = s_batch + round4(5 * n_items);
+    const size_t s_order = s_tiles + round4(tiles.size());
+    const size_t words = s_order + (with_order ? rows : 0);
+    const size_t up_words = std::max<size_t>(words - s_pairs, 4);
+    void* host = nullptr;
+    int status = stage(ctx, up_words * sizeof(uint32_t), &host);
+    if (status)
+        return status;
+    // staging holds d_meta[s_pairs, words)
+    const auto section = [&](size_t at) { return static_cast<uint32_t*>(host) + (at - s_pairs); };
+    uint32_t* pairs = section(s_pairs);
+    for (size_t k = 0; k < n_pairs; ++k) {
+        const uint32_t at = pool->dirty[k];
+        pairs[2 * k] = at;
+        pairs[2 * k + 1] = pool->seq_host[at];
+        pool->seq_dirty[at] = 0;
+    }
+    pool->dirty.clear();
+    uint32_t* b = section(s_batch);
+    for (size_t i = 0, r = 0; i < n_items; ++i) {
+        b[i] = seq[i];
+        b[n_items + i] = first_position[i];
+        b[2 * n_items + i] = token_count[i];
+        b[3 * n_items + i] = (uint32_t)r;
+        b[4 * n_items + i] = pool->seq_len[seq[i]];
+        r += token_count[i];
+    }
+    if (!tiles.empty())
+        std::memcpy(section(s_tiles), tiles.data(), tiles.size() * sizeof(uint32_t));
+    if (with_order)
+        decode_order(positions, pool->sort_keys, section(s_order));
+    status = ensure_device(ctx, &pool->d_meta, &pool->d_meta_words, s_pairs + up_words,
+                           "metadata buffer");
+    if (status)
+        return status;
+    uint32_t* d = pool->d_meta;
+    status = upload_staged(ctx, d + s_pairs, up_words * sizeof(uint32_t));
+    if (status)
+        return status;
+    uint32_t* arena = pool->d_seq;
+    if (n_pairs) {
+        status = run_kernel(ctx, "tables_patch", [&] {
+            return launch_table_patch(ctx->stream, arena, d + s_pairs, (uint32_t)n_pairs);
+        });
+        if (status)
+            return status;
+    }
+    status = run_kernel(ctx, "batch_expand", [&] {
+        return launch_expand_batch(ctx->stream, d + s_batch, (uint32_t)n_items, (uint32_t)rows,
+                                   arena, (uint32_t)pool->seq_cap, (uint32_t)bs, with_slots != 0,
+                                   d + s_offsets, d + s_lengths, d + s_positions, d + s_slots);
+    });
+    if (status)
+        return status;
+
+    meta_view& m = pool->meta;
+    m.table = arena;
+    m.offsets = d + s_offsets;
+    m.lengths = d + s_lengths;
+    m.positions = d + s_positions;
+    m.slots = d + s_slots;
+    m.tiles = d + s_tiles;
+    m.order = d + s_order;
+    m.n_tiles = (uint32_t)(tiles.size() / 2);
+    adopt_batch(pool, rows, pool->seq_max * pool->seq_cap, with_slots != 0, shared, fusable,
+                with_order, true);
+    return CKV_OK;
 }
 
 int ckv_append(ckv_pool* pool, size_t layer, const void* keys, const void* values, size_t rows)
@@ -883,7 +1191,7 @@ int ckv_append(ckv_pool* pool, size_t layer, const void* keys, const void* value
         return set_error(ctx, CKV_E_INVALID_ARGUMENT, "keys and values are required");
     if (!pool->uploaded || !pool->has_slots)
         return set_error(ctx, CKV_E_NO_TABLES, "append before slots were uploaded");
-    if (rows != pool->slots.size())
+    if (rows != pool->slot_rows)
         return set_error(ctx, CKV_E_CACHE_SLOT_COUNT_MISMATCH, "rows != uploaded slots");
     if (layer >= pool->layers)
         return set_error(ctx, CKV_E_CACHE_LAYER_OUT_OF_RANGE, "layer >= layers");
@@ -954,7 +1262,7 @@ int ckv_rope_append(ckv_pool* pool, size_t layer, const void* keys, const void* 
         return set_error(ctx, CKV_E_INVALID_ARGUMENT, "keys and values are required");
     if (!pool->uploaded || !pool->has_slots)
         return set_error(ctx, CKV_E_NO_TABLES, "append before slots were uploaded");
-    if (rows != pool->slots.size())
+    if (rows != pool->slot_rows)
         return set_error(ctx, CKV_E_CACHE_SLOT_COUNT_MISMATCH, "rows != uploaded slots");
     if (layer >= pool->layers)
         return set_error(ctx, CKV_E_CACHE_LAYER_OUT_OF_RANGE, "layer >= layers");
@@ -981,7 +1289,7 @@ int ckv_gather(ckv_pool* pool, size_t layer, size_t table_offset, size_t table_l
         return set_error(ctx, CKV_E_NO_TABLES, "gather before ckv_tables_upload");
     if (layer >= pool->layers)
         return set_error(ctx, CKV_E_CACHE_LAYER_OUT_OF_RANGE, "layer >= layers");
-    if (table_offset > pool->table.size() || table_length > pool->table.size() - table_offset
+    if (table_offset > pool->n_entries || table_length > pool->n_entries - table_offset
         || n_tokens > table_length * pool->block_size)
         return set_error(ctx, CKV_E_BLOCK_TABLE_RANGE_OUT_OF_BOUNDS, "gather range");
     const pool_view view = view_of(pool);
@@ -1013,7 +1321,7 @@ int ckv_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void
         return set_error(ctx, CKV_E_INVALID_ARGUMENT, "keys and values are required");
     if (!pool->uploaded || !pool->has_slots)
         return set_error(ctx, CKV_E_NO_TABLES, "append before slots were uploaded");
-    if (rows != pool->slots.size())
+    if (rows != pool->slot_rows)
         return set_error(ctx, CKV_E_CACHE_SLOT_COUNT_MISMATCH, "rows != uploaded slots");
     int status = check_attention(pool, layer, queries, q_heads, output, rows);
     if (status || !rows)
@@ -1022,6 +1330,9 @@ int ckv_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void
     const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     if (pool->fusable && decode_fast_applies(view, (uint32_t)q_heads, queries, output)
         && aligned(keys) && aligned(values)) {
+        status = ensure_order(pool);
+        if (status)
+            return status;
         return run_kernel(ctx, "append_decode", [&] {
             return launch_append_decode(ctx->stream, view, pool->meta, (uint32_t)layer, keys,
                                         values, queries, (uint32_t)q_heads, scale, output);

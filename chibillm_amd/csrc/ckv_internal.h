@@ -90,11 +90,18 @@ struct ckv_context {
     hipStream_t stream = nullptr;
     std::string last_error;
 
-    // pinned staging for metadata uploads; reused after staging_done completes
-    void* pinned = nullptr;
-    size_t pinned_bytes = 0;
-    hipEvent_t staging_done = nullptr;
-    bool staging_pending = false;
+    // pinned staging for metadata uploads: a ring of slots, each reused once
+    // the copy last made from it has completed, so the host can prepare the
+    // next uploads while earlier ones wait in the stream behind kernels
+    static constexpr int staging_slots = 4;
+    struct staging_slot {
+        void* pinned = nullptr;
+        size_t bytes = 0;
+        hipEvent_t done = nullptr;
+        bool pending = false;
+    };
+    staging_slot staging[staging_slots];
+    int staging_next = 0; // the slot stage() hands out
 
     bool profile = false;
     std::vector<ckv::pending_timing> pending;
@@ -112,19 +119,44 @@ struct ckv_pool {
     size_t bytes_each = 0;
     bool owned = false;
 
-    // host mirror of the uploaded metadata
+    // host state of the current batch
     bool uploaded = false;
     bool has_slots = false;
-    std::vector<uint32_t> table, offsets, lengths, positions, slots;
-    std::vector<uint32_t> items, row_first, row_count, tiles, order;
-    uint32_t chunk = 0;
+    size_t n_entries = 0; // entries of the table the rows index
+    size_t slot_rows = 0; // rows with an uploaded slot (0 without slots)
+    std::vector<uint32_t> positions;
     bool shared_tile = false;
     bool fusable = false; // slots are the rows' own positions, one row per table range
+    // derived when a decode launch first needs them: the longest-first row
+    // order (uploaded with the batch when the batch goes to the decode
+    // kernel anyway) and the split-KV work list
+    bool order_ready = false;
+    bool work_ready = false;
+    bool work_multi = false; // some row has more than one chunk: partials are merged
+    std::vector<uint32_t> scratch; // host staging of the derived arrays
+    std::vector<uint64_t> sort_keys;
+    std::vector<uint32_t> stamp; // distinctness checks (all_distinct)
+    uint32_t stamp_generation = 0;
 
     // device copies
     uint32_t* d_meta = nullptr;
     size_t d_meta_words = 0;
+    uint32_t* d_order = nullptr;
+    size_t d_order_words = 0;
+    uint32_t* d_work = nullptr;
+    size_t d_work_words = 0;
     ckv::meta_view meta {};
+
+    // device-resident sequence tables (ckv_seq_tables_*): seq_max rows of
+    // seq_cap page ids. The host keeps a mirror of the entries and the rows'
+    // lengths; entries written since the last batch upload are pending
+    // (listed once each in `dirty`) and go up with the next batch.
+    bool device_tables = false; // the current batch indexes the sequence tables
+    uint32_t* d_seq = nullptr;
+    size_t d_seq_words = 0;
+    size_t seq_max = 0, seq_cap = 0;
+    std::vector<uint32_t> seq_len, seq_host, dirty;
+    std::vector<uint8_t> seq_dirty;
 
     // device scratch
     float* d_partials = nullptr;
@@ -146,6 +178,16 @@ hipError_t launch_checkpoint(hipStream_t s, const pool_view& p, uint32_t layers,
                              const uint32_t* blocks, uint32_t tokens, void* packed_keys,
                              void* packed_values, bool unpack);
 hipError_t launch_table_patch(hipStream_t s, uint32_t* table, const uint32_t* pairs, uint32_t n);
+// dst[0..n) = value (a kernel, not hipMemsetAsync: callers may capture it)
+hipError_t launch_fill(hipStream_t s, uint32_t* dst, uint32_t value, uint32_t n);
+// Expands a batch given as items into per-row metadata. `items` holds five
+// sections of n_items words: sequence, first position, token count, first
+// row, table length. Rows get offset seq*cap, the item's length, position
+// first + j and (with_slots) slot seq_table[seq*cap + pos/bs]*bs + pos%bs.
+hipError_t launch_expand_batch(hipStream_t s, const uint32_t* items, uint32_t n_items,
+                               uint32_t rows, const uint32_t* seq_table, uint32_t cap,
+                               uint32_t block_size, bool with_slots, uint32_t* offsets,
+                               uint32_t* lengths, uint32_t* positions, uint32_t* slots);
 
 // ---- launchers (kernels_decode.hip) ------------------------------------------
 // Returns hipErrorInvalidValue when no kernel fits the geometry. The fast

@@ -125,6 +125,45 @@ __global__ __launch_bounds__(256) void table_patch_kernel(uint32_t* __restrict__
         table[pairs[2 * i]] = pairs[2 * i + 1];
 }
 
+__global__ __launch_bounds__(256) void fill_kernel(uint32_t* __restrict__ dst, uint32_t value,
+                                                   uint32_t n)
+{
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        dst[i] = value;
+}
+
+// One thread per row; the row's item is found by binary search over the
+// items' first rows (ascending).
+__global__ __launch_bounds__(256) void expand_batch_kernel(
+    const uint32_t* __restrict__ items, uint32_t n_items, uint32_t rows,
+    const uint32_t* __restrict__ seq_table, uint32_t cap, uint32_t block_size, bool with_slots,
+    uint32_t* __restrict__ offsets, uint32_t* __restrict__ lengths,
+    uint32_t* __restrict__ positions, uint32_t* __restrict__ slots)
+{
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows)
+        return;
+    const uint32_t* seq = items;
+    const uint32_t* first = items + n_items;
+    const uint32_t* row_start = items + 3 * n_items;
+    const uint32_t* length = items + 4 * n_items;
+    uint32_t lo = 0, hi = n_items - 1; // last item whose first row <= r
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1) / 2;
+        if (row_start[mid] <= r)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const uint32_t position = first[lo] + (r - row_start[lo]);
+    const uint32_t base = seq[lo] * cap;
+    offsets[r] = base;
+    lengths[r] = length[lo];
+    positions[r] = position;
+    if (with_slots)
+        slots[r] = seq_table[base + position / block_size] * block_size + position % block_size;
+}
+
 // Widest vector that divides the row and the given pointers' alignment.
 int vector_width(uint64_t bytes, std::initializer_list<const void*> pointers)
 {
@@ -243,6 +282,28 @@ hipError_t launch_table_patch(hipStream_t s, uint32_t* table, const uint32_t* pa
     if (!n)
         return hipSuccess;
     table_patch_kernel<<<(n + 255) / 256, 256, 0, s>>>(table, pairs, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill(hipStream_t s, uint32_t* dst, uint32_t value, uint32_t n)
+{
+    if (!n)
+        return hipSuccess;
+    const uint32_t blocks = std::min<uint32_t>((n + 255) / 256, 4096);
+    fill_kernel<<<blocks, 256, 0, s>>>(dst, value, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_expand_batch(hipStream_t s, const uint32_t* items, uint32_t n_items,
+                               uint32_t rows, const uint32_t* seq_table, uint32_t cap,
+                               uint32_t block_size, bool with_slots, uint32_t* offsets,
+                               uint32_t* lengths, uint32_t* positions, uint32_t* slots)
+{
+    if (!rows || !n_items)
+        return hipSuccess;
+    expand_batch_kernel<<<(rows + 255) / 256, 256, 0, s>>>(items, n_items, rows, seq_table, cap,
+                                                           block_size, with_slots, offsets,
+                                                           lengths, positions, slots);
     return hipGetLastError();
 }
 

@@ -37,6 +37,8 @@ struct options {
     std::size_t layers = 28, kv_heads = 8, q_heads = 16, head_dim = 128, block_size = 16;
     std::size_t max_batch_tokens = 2048, prefill_chunk = 512;
     bool profile = false;
+    bool device_tables = false; // sequence tables kept on the device (device_tables)
+    bool host_timing = false;   // drain the GPU before each step's metadata work and time it
 };
 
 // Seeded draws: std::mt19937_64 (fully specified) with explicit transforms.
@@ -87,6 +89,9 @@ struct totals {
     std::size_t prefill_rows = 0, decode_rows = 0;
     double kv_read_bytes = 0, append_bytes = 0, metadata_bytes = 0, qo_bytes = 0;
     double decode_bytes = 0; // the decode steps' share: K/V read, appends, Q and O
+    double h2d_bytes = 0;    // metadata sent over PCIe
+    double metadata_host_s = 0;
+    std::size_t timed_steps = 0;
 };
 
 // The model stand-in: runs the KV path of every layer for each batch.
@@ -108,6 +113,15 @@ public:
         if (!s)
             return fail(model_runner_errc::backend_failure, s.error(), "device KV pool");
         state_ = s->get();
+        if (opt_.device_tables) {
+            const std::size_t longest = opt_.prompt_max + opt_.output_max;
+            auto on = state_->enable_device_tables(config.max_sequences,
+                                                   (longest + config.kv_block_size - 1)
+                                                           / config.kv_block_size
+                                                       + 1);
+            if (!on)
+                return fail(model_runner_errc::backend_failure, on.error(), "device tables");
+        }
         return std::unique_ptr<model_state>(std::move(*s));
     }
 
@@ -133,16 +147,35 @@ public:
                                                               model_state&) override
     {
         auto& cache = state_->cache();
-        auto md = prepare_paged_batch(batch, info_.max_context_tokens, cache.block_count(),
-                                      cache.block_size());
-        if (!md)
-            return fail(model_runner_errc::inconsistent_batch, md.error());
         const std::size_t rows = batch.tokens.size();
-        positions_.assign(batch.positions.begin(), batch.positions.end());
-        auto up = upload_attention_metadata(cache, { positions_, md->slots, md->block_table,
-                                                     md->table_offsets, md->table_lengths });
-        if (!up)
-            return fail(model_runner_errc::backend_failure, up.error());
+        if (opt_.host_timing)
+            (void)ctx_.sync();
+        const auto t0 = std::chrono::steady_clock::now();
+        double h2d = 0;
+        if (auto* tables = state_->tables()) {
+            const std::size_t sent = tables->entries_sent();
+            auto up = tables->upload(batch, info_.max_context_tokens, true);
+            if (!up)
+                return fail(model_runner_errc::backend_failure, up.error());
+            // (seq, index, block) per changed entry, 5 words per item
+            h2d = 4.0 * (3.0 * (tables->entries_sent() - sent) + 5.0 * batch.items.size());
+        } else {
+            auto md = prepare_paged_batch(batch, info_.max_context_tokens, cache.block_count(),
+                                          cache.block_size());
+            if (!md)
+                return fail(model_runner_errc::inconsistent_batch, md.error());
+            positions_.assign(batch.positions.begin(), batch.positions.end());
+            auto up = upload_attention_metadata(cache, { positions_, md->slots, md->block_table,
+                                                         md->table_offsets, md->table_lengths });
+            if (!up)
+                return fail(model_runner_errc::backend_failure, up.error());
+            h2d = 4.0 * (md->block_table.size() + 4.0 * rows);
+        }
+        if (opt_.host_timing) {
+            totals_.metadata_host_s +=
+                std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+            ++totals_.timed_steps;
+        }
         const std::size_t F = opt_.kv_heads * opt_.head_dim, QF = opt_.q_heads * opt_.head_dim;
         const device_tensor k { k_.data(), dtype::bf16, { rows, F } };
         const device_tensor v { v_.data(), dtype::bf16, { rows, F } };
@@ -163,7 +196,7 @@ public:
                     return fail(model_runner_errc::backend_failure, attended.error());
             }
         }
-        account(batch, *md);
+        account(batch, h2d);
         return std::vector<token_id>(batch.sample_count(), 7);
     }
 
@@ -174,7 +207,7 @@ private:
     // Algorithmic bytes of one step, all layers: K+V of every attended token
     // (once per decode row; once per prefill tile, whose rows share it), the
     // appended rows, Q and O, and the uploaded metadata.
-    void account(const model_batch& batch, const paged_batch_metadata& md)
+    void account(const model_batch& batch, double h2d)
     {
         const double L = static_cast<double>(opt_.layers);
         const double row_kv = 2.0 * opt_.kv_heads * opt_.head_dim * 2.0;
@@ -192,7 +225,9 @@ private:
         totals_.kv_read_bytes += kv;
         totals_.append_bytes += append;
         totals_.qo_bytes += qo;
-        totals_.metadata_bytes += 4.0 * (md.block_table.size() + 4.0 * rows);
+        // the per-row metadata the kernels read (offset, length, position, slot)
+        totals_.metadata_bytes += h2d + 16.0 * rows;
+        totals_.h2d_bytes += h2d;
         if (batch.phase == batch_phase::decode) {
             totals_.decode_bytes += kv + append + qo;
             ++totals_.decode_steps;
@@ -221,6 +256,14 @@ parse(int argc, char** argv, options& o)
         const char* v = nullptr;
         if (a == "--profile") {
             o.profile = true;
+            continue;
+        }
+        if (a == "--device-tables") {
+            o.device_tables = true;
+            continue;
+        }
+        if (a == "--host-timing") {
+            o.host_timing = true;
             continue;
         }
         if (!(v = next()))
@@ -259,7 +302,8 @@ main(int argc, char** argv)
         std::fprintf(stderr,
                      "usage: churn [--steps N] [--seed S] [--pool-gb G] [--max-live N] "
                      "[--arrival-mean M] [--layers L] [--max-batch-tokens T] "
-                     "[--prefill-chunk C] [--sigma S] [--profile]\n");
+                     "[--prefill-chunk C] [--sigma S] [--profile] [--device-tables] "
+                     "[--host-timing]\n");
         return 2;
     }
     auto ctx = hip_context::make(0);
@@ -370,12 +414,18 @@ main(int argc, char** argv)
                 "\"hbm_frac\": %.4f, \"kv_read_bytes\": %.6e, \"append_bytes\": %.6e, "
                 "\"decode_step_bytes\": %.6e, "
                 "\"arrived\": %zu, \"admitted\": %zu, \"finished\": %zu, \"rejected\": %zu, "
-                "\"pending_at_end\": %zu, \"peak_live\": %zu, \"pool_pages\": %zu",
+                "\"pending_at_end\": %zu, \"peak_live\": %zu, \"pool_pages\": %zu, "
+                "\"device_tables\": %s, \"h2d_bytes_per_step\": %.1f",
                 opt.steps, seconds, opt.steps / seconds, rows / seconds, t.prefill_rows,
                 t.decode_rows, t.prefill_steps, t.decode_steps, bytes, bytes / seconds / 1e9,
                 bytes / seconds / 8e12, t.kv_read_bytes, t.append_bytes, t.decode_bytes, arrived,
                 admitted,
-                finished, rejected, pending.size(), peak_live, config.kv_block_count);
+                finished, rejected, pending.size(), peak_live, config.kv_block_count,
+                opt.device_tables ? "true" : "false",
+                t.h2d_bytes / std::max<std::size_t>(1, t.prefill_steps + t.decode_steps));
+    if (opt.host_timing)
+        std::printf(", \"metadata_host_us_per_step\": %.2f",
+                    1e6 * t.metadata_host_s / std::max<std::size_t>(1, t.timed_steps));
     if (opt.profile) {
         std::printf(", \"kernels_ms\": {");
         const char* names[] = { "append_decode", "paged_attention_decode", "paged_attention_merge",

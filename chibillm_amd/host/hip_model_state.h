@@ -17,6 +17,7 @@
 
 #include "block_manager.h"
 #include "hip_kv_cache.h"
+#include "tensor_ops.h"
 
 namespace chibillm {
 
@@ -52,7 +53,12 @@ public:
     {
         return pages_->reserve(id, tokens);
     }
-    void release(seq_id id) noexcept override { pages_->release(id); }
+    void release(seq_id id) noexcept override
+    {
+        pages_->release(id);
+        if (tables_)
+            tables_->release(id);
+    }
     std::size_t block_size() const noexcept override { return pages_->block_size(); }
     sequence_resources resources(seq_id id) const noexcept override
     {
@@ -63,6 +69,19 @@ public:
     result<std::unique_ptr<model_checkpoint>, state_error> checkpoint(seq_id id,
                                                                       std::size_t tokens) const override;
     result<void, state_error> restore(seq_id id, const model_checkpoint& saved) override;
+
+    // Keeps the sequences' block tables on the device (device_tables); the
+    // rows of released sequences are returned to it.
+    result<void, tensor_op_error> enable_device_tables(std::size_t max_sequences,
+                                                       std::size_t pages_per_sequence)
+    {
+        auto made = device_tables::make(cache_, max_sequences, pages_per_sequence);
+        if (!made)
+            return fail(made.error());
+        tables_ = std::make_unique<device_tables>(std::move(*made));
+        return {};
+    }
+    device_tables* tables() noexcept { return tables_.get(); }
 
     hip_kv_cache& cache() noexcept { return cache_; }
     const hip_kv_cache& cache() const noexcept { return cache_; }
@@ -84,6 +103,7 @@ private:
     hip_kv_cache cache_;
     prefix_sharing sharing_;
     std::size_t cow_copies_ = 0;
+    std::unique_ptr<device_tables> tables_;
 };
 
 } // namespace chibillm

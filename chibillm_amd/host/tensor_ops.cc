@@ -1,7 +1,10 @@
 #include "tensor_ops.h"
 
 #include <cmath>
+#include <cstring>
 #include <initializer_list>
+
+#include "model_batch.h"
 
 namespace chibillm {
 
@@ -109,6 +112,132 @@ upload_attention_metadata(hip_kv_cache& cache, attention_metadata md)
                                      md.slots.empty() ? nullptr : md.slots.data(), rows);
     if (rc)
         return from_ckv(cache, rc);
+    return {};
+}
+
+device_tables::device_tables(hip_kv_cache& cache, std::size_t max_sequences, std::size_t cap)
+    : cache_(&cache)
+    , cap_(cap)
+    , sent_(max_sequences)
+{
+    free_rows_.reserve(max_sequences);
+    for (std::size_t r = max_sequences; r-- > 0;)
+        free_rows_.push_back(static_cast<std::uint32_t>(r));
+}
+
+result<device_tables, tensor_op_error>
+device_tables::make(hip_kv_cache& cache, std::size_t max_sequences, std::size_t pages_per_sequence)
+{
+    const int rc = ckv_seq_tables_reserve(cache.pool(), max_sequences, pages_per_sequence);
+    if (rc)
+        return from_ckv(cache, rc);
+    return device_tables(cache, max_sequences, pages_per_sequence);
+}
+
+void
+device_tables::release(seq_id id) noexcept
+{
+    const auto it = row_of_.find(id);
+    if (it == row_of_.end())
+        return;
+    // the row's entries stay on the device and are overwritten by its next owner
+    sent_[it->second].clear();
+    free_rows_.push_back(it->second);
+    row_of_.erase(it);
+}
+
+result<void, tensor_op_error>
+device_tables::upload(const model_batch& batch, std::size_t max_positions, bool with_slots)
+{
+    const std::size_t bs = cache_->block_size();
+    seq_.clear();
+    index_.clear();
+    block_.clear();
+    len_seq_.clear();
+    length_.clear();
+    item_row_.clear();
+    item_first_.clear();
+    item_count_.clear();
+    // the shape checks of prepare_paged_batch (src/model_batch.cc:148-185),
+    // on items: rows covered in order, consecutive positions, each position
+    // inside its item's table
+    std::size_t expected = 0;
+    for (const auto& item : batch.items) {
+        if (!item.token_count || item.token_offset != expected
+            || item.token_count > batch.positions.size() - expected)
+            return fail(tensor_op_errc::position_count_mismatch);
+        const std::uint32_t first = batch.positions[item.token_offset];
+        for (std::size_t j = 1; j < item.token_count; ++j)
+            if (batch.positions[item.token_offset + j] != first + j)
+                return fail(tensor_op_errc::position_count_mismatch);
+        const std::size_t last = static_cast<std::size_t>(first) + item.token_count - 1;
+        if (last >= max_positions || last / bs >= item.block_table.size()
+            || item.block_table.size() > cap_)
+            return fail(tensor_op_errc::block_table_range_out_of_bounds);
+        expected += item.token_count;
+    }
+    if (expected != batch.positions.size())
+        return fail(tensor_op_errc::position_count_mismatch);
+
+    // rows for new sequences, then the table deltas
+    std::vector<seq_id> taken; // rows given out by this call, returned on failure
+    auto undo = [&] {
+        for (const seq_id id : taken)
+            release(id);
+    };
+    for (const auto& item : batch.items) {
+        auto it = row_of_.find(item.id);
+        if (it == row_of_.end()) {
+            if (free_rows_.empty()) {
+                undo();
+                return fail(tensor_op_errc::block_table_range_out_of_bounds);
+            }
+            it = row_of_.emplace(item.id, free_rows_.back()).first;
+            free_rows_.pop_back();
+            taken.push_back(item.id);
+        }
+        const std::uint32_t row = it->second;
+        const auto& table = item.block_table;
+        const auto& sent = sent_[row];
+        // tables mostly grow at the end: compare the common part in one pass
+        const std::size_t common = std::min(sent.size(), table.size());
+        std::size_t i = 0;
+        if (common
+            && std::memcmp(sent.data(), table.data(), common * sizeof(block_id)) == 0)
+            i = common;
+        for (; i < table.size(); ++i)
+            if (i >= sent.size() || sent[i] != table[i]) {
+                seq_.push_back(row);
+                index_.push_back(static_cast<std::uint32_t>(i));
+                block_.push_back(table[i]);
+            }
+        if (table.size() != sent.size()) {
+            len_seq_.push_back(row);
+            length_.push_back(static_cast<std::uint32_t>(table.size()));
+        }
+        item_row_.push_back(row);
+        item_first_.push_back(batch.positions[item.token_offset]);
+        item_count_.push_back(static_cast<std::uint32_t>(item.token_count));
+    }
+    int rc = ckv_seq_tables_update(cache_->pool(), seq_.data(), index_.data(), block_.data(),
+                                   seq_.size(), len_seq_.data(), length_.data(), len_seq_.size());
+    if (rc) {
+        undo();
+        return from_ckv(*cache_, rc);
+    }
+    entries_sent_ += seq_.size();
+    for (std::size_t k = 0; k < seq_.size(); ++k) { // the mirror takes the sent entries
+        auto& sent = sent_[seq_[k]];
+        if (index_[k] >= sent.size())
+            sent.resize(index_[k] + 1);
+        sent[index_[k]] = block_[k];
+    }
+    for (std::size_t k = 0; k < len_seq_.size(); ++k)
+        sent_[len_seq_[k]].resize(length_[k]);
+    rc = ckv_batch_upload(cache_->pool(), item_row_.data(), item_first_.data(),
+                          item_count_.data(), item_row_.size(), with_slots ? 1 : 0);
+    if (rc)
+        return from_ckv(*cache_, rc);
     return {};
 }
 

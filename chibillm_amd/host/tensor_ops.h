@@ -7,6 +7,7 @@
 
 #include <cstdint>
 #include <span>
+#include <unordered_map>
 #include <vector>
 
 #include "hip_kv_cache.h"
@@ -92,6 +93,50 @@ struct attention_metadata {
 // Validates on the host and uploads (src/tensor/attention.cc:8-29, :110-137).
 result<void, tensor_op_error> upload_attention_metadata(hip_kv_cache& cache,
                                                         attention_metadata metadata);
+
+struct model_batch;
+
+// prepare_paged_batch + upload_attention_metadata with the tables kept on the
+// device (src/model_batch.cc:127-204, src/tensor/attention.cc:8-29): every
+// live sequence owns a row of the pool's sequence-table arena, upload() sends
+// only the table entries that changed since the sequence's previous batch and
+// one (sequence row, first position, token count) triple per item, and the
+// device expands the per-row offsets, lengths, positions and slots. The
+// result is the metadata prepare_paged_batch would upload for the same batch.
+class device_tables {
+public:
+    static result<device_tables, tensor_op_error> make(hip_kv_cache& cache,
+                                                       std::size_t max_sequences,
+                                                       std::size_t pages_per_sequence);
+
+    // The batch's items must cover its rows in order with consecutive
+    // positions (as the scheduler builds them); positions must stay below
+    // max_positions. Errors: position_count_mismatch (rows not covered or
+    // not consecutive), block_table_range_out_of_bounds (a position past the
+    // item's table, max_positions, a table longer than pages_per_sequence or
+    // more live sequences than max_sequences), cache_block_out_of_range.
+    result<void, tensor_op_error> upload(const model_batch& batch, std::size_t max_positions,
+                                         bool with_slots);
+    // Frees the sequence's row (model_state::release). Unknown ids are harmless.
+    void release(seq_id id) noexcept;
+
+    std::size_t live_sequences() const noexcept { return row_of_.size(); }
+    // Table entries sent to the device so far (the deltas).
+    std::size_t entries_sent() const noexcept { return entries_sent_; }
+
+private:
+    device_tables(hip_kv_cache& cache, std::size_t max_sequences, std::size_t cap);
+
+    hip_kv_cache* cache_;
+    std::size_t cap_;
+    std::unordered_map<seq_id, std::uint32_t> row_of_;
+    std::vector<std::uint32_t> free_rows_;
+    std::vector<std::vector<block_id>> sent_; // per row: the table the device holds
+    std::size_t entries_sent_ = 0;
+    // per-upload staging, kept to avoid reallocation
+    std::vector<std::uint32_t> seq_, index_, block_, len_seq_, length_;
+    std::vector<std::uint32_t> item_row_, item_first_, item_count_;
+};
 
 // keys/values: [rows, kv_heads * head_dim] of the cache dtype (src/tensor/tensor_ops.cc:412-463).
 result<void, tensor_op_error> store_kv(hip_kv_cache& cache, const device_tensor& keys,

@@ -131,7 +131,8 @@ int ckv_copy_to_host(ckv_context* ctx, void* host_dst, const void* device_src, s
  * kernel's name. Query synchronises the stream. Names: "store_kv",
  * "gather_kv", "paged_attention_decode", "paged_attention_merge", "append_decode",
  * "paged_attention_prefill", "copy_blocks", "checkpoint_pack",
- * "checkpoint_unpack", "tables_patch", "rope", "rope_append". */
+ * "checkpoint_unpack", "tables_patch", "tables_fill", "batch_expand", "rope",
+ * "rope_append". */
 int ckv_profile_enable(ckv_context* ctx, int enabled);
 int ckv_profile_query(ckv_context* ctx, const char* kernel, double* total_ms,
                       uint64_t* launches);
@@ -167,9 +168,11 @@ int ckv_element_offset(const ckv_pool* pool, size_t layer, size_t block, size_t 
  *   cache_block_out_of_range         a table entry >= blocks
  *   cache_slot_out_of_range          a slot >= blocks*block_size
  * slots may be NULL when no append follows. The query tiles of
- * prepared_attention_batch::make (src/tensor/attention.cc:142-167) and the
- * split-KV decode work list are derived here, once per batch, and reused by
- * every layer. */
+ * prepared_attention_batch::make (src/tensor/attention.cc:142-167) are derived
+ * here, once per batch, and reused by every layer; so is the decode kernel's
+ * row order when every tile is a single row. The split-KV decode work list
+ * (and the row order of other batches) are derived and uploaded by the
+ * batch's first decode launch that needs them. */
 int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entries,
                       const uint32_t* offsets, const uint32_t* lengths,
                       const uint32_t* positions, const uint32_t* slots, size_t rows);
@@ -179,6 +182,51 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
  * (block_table_range_out_of_bounds) and every val < blocks
  * (cache_block_out_of_range). */
 int ckv_tables_patch(ckv_pool* pool, const uint32_t* idx, const uint32_t* val, size_t n);
+
+/* ---- Device-resident sequence tables (prepare_paged_batch on the device) ----
+ * The alternative to ckv_tables_upload for a serving loop: every live
+ * sequence's block table stays in a device arena of max_sequences rows of
+ * pages_per_sequence entries (entry (s, i) at s*pages_per_sequence + i), and
+ * only its changes cross PCIe. A batch is then given per item (sequence,
+ * first position, token count) and its per-row offsets, lengths, positions
+ * and slots are expanded on the device: the loop of prepare_paged_batch
+ * (src/model_batch.cc:127-204) that concatenates each item's block table
+ * and computes slot = table[position / block_size] * block_size +
+ * position % block_size for every row. */
+
+/* Allocates the arena (kept until the pool is destroyed; a second call
+ * resizes it) and sets every entry to page 0 and every table length to 0.
+ * A batch uploaded from the previous arena must be uploaded again. */
+int ckv_seq_tables_reserve(ckv_pool* pool, size_t max_sequences, size_t pages_per_sequence);
+/* Mirrors block_manager changes (src/block_manager.cc:5-64: pages appended
+ * to a reservation, a release; and a copy-on-write page replacement):
+ * entry (seq[i], index[i]) = block[i] for i < n, then table length of
+ * len_seq[j] = length[j] for j < m. Host work only: the written entries are
+ * pending (a later write of one entry wins) and reach the device with the
+ * next ckv_batch_upload, in its single copy. Checks, before anything changes:
+ *   block_table_range_out_of_bounds  seq >= max_sequences, index or length
+ *                                    > pages_per_sequence (index ==)
+ *   cache_block_out_of_range         block >= blocks
+ *   no_tables                        before ckv_seq_tables_reserve */
+int ckv_seq_tables_update(ckv_pool* pool, const uint32_t* seq, const uint32_t* index,
+                          const uint32_t* block, size_t n, const uint32_t* len_seq,
+                          const uint32_t* length, size_t m);
+/* Uploads a batch of n_items items; item i is token_count[i] rows of
+ * sequence seq[i] at positions first_position[i] + j, rows numbered in item
+ * order (model_batch::items, src/model_batch.h). Equivalent to
+ * ckv_tables_upload with the sequences' tables as the flat table, offsets
+ * seq*pages_per_sequence, lengths the sequences' table lengths, and (when
+ * with_slots) the slots of prepare_paged_batch. Checks (the row checks of
+ * src/model_batch.cc:151-185 and src/tensor/attention.cc:110-137):
+ *   invalid_argument                 an item with no tokens
+ *   block_table_range_out_of_bounds  seq >= max_sequences, or the item's
+ *                                    last position / block_size >= the
+ *                                    sequence's table length
+ * Table entries are checked when they are written (ckv_seq_tables_update),
+ * so slots cannot leave the pool. ckv_tables_patch is refused while such a
+ * batch is current. */
+int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_position,
+                     const uint32_t* token_count, size_t n_items, int with_slots);
 
 /* ---- Ops -------------------------------------------------------------------------- */
 /* store_kv (src/tensor/tensor_ops.cc:412-463; kernel src/metal/kernels/attention.metal:3-33):

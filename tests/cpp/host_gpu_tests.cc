@@ -7,6 +7,7 @@
 #include <array>
 #include <cmath>
 #include <cstring>
+#include <deque>
 #include <numeric>
 #include <unordered_map>
 
@@ -335,18 +336,25 @@ struct kv_path_runner final : model_runner {
     prefix_sharing sharing = prefix_sharing::shared_pages;
     std::unordered_map<seq_id, std::vector<std::vector<float>>> outputs; // per sample
     std::size_t prefill_tokens = 0;
+    bool device_tables = false; // tables kept on the device instead of prepare_paged_batch
 
     const model_info& info() const noexcept override
     {
         static const model_info value { "kv-path", 512, -1 };
         return value;
     }
-    result<std::unique_ptr<model_state>, model_runner_error> make_state(scheduler_config) const override
+    result<std::unique_ptr<model_state>, model_runner_error> make_state(
+        scheduler_config config) const override
     {
         auto s = hip_model_state::make(gpu(), shared_geometry, kv_dtype::bf16, sharing);
         if (!s)
             return fail(model_runner_errc::backend_failure, s.error());
         state = s->get();
+        if (device_tables) {
+            auto on = state->enable_device_tables(config.max_sequences, 512 / 16);
+            if (!on)
+                return fail(model_runner_errc::backend_failure, on.error());
+        }
         return std::unique_ptr<model_state>(std::move(*s));
     }
     result<std::vector<token_id>, model_runner_error> execute(const model_batch& batch,
@@ -355,17 +363,23 @@ struct kv_path_runner final : model_runner {
         auto& cache = state->cache();
         const std::size_t F = cache.elements_per_token();
         const std::size_t qf = 4 * cache.head_dimension(); // 4 q heads over 2 KV heads
-        auto md = prepare_paged_batch(batch, 512, cache.block_count(), cache.block_size());
-        if (!md)
-            return fail(model_runner_errc::inconsistent_batch, md.error());
         if (batch.phase == batch_phase::prefill)
             prefill_tokens += batch.tokens.size();
         const std::size_t rows = batch.tokens.size();
-        std::vector<std::uint32_t> positions(batch.positions.begin(), batch.positions.end());
-        auto up = upload_attention_metadata(cache, { positions, md->slots, md->block_table,
-                                                     md->table_offsets, md->table_lengths });
-        if (!up)
-            return fail(model_runner_errc::backend_failure, up.error());
+        if (device_tables) {
+            auto up = state->tables()->upload(batch, 512, true);
+            if (!up)
+                return fail(model_runner_errc::backend_failure, up.error());
+        } else {
+            auto md = prepare_paged_batch(batch, 512, cache.block_count(), cache.block_size());
+            if (!md)
+                return fail(model_runner_errc::inconsistent_batch, md.error());
+            std::vector<std::uint32_t> positions(batch.positions.begin(), batch.positions.end());
+            auto up = upload_attention_metadata(cache, { positions, md->slots, md->block_table,
+                                                         md->table_offsets, md->table_lengths });
+            if (!up)
+                return fail(model_runner_errc::backend_failure, up.error());
+        }
         auto out = device_buffer::make(gpu(), rows * qf * 2);
         if (!out)
             return fail(model_runner_errc::backend_failure, out.error());
@@ -492,6 +506,57 @@ TEST("shared prefix: a restored prefix attends like a cold prefill and copies on
             for (seq_id id : { 2, 3 })
                 CHECK(close_rows(warm.outputs[id], cold.outputs[id]));
         }
+    }
+}
+
+TEST("device tables: an engine run over device-resident tables equals the host-uploaded run")
+{
+    // shared prefixes (page sharing + copy-on-write tails), several live
+    // sequences with ragged prompts, rows reused after sequences finish
+    std::unordered_map<seq_id, std::vector<std::vector<float>>> runs[2];
+    std::size_t live_rows = 0;
+    for (int mode = 0; mode < 2; ++mode) {
+        kv_path_runner runner;
+        runner.device_tables = mode == 1;
+        auto engine = inference_engine::make(shared_config(), runner);
+        REQUIRE(engine);
+        auto base = seq::make(1, prompt_of(45, 1000), generation_params { 4 }, { 40 });
+        REQUIRE(base);
+        REQUIRE(engine->add(std::move(*base)));
+        run_all(*engine);
+        const std::size_t lengths[] = { 47, 9, 130, 61, 23 };
+        std::deque<seq> pending;
+        for (seq_id id = 2; id < 7; ++id) {
+            auto p = prompt_of(lengths[id - 2], id < 4 ? 1000 : 3000 + 200 * id);
+            std::vector<std::size_t> marks; // a prefix checkpoint where the prompt has one
+            if (p.size() > 40)
+                marks.push_back(40);
+            auto s = seq::make(id, p, generation_params { 3 + id % 3 }, marks);
+            REQUIRE(s);
+            pending.push_back(std::move(*s));
+        }
+        // admitted as pages free up: later sequences take finished ones' rows
+        while (!pending.empty() || !engine->is_finished()) {
+            while (!pending.empty()) {
+                auto r = engine->try_add(pending.front());
+                REQUIRE(r);
+                if (*r == admission_result::deferred)
+                    break;
+                REQUIRE(*r == admission_result::admitted);
+                pending.pop_front();
+            }
+            if (!engine->is_finished())
+                REQUIRE(engine->step());
+        }
+        if (mode == 1)
+            live_rows = runner.state->tables()->live_sequences();
+        runs[mode] = runner.outputs;
+    }
+    CHECK(live_rows == 0); // every finished sequence gave its row back
+    REQUIRE(runs[0].size() == 6 && runs[1].size() == 6);
+    for (const auto& [id, rows] : runs[0]) {
+        REQUIRE(runs[1].count(id) == 1);
+        CHECK(runs[1][id] == rows); // bit-exact: same kernels, same metadata
     }
 }
 

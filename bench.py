@@ -452,6 +452,96 @@ def bench_config4(args):
     return result
 
 
+PCIE5_X16_GBS = 64.0  # PCIe 5.0 x16, one direction
+
+
+def bench_spill(args):
+    """A cached prefix leaving HBM and coming back: config 4's 2,008-token
+    prefix (28 layers, 16-token pages in seeded order) exported to pinned host
+    memory in the packed [layer, token, kv_head, feature] layout and imported
+    into other pages (ckv_checkpoint_export / ckv_checkpoint_import), one of
+    each per step; the bytes cross PCIe once each way."""
+    import torch
+
+    from chibillm_amd import ckv
+    from oracle import oracle as orc  # seeded page order only
+
+    device = torch.device("cuda:0")
+    tokens = args.prefix
+    F = KV_HEADS * HEAD_DIM
+    pages = math.ceil(tokens / BLOCK)
+    n_pool = 2 * pages + 16
+    perm = orc.Mt64(args.seed).permutation(n_pool)
+    src, dst = perm[:pages], perm[pages:2 * pages]
+    ctx = ckv.Context(0, stream=torch.cuda.current_stream())
+    elems = LAYERS * n_pool * BLOCK * F
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed)
+    keys = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=gen)
+    values = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=gen)
+    pool = ckv.Pool(ctx, LAYERS, n_pool, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16, keys, values)
+    packed = LAYERS * tokens * F * 2  # bytes per tensor
+    hk = ctx.host_alloc(packed)
+    hv = ctx.host_alloc(packed)
+    log(f"spill: {tokens}-token prefix, {LAYERS} layers, {2 * packed / 2**20:.1f} MiB each way")
+
+    def one_step():
+        pool.checkpoint_export(src, tokens, hk, hv)
+        pool.checkpoint_import(dst, tokens, hk, hv)
+
+    for _ in range(args.warmup):
+        one_step()
+    ctx.sync()
+    ctx.profile(True)
+    ctx.profile_reset()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_step()
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    kernels = {name: ctx.profile_query(name) for name in ("checkpoint_export", "checkpoint_import")}
+    ctx.profile(False)
+    moved = 2 * 2 * packed  # keys + values, down and up
+    gbs = moved * args.steps / elapsed / 1e9
+    result = {
+        "metric": "prefix spill round trip (export to pinned host + import), GB/s over PCIe",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) K/V, seeded page order",
+        "config": {
+            "workload": f"spill: a {tokens}-token prefix of {LAYERS} layers exported to pinned "
+                        "host memory (packed layout) and imported into other pages, per step",
+            "layers": LAYERS, "tokens": tokens, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM,
+            "block_size": BLOCK, "bytes_each_way": 2 * packed,
+        },
+        "kernels_ms_per_step": {k: round(v[0] / args.steps, 4) for k, v in kernels.items()},
+        # the two directions run one after the other on one stream, so the
+        # bytes over the whole step time are the rate of the active direction
+        "roofline": {
+            "kernel": "checkpoint export + import (DMA over PCIe)",
+            "bound": "pcie",
+            "achieved": round(gbs, 2),
+            "peak": PCIE5_X16_GBS,
+            "unit": "GB/s (one direction at a time)",
+            "frac": round(gbs / PCIE5_X16_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": None,
+    }
+    ctx.host_free(hk)
+    ctx.host_free(hv)
+    pool.close()
+    return result
+
+
 CHURN_STEPS = 5000
 
 
@@ -540,16 +630,19 @@ def main():
                          "written), the known-size copy the HBM counters are scaled by")
     ap.add_argument("--no-fuse", action="store_true",
                     help="append and decode as two launches instead of ckv_append_decode")
-    ap.add_argument("--workload", choices=["config3", "config4", "config5"], default="config3",
+    ap.add_argument("--workload", choices=["config3", "config4", "config5", "spill"],
+                    default="config3",
                     help="config3 (default): the headline decode step; config4: chunked "
                          "prefill of 64 sequences over a shared prefix (MFMA tiles); config5: "
-                         "the continuous-batching churn trace (C++ scheduler driver)")
+                         "the continuous-batching churn trace (C++ scheduler driver); spill: "
+                         "a cached prefix exported to host memory and imported back")
     ap.add_argument("--rope", action="store_true",
                     help="config4: rotate the chunk's keys inside the append (ckv_rope_append) "
                          "and the queries in place (ckv_rope), Qwen3 theta 1e6")
     ap.add_argument("--prefix", type=int, default=2008,
                     help="config4 shared prefix tokens (2008 leaves a partial tail page, "
-                         "so every sequence copies it on write; 2000 does not)")
+                         "so every sequence copies it on write; 2000 does not); spill: the "
+                         "prefix moved")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -560,6 +653,8 @@ def main():
         result = bench_config4(args)
     elif args.workload == "config5":
         result = bench_config5(args)
+    elif args.workload == "spill":
+        result = bench_spill(args)
     else:
         result = bench_config3(args)
     print(json.dumps(result), flush=True)

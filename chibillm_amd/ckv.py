@@ -40,6 +40,8 @@ _SIGNATURES = [
     ("ckv_sync", _i, [_vp]),
     ("ckv_device_alloc", _i, [_vp, _sz, C.POINTER(_vp)]),
     ("ckv_device_free", _i, [_vp, _vp]),
+    ("ckv_host_alloc", _i, [_vp, _sz, C.POINTER(_vp)]),
+    ("ckv_host_free", _i, [_vp, _vp]),
     ("ckv_copy_to_device", _i, [_vp, _vp, _vp, _sz]),
     ("ckv_copy_to_host", _i, [_vp, _vp, _vp, _sz]),
     ("ckv_profile_enable", _i, [_vp, _i]),
@@ -66,6 +68,8 @@ _SIGNATURES = [
     ("ckv_copy_blocks", _i, [_vp, _u32p, _u32p, _sz]),
     ("ckv_checkpoint_pack", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
     ("ckv_checkpoint_unpack", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
+    ("ckv_checkpoint_export", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
+    ("ckv_checkpoint_import", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
 ]
 SYMBOLS = [name for name, _, _ in _SIGNATURES]
 
@@ -121,6 +125,12 @@ def _ptr(x) -> Optional[int]:
     return x.data_ptr()
 
 
+def _host(a: np.ndarray) -> int:
+    if not isinstance(a, np.ndarray) or not a.flags.c_contiguous or not a.flags.writeable:
+        raise ValueError("host buffers must be writeable contiguous numpy arrays")
+    return a.ctypes.data
+
+
 def _u32(a) -> Optional[np.ndarray]:
     if a is None:
         return None
@@ -161,6 +171,21 @@ class Context:
     def sync(self) -> None:
         self.check(load().ckv_sync(self.handle))
 
+    def host_alloc(self, nbytes: int) -> np.ndarray:
+        """Pinned host memory (ckv_host_alloc) as a uint8 numpy array; freed by
+        host_free (which waits for the stream) or when the context closes."""
+        ptr = _vp()
+        self.check(load().ckv_host_alloc(self.handle, nbytes, C.byref(ptr)))
+        buf = (C.c_uint8 * nbytes).from_address(ptr.value)
+        arr = np.frombuffer(buf, dtype=np.uint8)
+        self._pinned = getattr(self, "_pinned", {})
+        self._pinned[arr.ctypes.data] = ptr.value
+        return arr
+
+    def host_free(self, arr: np.ndarray) -> None:
+        ptr = self._pinned.pop(arr.ctypes.data)
+        self.check(load().ckv_host_free(self.handle, ptr))
+
     def profile(self, enabled: bool = True) -> None:
         self.check(load().ckv_profile_enable(self.handle, 1 if enabled else 0))
 
@@ -175,6 +200,9 @@ class Context:
 
     def close(self) -> None:
         if getattr(self, "handle", None):
+            for ptr in getattr(self, "_pinned", {}).values():
+                load().ckv_host_free(self.handle, ptr)
+            self._pinned = {}
             load().ckv_context_destroy(self.handle)
             self.handle = None
 
@@ -304,6 +332,20 @@ class Pool:
         b = _u32(blocks)
         self.ctx.check(load().ckv_checkpoint_unpack(self.handle, _p(b), b.size, tokens,
                                                     _ptr(packed_keys), _ptr(packed_values)))
+
+    def checkpoint_export(self, blocks, tokens: int, host_keys: np.ndarray,
+                          host_values: np.ndarray) -> None:
+        """Packed prefix into host memory (numpy arrays, pinned from
+        Context.host_alloc or pageable); read them only after ctx.sync()."""
+        b = _u32(blocks)
+        self.ctx.check(load().ckv_checkpoint_export(self.handle, _p(b), b.size, tokens,
+                                                    _host(host_keys), _host(host_values)))
+
+    def checkpoint_import(self, blocks, tokens: int, host_keys: np.ndarray,
+                          host_values: np.ndarray) -> None:
+        b = _u32(blocks)
+        self.ctx.check(load().ckv_checkpoint_import(self.handle, _p(b), b.size, tokens,
+                                                    _host(host_keys), _host(host_values)))
 
     def close(self) -> None:
         if getattr(self, "handle", None):

@@ -405,6 +405,71 @@ int run_checkpoint(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks, size
     });
 }
 
+// Packed prefix <-> host memory, through a device staging buffer of at most
+// spill_chunk_bytes per tensor: whole layers at a time, pack then copy down
+// (export), or copy up then unpack (import). The packed layout is that of
+// ckv_checkpoint_pack, so a layer range is one contiguous span of it.
+constexpr size_t spill_chunk_bytes = 64u << 20;
+
+int run_transfer(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks, size_t tokens,
+                 void* host_keys, void* host_values, bool import)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    int status = validate_prefix(pool, blocks, n_blocks, tokens);
+    if (status)
+        return set_error(ctx, status, "invalid checkpoint prefix");
+    if (!host_keys || !host_values)
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "host buffers are required");
+    const size_t required = 1 + (tokens - 1) / pool->block_size;
+    status = stage_list(pool, blocks, required);
+    if (status)
+        return status;
+    const size_t layer_bytes = tokens * pool->kv_heads * pool->head_dim * pool->elem_size;
+    const size_t per_chunk = std::clamp<size_t>(spill_chunk_bytes / layer_bytes, 1, pool->layers);
+    const size_t chunk_bytes = per_chunk * layer_bytes;
+    status = ensure_device(ctx, &pool->d_spill, &pool->d_spill_bytes, 2 * chunk_bytes,
+                           "spill staging");
+    if (status)
+        return status;
+    char* stage_k = pool->d_spill;
+    char* stage_v = pool->d_spill + chunk_bytes;
+    auto* hk = static_cast<char*>(host_keys);
+    auto* hv = static_cast<char*>(host_values);
+    const size_t page_layer_bytes = pool->blocks * pool->block_size * pool->kv_heads
+        * pool->head_dim * pool->elem_size;
+    for (size_t l0 = 0; l0 < pool->layers; l0 += per_chunk) {
+        const size_t n = std::min(per_chunk, pool->layers - l0);
+        const size_t bytes = n * layer_bytes, at = l0 * layer_bytes;
+        pool_view view = view_of(pool); // layers l0 .. l0 + n
+        view.keys = static_cast<char*>(view.keys) + l0 * page_layer_bytes;
+        view.values = static_cast<char*>(view.values) + l0 * page_layer_bytes;
+        auto copy = [&](void* dst, const void* src, hipMemcpyKind kind) {
+            const hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, ctx->stream);
+            return e == hipSuccess ? CKV_OK : hip_error(ctx, e, "checkpoint host copy");
+        };
+        if (import) {
+            status = copy(stage_k, hk + at, hipMemcpyHostToDevice);
+            if (!status)
+                status = copy(stage_v, hv + at, hipMemcpyHostToDevice);
+        }
+        if (!status)
+            status = run_kernel(ctx, import ? "checkpoint_import" : "checkpoint_export", [&] {
+                return launch_checkpoint(ctx->stream, view, (uint32_t)n, pool->d_pairs,
+                                         (uint32_t)tokens, stage_k, stage_v, import);
+            });
+        if (!status && !import) {
+            status = copy(hk + at, stage_k, hipMemcpyDeviceToHost);
+            if (!status)
+                status = copy(hv + at, stage_v, hipMemcpyDeviceToHost);
+        }
+        if (status)
+            return status;
+    }
+    return CKV_OK;
+}
+
 int create_pool(ckv_context* ctx, size_t layers, size_t blocks, size_t block_size,
                 size_t kv_heads, size_t head_dim, int dtype, void* keys, void* values,
                 ckv_pool** out)
@@ -669,6 +734,35 @@ int ckv_device_free(ckv_context* ctx, void* ptr)
     return CKV_OK;
 }
 
+int ckv_host_alloc(ckv_context* ctx, size_t bytes, void** out)
+{
+    if (!ctx || !out)
+        return CKV_E_INVALID_ARGUMENT;
+    *out = nullptr;
+    (void)hipSetDevice(ctx->device);
+    const hipError_t e = hipHostMalloc(out, bytes ? bytes : 1, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return hip_error(ctx, e, "pinned host allocation");
+    }
+    return CKV_OK;
+}
+
+int ckv_host_free(ckv_context* ctx, void* ptr)
+{
+    if (!ctx)
+        return CKV_E_INVALID_ARGUMENT;
+    if (!ptr)
+        return CKV_OK;
+    // copies to or from the buffer may still be queued
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess)
+        e = hipHostFree(ptr);
+    if (e != hipSuccess)
+        return hip_error(ctx, e, "pinned host free");
+    return CKV_OK;
+}
+
 int ckv_copy_to_device(ckv_context* ctx, void* device_dst, const void* host_src, size_t bytes)
 {
     if (!ctx || (bytes && (!device_dst || !host_src)))
@@ -776,6 +870,8 @@ int ckv_pool_destroy(ckv_pool* pool)
         (void)hipFree(pool->d_order);
     if (pool->d_work)
         (void)hipFree(pool->d_work);
+    if (pool->d_spill)
+        (void)hipFree(pool->d_spill);
     delete pool;
     return CKV_OK;
 }
@@ -1410,6 +1506,19 @@ int ckv_checkpoint_unpack(ckv_pool* pool, const uint32_t* blocks, size_t n_block
                           size_t tokens, const void* packed_keys, const void* packed_values)
 {
     return run_checkpoint(pool, blocks, n_blocks, tokens, packed_keys, packed_values, true);
+}
+
+int ckv_checkpoint_export(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks, size_t tokens,
+                          void* host_keys, void* host_values)
+{
+    return run_transfer(pool, blocks, n_blocks, tokens, host_keys, host_values, false);
+}
+
+int ckv_checkpoint_import(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks,
+                          size_t tokens, const void* host_keys, const void* host_values)
+{
+    return run_transfer(pool, blocks, n_blocks, tokens, const_cast<void*>(host_keys),
+                        const_cast<void*>(host_values), true);
 }
 
 } // extern "C"

@@ -163,6 +163,8 @@ struct ckv_pool {
     size_t d_partials_bytes = 0;
     uint32_t* d_pairs = nullptr; // block-id pairs / patch pairs
     size_t d_pairs_words = 0;
+    char* d_spill = nullptr; // staging of checkpoint export/import
+    size_t d_spill_bytes = 0;
 };
 
 namespace ckv {

@@ -104,6 +104,43 @@ device_buffer::download(void* host, std::size_t bytes) const
     return {};
 }
 
+result<host_buffer, ckv_failure>
+host_buffer::make(const hip_context& ctx, std::size_t bytes)
+{
+    host_buffer b;
+    const int rc = ckv_host_alloc(ctx.get(), bytes, &b.ptr_);
+    if (rc)
+        return fail(ctx.last(rc));
+    b.ctx_ = ctx.get();
+    b.bytes_ = bytes;
+    return b;
+}
+
+host_buffer::host_buffer(host_buffer&& other) noexcept
+    : ctx_(std::exchange(other.ctx_, nullptr))
+    , ptr_(std::exchange(other.ptr_, nullptr))
+    , bytes_(std::exchange(other.bytes_, 0))
+{}
+
+host_buffer&
+host_buffer::operator=(host_buffer&& other) noexcept
+{
+    if (this != &other) {
+        if (ptr_)
+            ckv_host_free(ctx_, ptr_);
+        ctx_ = std::exchange(other.ctx_, nullptr);
+        ptr_ = std::exchange(other.ptr_, nullptr);
+        bytes_ = std::exchange(other.bytes_, 0);
+    }
+    return *this;
+}
+
+host_buffer::~host_buffer()
+{
+    if (ptr_)
+        ckv_host_free(ctx_, ptr_);
+}
+
 // ---- hip_kv_cache ------------------------------------------------------------------
 
 result<hip_kv_cache, kv_cache_error>
@@ -222,6 +259,47 @@ hip_kv_cache::restore(std::span<const block_id> blocks, const kv_cache_checkpoin
         return fail(state_errc::invalid_reservation);
     if (rc)
         return fail(state_errc::backend_failure, ctx_->last(rc), "checkpoint unpack");
+    return {};
+}
+
+result<std::unique_ptr<host_kv_checkpoint>, state_error>
+hip_kv_cache::export_prefix(std::span<const block_id> blocks, std::size_t tokens) const
+{
+    const std::size_t bytes = checkpoint_bytes(tokens);
+    if (!bytes)
+        return fail(state_errc::invalid_reservation);
+    auto saved = std::make_unique<host_kv_checkpoint>(config_, tokens);
+    auto k = host_buffer::make(*ctx_, bytes / 2);
+    auto v = host_buffer::make(*ctx_, bytes / 2);
+    if (!k || !v)
+        return fail(state_errc::allocation_failed);
+    saved->keys = std::move(*k);
+    saved->values = std::move(*v);
+    const int rc = ckv_checkpoint_export(pool_, blocks.data(), blocks.size(), tokens,
+                                         saved->keys.data(), saved->values.data());
+    if (rc == CKV_E_STATE_INVALID_RESERVATION)
+        return fail(state_errc::invalid_reservation);
+    if (rc)
+        return fail(state_errc::backend_failure, ctx_->last(rc), "checkpoint export");
+    return saved;
+}
+
+result<void, state_error>
+hip_kv_cache::import_prefix(std::span<const block_id> blocks, const host_kv_checkpoint& saved)
+{
+    const bool same_geometry = saved.config.layer_count == layer_count()
+        && saved.config.kv_head_count == kv_head_count()
+        && saved.config.head_dimension == head_dimension();
+    const std::size_t bytes = checkpoint_bytes(saved.token_count);
+    if (!same_geometry || !bytes || saved.keys.size_bytes() != bytes / 2
+        || saved.values.size_bytes() != bytes / 2)
+        return fail(state_errc::invalid_reservation);
+    const int rc = ckv_checkpoint_import(pool_, blocks.data(), blocks.size(), saved.token_count,
+                                         saved.keys.data(), saved.values.data());
+    if (rc == CKV_E_STATE_INVALID_RESERVATION)
+        return fail(state_errc::invalid_reservation);
+    if (rc)
+        return fail(state_errc::backend_failure, ctx_->last(rc), "checkpoint import");
     return {};
 }
 

@@ -80,6 +80,27 @@ private:
     std::size_t bytes_ = 0;
 };
 
+// Move-only pinned host allocation (ckv_host_alloc); freeing it waits for the
+// context stream, so queued copies from or to it finish first.
+class host_buffer {
+public:
+    static result<host_buffer, ckv_failure> make(const hip_context& ctx, std::size_t bytes);
+    host_buffer() = default;
+    host_buffer(host_buffer&& other) noexcept;
+    host_buffer& operator=(host_buffer&& other) noexcept;
+    host_buffer(const host_buffer&) = delete;
+    host_buffer& operator=(const host_buffer&) = delete;
+    ~host_buffer();
+
+    void* data() const noexcept { return ptr_; }
+    std::size_t size_bytes() const noexcept { return bytes_; }
+
+private:
+    ckv_context* ctx_ = nullptr;
+    void* ptr_ = nullptr;
+    std::size_t bytes_ = 0;
+};
+
 struct kv_cache_config {
     std::size_t layer_count;
     std::size_t block_count;
@@ -130,6 +151,23 @@ struct kv_cache_checkpoint : model_checkpoint {
     kv_cache_config config;
     device_buffer keys;
     device_buffer values;
+    std::size_t size_bytes() const noexcept override
+    {
+        return keys.size_bytes() + values.size_bytes();
+    }
+};
+
+// The same packed data in pinned host memory (ckv_checkpoint_export): where the
+// reference keeps its checkpoints (host byte vectors, src/metal/metal_kv_cache.h:24-40),
+// so a prefix outlives its pages without holding HBM.
+struct host_kv_checkpoint : model_checkpoint {
+    host_kv_checkpoint(kv_cache_config c, std::size_t tokens)
+        : model_checkpoint(tokens)
+        , config(c)
+    {}
+    kv_cache_config config;
+    host_buffer keys;
+    host_buffer values;
     std::size_t size_bytes() const noexcept override
     {
         return keys.size_bytes() + values.size_bytes();
@@ -192,6 +230,12 @@ public:
     checkpoint(std::span<const block_id> blocks, std::size_t tokens) const;
     result<void, state_error> restore(std::span<const block_id> blocks,
                                       const kv_cache_checkpoint& saved);
+    // The packed prefix to and from pinned host memory. Both are queued on the
+    // context stream; the checkpoint's buffers wait for it before they are freed.
+    result<std::unique_ptr<host_kv_checkpoint>, state_error>
+    export_prefix(std::span<const block_id> blocks, std::size_t tokens) const;
+    result<void, state_error> import_prefix(std::span<const block_id> blocks,
+                                            const host_kv_checkpoint& saved);
     // Page copies on the device, all layers, keys and values.
     result<void, state_error> copy_pages(std::span<const block_id> from,
                                          std::span<const block_id> to);

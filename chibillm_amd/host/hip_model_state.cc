@@ -16,10 +16,59 @@ hip_model_state::make(const hip_context& ctx, kv_cache_config config, kv_dtype t
         std::make_shared<block_manager>(std::move(*pages)), std::move(*cache), sharing));
 }
 
+result<void, state_error>
+hip_model_state::reserve(seq_id id, std::size_t tokens)
+{
+    auto reserved = pages_->reserve(id, tokens);
+    if (reserved || reserved.error().code != state_errc::capacity_exhausted || !spill_)
+        return reserved;
+    const std::size_t bs = pages_->block_size();
+    const std::size_t required = tokens ? 1 + (tokens - 1) / bs : 0;
+    const std::size_t held = pages_->resources(id).blocks.size();
+    if (required <= held || !spill_for(required - held))
+        return reserved;
+    return pages_->reserve(id, tokens);
+}
+
+bool
+hip_model_state::spill_for(std::size_t pages) noexcept
+try {
+    // passes until no checkpoint frees a page: spilling one checkpoint can
+    // leave an older one (a shorter prefix of the same pages) the only holder
+    for (bool progress = true; progress && pages_->free_block_count() < pages;) {
+        progress = false;
+        for (shared_prefix_checkpoint* saved : *live_) {
+            if (pages_->free_block_count() >= pages)
+                break;
+            if (saved->is_spilled())
+                continue;
+            // only pages that nothing else references come free
+            std::size_t freed = 0;
+            for (const block_id b : saved->pages)
+                freed += pages_->refcount(b) == 1;
+            if (!freed)
+                continue;
+            // the export is queued before any later write of the freed pages
+            auto exported = cache_.export_prefix(saved->pages, saved->token_count);
+            if (!exported)
+                return false;
+            saved->spilled = std::move(*exported);
+            pages_->drop(saved->pages);
+            saved->pages.clear();
+            ++spills_;
+            spilled_pages_ += freed;
+            progress = true;
+        }
+    }
+    return pages_->free_block_count() >= pages;
+} catch (const std::bad_alloc&) {
+    return false;
+}
+
 std::size_t
 hip_model_state::checkpoint_bytes(std::size_t tokens) const noexcept
 {
-    if (sharing_ == prefix_sharing::packed_copy)
+    if (sharing_ != prefix_sharing::shared_pages)
         return cache_.checkpoint_bytes(tokens);
     if (!tokens || tokens > cache_.block_count() * cache_.block_size())
         return 0;
@@ -37,6 +86,12 @@ hip_model_state::checkpoint(seq_id id, std::size_t tokens) const
             return fail(saved.error());
         return std::unique_ptr<model_checkpoint>(std::move(*saved));
     }
+    if (sharing_ == prefix_sharing::host_copy) {
+        auto saved = cache_.export_prefix(table, tokens);
+        if (!saved)
+            return fail(saved.error());
+        return std::unique_ptr<model_checkpoint>(std::move(*saved));
+    }
     const std::size_t bytes = checkpoint_bytes(tokens);
     if (!bytes)
         return fail(state_errc::invalid_reservation);
@@ -46,14 +101,22 @@ hip_model_state::checkpoint(seq_id id, std::size_t tokens) const
     std::vector<block_id> held(table.begin(), table.begin() + needed);
     CL_TRY(pages_->retain(held));
     return std::unique_ptr<model_checkpoint>(
-        std::make_unique<shared_prefix_checkpoint>(pages_, std::move(held), tokens, bytes));
+        std::make_unique<shared_prefix_checkpoint>(pages_, live_, std::move(held), tokens, bytes));
 }
 
 result<void, state_error>
 hip_model_state::restore(seq_id id, const model_checkpoint& saved)
 {
-    if (const auto* shared = dynamic_cast<const shared_prefix_checkpoint*>(&saved))
-        return restore_shared(id, *shared);
+    const host_kv_checkpoint* host = dynamic_cast<const host_kv_checkpoint*>(&saved);
+    if (const auto* shared = dynamic_cast<const shared_prefix_checkpoint*>(&saved)) {
+        if (!shared->is_spilled())
+            return restore_shared(id, *shared);
+        host = shared->spilled.get();
+    }
+    if (host) { // reserve, copy in from host memory
+        CL_TRY(reserve(id, host->token_count));
+        return cache_.import_prefix(resources(id).blocks, *host);
+    }
     const auto* packed = dynamic_cast<const kv_cache_checkpoint*>(&saved);
     if (!packed)
         return fail(state_errc::invalid_reservation);

@@ -122,6 +122,11 @@ int ckv_sync(ckv_context* ctx);
  * The copies are synchronous with respect to the context stream. */
 int ckv_device_alloc(ckv_context* ctx, size_t bytes, void** out);
 int ckv_device_free(ckv_context* ctx, void* ptr);
+/* Pinned (page-locked) host memory, for spilled checkpoints (ckv_checkpoint_export):
+ * copies to and from it run asynchronously on the context stream. Free waits for
+ * the stream first. */
+int ckv_host_alloc(ckv_context* ctx, size_t bytes, void** out);
+int ckv_host_free(ckv_context* ctx, void* ptr);
 int ckv_copy_to_device(ckv_context* ctx, void* device_dst, const void* host_src, size_t bytes);
 int ckv_copy_to_host(ckv_context* ctx, void* host_dst, const void* device_src, size_t bytes);
 
@@ -311,6 +316,20 @@ int ckv_checkpoint_pack(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks,
                         void* packed_keys, void* packed_values);
 int ckv_checkpoint_unpack(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks,
                           size_t tokens, const void* packed_keys, const void* packed_values);
+/* The same packed prefix in host memory: a prefix checkpoint that outlives its
+ * pages (the reference's kv_cache_checkpoint holds it in host byte vectors,
+ * src/metal/metal_kv_cache.h:24-40, and the byte-bounded prefix cache,
+ * src/prefix_cache.cc:42-73, keeps it after the pages are reused). Host
+ * buffers hold layers*tokens*kv_heads*head_dim elements each, in the layout of
+ * ckv_checkpoint_pack. The copies run on the context stream through a device
+ * staging buffer of at most 64 MiB per tensor, whole layers at a time; they are
+ * asynchronous when the host buffers are pinned (ckv_host_alloc): do not read an
+ * exported buffer, or change or free an imported one, before ckv_sync. Checks as
+ * ckv_checkpoint_pack. Profile names "checkpoint_export", "checkpoint_import". */
+int ckv_checkpoint_export(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks, size_t tokens,
+                          void* host_keys, void* host_values);
+int ckv_checkpoint_import(ckv_pool* pool, const uint32_t* blocks, size_t n_blocks,
+                          size_t tokens, const void* host_keys, const void* host_values);
 
 #ifdef __cplusplus
 }

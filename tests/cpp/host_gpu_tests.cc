@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <array>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <deque>
 #include <numeric>
@@ -630,4 +631,104 @@ TEST("shared prefix: the copy-on-write tail page equals its source bit for bit")
     for (std::size_t i = 0; i < rk.size(); ++i)
         changed += rk[i] != k[i];
     CHECK(changed <= cache.layer_count() * per_page);
+}
+
+TEST("spill: an exhausted pool moves a lone prefix checkpoint to host memory and restores it")
+{
+    auto made = hip_model_state::make(gpu(), shared_geometry, kv_dtype::bf16);
+    REQUIRE(made);
+    auto& state = **made;
+    auto& cache = state.cache();
+    std::vector<std::uint16_t> k(cache.element_count()), v(cache.element_count());
+    for (std::size_t i = 0; i < k.size(); ++i) {
+        k[i] = static_cast<std::uint16_t>(i * 7919u + 3);
+        v[i] = static_cast<std::uint16_t>(i * 104729u + 5);
+    }
+    write_cache(cache, cache.keys(), k);
+    write_cache(cache, cache.values(), v);
+    REQUIRE(state.reserve(1, 40)); // 3 pages
+    const auto first = state.resources(1).blocks;
+    const std::vector<block_id> held(first.begin(), first.end());
+    auto cp = state.checkpoint(1, 40);
+    REQUIRE(cp);
+    state.release(1); // the checkpoint alone holds the 3 pages
+    // the whole pool for one sequence: the checkpoint must leave
+    REQUIRE(state.reserve(2, 32 * 16));
+    CHECK(state.spills() == 1);
+    CHECK(state.spilled_pages() == 3);
+    CHECK(state.pages().free_block_count() == 0);
+    // the pages are reused and overwritten
+    std::vector<std::uint16_t> junk(cache.element_count(), 0x7F80);
+    write_cache(cache, cache.keys(), junk);
+    write_cache(cache, cache.values(), junk);
+    state.release(2);
+    REQUIRE(state.reserve(3, 1));
+    REQUIRE(state.restore(3, **cp)); // copied in from host memory
+    const auto own = state.resources(3).blocks;
+    REQUIRE(own.size() == 3);
+    const auto rk = read_cache<std::uint16_t>(cache, cache.keys());
+    const auto rv = read_cache<std::uint16_t>(cache, cache.values());
+    const std::size_t per_token = cache.elements_per_token();
+    const std::size_t per_page = cache.elements_per_block();
+    std::size_t mismatches = 0;
+    for (std::size_t layer = 0; layer < cache.layer_count(); ++layer) {
+        const std::size_t base = layer * cache.elements_per_layer();
+        for (std::size_t t = 0; t < 40; ++t) {
+            const std::size_t to = base + own[t / 16] * per_page + (t % 16) * per_token;
+            const std::size_t from = base + held[t / 16] * per_page + (t % 16) * per_token;
+            mismatches += !std::equal(rk.begin() + to, rk.begin() + to + per_token,
+                                      k.begin() + from);
+            mismatches += !std::equal(rv.begin() + to, rv.begin() + to + per_token,
+                                      v.begin() + from);
+        }
+    }
+    CHECK(mismatches == 0);
+}
+
+TEST("spill: a sequence that needs the pool spills a cached prefix; a later hit restores it")
+{
+    std::unordered_map<seq_id, std::vector<std::vector<float>>> outputs[2];
+    std::size_t spills = 0, spilled_pages = 0;
+    for (int cold = 0; cold < 2; ++cold) {
+        kv_path_runner runner;
+        auto config = shared_config();
+        if (cold)
+            config.prefix_cache_bytes = 0;
+        auto engine = inference_engine::make(config, runner);
+        REQUIRE(engine);
+        if (!cold) { // caches a 40-token prefix, which then holds 3 pages alone
+            auto first = seq::make(1, prompt_of(45, 1000), generation_params { 2 }, { 40 });
+            REQUIRE(first);
+            REQUIRE(engine->add(std::move(*first)));
+            run_all(*engine);
+            REQUIRE(engine->engine_scheduler().prefixes().entry_count() == 1);
+            CHECK(runner.state->pages().free_block_count() == 29);
+        }
+        // 30 pages of budget: only fits once the prefix's pages are spilled
+        auto big = seq::make(2, prompt_of(470, 9000), generation_params { 3 });
+        REQUIRE(big);
+        REQUIRE(engine->add(std::move(*big)));
+        run_all(*engine);
+        auto p = prompt_of(40, 1000);
+        for (int i = 0; i < 9; ++i)
+            p.push_back(static_cast<token_id>(7000 + i));
+        auto hit = seq::make(3, p, generation_params { 3 }, { 40 });
+        REQUIRE(hit);
+        REQUIRE(engine->add(std::move(*hit)));
+        if (!cold)
+            CHECK(engine->find_sequence(3)->cached_token_count() == 40);
+        run_all(*engine);
+        if (!cold) {
+            spills = runner.state->spills();
+            spilled_pages = runner.state->spilled_pages();
+        }
+        outputs[cold] = runner.outputs;
+    }
+    // the 40-token prefix (3 pages) makes room for sequence 2; sequence 2's
+    // own prompt checkpoint (469 tokens, 30 pages, the default boundary)
+    // then makes room for sequence 3's restore
+    CHECK(spills == 2);
+    CHECK(spilled_pages == 33);
+    for (seq_id id : { 2, 3 })
+        CHECK(close_rows(outputs[0][id], outputs[1][id]));
 }

@@ -160,6 +160,8 @@ def bench_config3(args):
     k_new = torch.randn(LAYERS, BATCH, F, generator=gen, device=device).to(torch.bfloat16)
     v_new = torch.randn(LAYERS, BATCH, F, generator=gen, device=device).to(torch.bfloat16)
     out = torch.empty(LAYERS, BATCH, Q_HEADS * HEAD_DIM, dtype=torch.bfloat16, device=device)
+    gate = (torch.randn(LAYERS, BATCH, Q_HEADS * HEAD_DIM, generator=gen, device=device)
+            .to(torch.bfloat16) if args.gate else None)
     scale = 1.0 / math.sqrt(HEAD_DIM)
     offsets = np.arange(BATCH, dtype=np.uint32) * max_pages
 
@@ -174,6 +176,9 @@ def bench_config3(args):
             if args.no_fuse:
                 pool.append(layer, k_new[layer], v_new[layer])
                 pool.decode(layer, q[layer], Q_HEADS, scale, out[layer])
+            elif args.gate:
+                pool.append_decode_gated(layer, k_new[layer], v_new[layer], q[layer], Q_HEADS,
+                                         scale, gate[layer], out[layer])
             else:
                 pool.append_decode(layer, k_new[layer], v_new[layer], q[layer], Q_HEADS, scale,
                                    out[layer])
@@ -211,8 +216,9 @@ def bench_config3(args):
     # algorithmic bytes of one launch (one layer): KV of every attended token,
     # Q and O, the table entries read, and (fused) the new K/V rows written
     appended = 0 if args.no_fuse else BATCH * kv_row_bytes
+    qo_rows = 3 if args.gate else 2  # Q and O, and the gate when it is read
     per_launch = (tokens_attended * kv_row_bytes + pages_read * 4
-                  + args.steps * (2 * BATCH * Q_HEADS * HEAD_DIM * 2 + appended)) / args.steps
+                  + args.steps * (qo_rows * BATCH * Q_HEADS * HEAD_DIM * 2 + appended)) / args.steps
     decode_avg_s = decode_ms / decode_n / 1e3
     achieved = per_launch / decode_avg_s / 1e9
     result = {
@@ -232,7 +238,8 @@ def bench_config3(args):
             "workload": "config3: 28-layer decode step (append 1 token/seq/layer + paged GQA "
                         "decode attention), batch 128, context U[1024,8192] growing 1/step",
             "launches": "two per layer (ckv_append, ckv_decode_attention)" if args.no_fuse
-                        else "one per layer (ckv_append_decode)",
+                        else ("one per layer (ckv_append_decode_gated: sigmoid gate in the "
+                              "epilogue)" if args.gate else "one per layer (ckv_append_decode)"),
             "layers": LAYERS, "batch": BATCH, "kv_heads": KV_HEADS, "q_heads": Q_HEADS,
             "head_dim": HEAD_DIM, "block_size": BLOCK, "pool_pages": n_pool,
             "kv_pool_gb": round(kv_gb, 2),
@@ -636,6 +643,9 @@ def main():
                          "prefill of 64 sequences over a shared prefix (MFMA tiles); config5: "
                          "the continuous-batching churn trace (C++ scheduler driver); spill: "
                          "a cached prefix exported to host memory and imported back")
+    ap.add_argument("--gate", action="store_true",
+                    help="config3: the Qwen3.5 sigmoid gate applied in the decode epilogue "
+                         "(ckv_append_decode_gated)")
     ap.add_argument("--rope", action="store_true",
                     help="config4: rotate the chunk's keys inside the append (ckv_rope_append) "
                          "and the queries in place (ckv_rope), Qwen3 theta 1e6")

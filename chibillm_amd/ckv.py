@@ -68,6 +68,9 @@ _SIGNATURES = [
     ("ckv_copy_blocks", _i, [_vp, _u32p, _u32p, _sz]),
     ("ckv_checkpoint_pack", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
     ("ckv_checkpoint_unpack", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
+    ("ckv_attention_gated", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _vp, _sz]),
+    ("ckv_append_decode_gated", _i, [_vp, _sz, _vp, _vp, _vp, _sz, C.c_float, _vp, _vp, _sz]),
+    ("ckv_sigmoid_mul", _i, [_vp, _i, _vp, _vp, _vp, _sz]),
     ("ckv_checkpoint_export", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
     ("ckv_checkpoint_import", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
 ]
@@ -185,6 +188,12 @@ class Context:
     def host_free(self, arr: np.ndarray) -> None:
         ptr = self._pinned.pop(arr.ctypes.data)
         self.check(load().ckv_host_free(self.handle, ptr))
+
+    def sigmoid_mul(self, gate, inputs, output, dtype=None) -> None:
+        """output = inputs * sigmoid(gate), elementwise (ckv_sigmoid_mul)."""
+        code = _dtype_code(dtype if dtype is not None else inputs.dtype)
+        self.check(load().ckv_sigmoid_mul(self.handle, code, _ptr(gate), _ptr(inputs),
+                                          _ptr(output), inputs.numel()))
 
     def profile(self, enabled: bool = True) -> None:
         self.check(load().ckv_profile_enable(self.handle, 1 if enabled else 0))
@@ -306,6 +315,19 @@ class Pool:
 
     def attention(self, layer, queries, q_heads, scale, output, rows=None) -> None:
         self._attend(load().ckv_attention, layer, queries, q_heads, scale, output, rows)
+
+    def attention_gated(self, layer, queries, q_heads, scale, gate, output, rows=None) -> None:
+        """output = attention * sigmoid(gate) (ckv_attention_gated)."""
+        rows = queries.shape[0] if rows is None else rows
+        self.ctx.check(load().ckv_attention_gated(self.handle, layer, _ptr(queries), q_heads,
+                                                  scale, _ptr(gate), _ptr(output), rows))
+
+    def append_decode_gated(self, layer, keys, values, queries, q_heads, scale, gate, output,
+                            rows=None) -> None:
+        rows = queries.shape[0] if rows is None else rows
+        self.ctx.check(load().ckv_append_decode_gated(self.handle, layer, _ptr(keys),
+                                                      _ptr(values), _ptr(queries), q_heads,
+                                                      scale, _ptr(gate), _ptr(output), rows))
 
     def rope(self, inputs, outputs, heads: int, theta: float, rotary_dim: int = 0,
              rows: Optional[int] = None) -> None:

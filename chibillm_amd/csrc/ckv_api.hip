@@ -303,7 +303,7 @@ int ensure_work(ckv_pool* pool)
 }
 
 int run_decode(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads, float scale,
-               void* output)
+               void* output, const void* gate = nullptr)
 {
     ckv_context* ctx = pool->ctx;
     const pool_view view = view_of(pool);
@@ -326,12 +326,13 @@ int run_decode(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads
     }
     status = run_kernel(ctx, "paged_attention_decode", [&] {
         return launch_decode(ctx->stream, view, pool->meta, (uint32_t)layer, queries,
-                             (uint32_t)q_heads, scale, output, partials, ctx->cu_count);
+                             (uint32_t)q_heads, scale, output, partials, ctx->cu_count, gate);
     });
     if (status || !needs_merge)
         return status;
     return run_kernel(ctx, "paged_attention_merge", [&] {
-        return launch_merge(ctx->stream, view, pool->meta, (uint32_t)q_heads, output, partials);
+        return launch_merge(ctx->stream, view, pool->meta, (uint32_t)q_heads, output, partials,
+                            gate);
     });
 }
 
@@ -1396,19 +1397,35 @@ int ckv_gather(ckv_pool* pool, size_t layer, size_t table_offset, size_t table_l
     });
 }
 
-int ckv_decode_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
-                         float scale, void* output, size_t rows)
+namespace {
+
+// The gate of the gated forms: [rows, q_heads * head_dim] of the pool dtype,
+// not the queries' or the output's memory (the epilogue reads it while other
+// workgroups still read queries).
+int check_gate(const ckv_pool* pool, const void* gate, const void* queries, const void* output,
+               size_t rows)
+{
+    if (rows && !gate)
+        return set_error(pool->ctx, CKV_E_INVALID_ARGUMENT, "gate is required");
+    if (gate && (gate == queries || gate == output))
+        return set_error(pool->ctx, CKV_E_UNSUPPORTED_ALIASING, "gate overlaps queries or output");
+    return CKV_OK;
+}
+
+int decode_impl(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads, float scale,
+                void* output, size_t rows, const void* gate)
 {
     if (!pool)
         return CKV_E_INVALID_ARGUMENT;
     const int status = check_attention(pool, layer, queries, q_heads, output, rows);
     if (status || !rows)
         return status;
-    return run_decode(pool, layer, queries, q_heads, scale, output);
+    return run_decode(pool, layer, queries, q_heads, scale, output, gate);
 }
 
-int ckv_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void* values,
-                      const void* queries, size_t q_heads, float scale, void* output, size_t rows)
+int append_decode_impl(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+                       const void* queries, size_t q_heads, float scale, void* output,
+                       size_t rows, const void* gate)
 {
     if (!pool)
         return CKV_E_INVALID_ARGUMENT;
@@ -1431,17 +1448,17 @@ int ckv_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void
             return status;
         return run_kernel(ctx, "append_decode", [&] {
             return launch_append_decode(ctx->stream, view, pool->meta, (uint32_t)layer, keys,
-                                        values, queries, (uint32_t)q_heads, scale, output);
+                                        values, queries, (uint32_t)q_heads, scale, output, gate);
         });
     }
     status = ckv_append(pool, layer, keys, values, rows);
     if (status)
         return status;
-    return run_decode(pool, layer, queries, q_heads, scale, output);
+    return run_decode(pool, layer, queries, q_heads, scale, output, gate);
 }
 
-int ckv_prefill_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
-                          float scale, void* output, size_t rows)
+int prefill_impl(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads, float scale,
+                 void* output, size_t rows, const void* gate)
 {
     if (!pool)
         return CKV_E_INVALID_ARGUMENT;
@@ -1449,25 +1466,91 @@ int ckv_prefill_attention(ckv_pool* pool, size_t layer, const void* queries, siz
     if (status || !rows)
         return status;
     const pool_view view = view_of(pool);
-    if (!prefill_supported(view, (uint32_t)q_heads, queries, output))
-        return run_decode(pool, layer, queries, q_heads, scale, output);
+    const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (!prefill_supported(view, (uint32_t)q_heads, queries, output) || (gate && !aligned(gate)))
+        return run_decode(pool, layer, queries, q_heads, scale, output, gate);
     ckv_context* ctx = pool->ctx;
     return run_kernel(ctx, "paged_attention_prefill", [&] {
         return launch_prefill(ctx->stream, view, pool->meta, (uint32_t)layer, queries,
-                              (uint32_t)q_heads, scale, output);
+                              (uint32_t)q_heads, scale, output, gate);
     });
 }
 
-int ckv_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
-                  float scale, void* output, size_t rows)
+int attention_impl(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads, float scale,
+                   void* output, size_t rows, const void* gate)
 {
     if (!pool)
         return CKV_E_INVALID_ARGUMENT;
     // src/tensor/attention.cc:290-309: tiles are used when some run of rows
     // shares a query tile and head_dim <= 128
     if (pool->shared_tile && pool->head_dim <= 128)
-        return ckv_prefill_attention(pool, layer, queries, q_heads, scale, output, rows);
-    return ckv_decode_attention(pool, layer, queries, q_heads, scale, output, rows);
+        return prefill_impl(pool, layer, queries, q_heads, scale, output, rows, gate);
+    return decode_impl(pool, layer, queries, q_heads, scale, output, rows, gate);
+}
+
+} // namespace
+
+int ckv_decode_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                         float scale, void* output, size_t rows)
+{
+    return decode_impl(pool, layer, queries, q_heads, scale, output, rows, nullptr);
+}
+
+int ckv_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+                      const void* queries, size_t q_heads, float scale, void* output, size_t rows)
+{
+    return append_decode_impl(pool, layer, keys, values, queries, q_heads, scale, output, rows,
+                              nullptr);
+}
+
+int ckv_prefill_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                          float scale, void* output, size_t rows)
+{
+    return prefill_impl(pool, layer, queries, q_heads, scale, output, rows, nullptr);
+}
+
+int ckv_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                  float scale, void* output, size_t rows)
+{
+    return attention_impl(pool, layer, queries, q_heads, scale, output, rows, nullptr);
+}
+
+int ckv_attention_gated(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                        float scale, const void* gate, void* output, size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    const int status = check_gate(pool, gate, queries, output, rows);
+    if (status)
+        return status;
+    return attention_impl(pool, layer, queries, q_heads, scale, output, rows, gate);
+}
+
+int ckv_append_decode_gated(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+                            const void* queries, size_t q_heads, float scale, const void* gate,
+                            void* output, size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    const int status = check_gate(pool, gate, queries, output, rows);
+    if (status)
+        return status;
+    return append_decode_impl(pool, layer, keys, values, queries, q_heads, scale, output, rows,
+                              gate);
+}
+
+int ckv_sigmoid_mul(ckv_context* ctx, int dtype, const void* gate, const void* input,
+                    void* output, size_t count)
+{
+    if (!ctx)
+        return CKV_E_INVALID_ARGUMENT;
+    if (dtype != CKV_F32 && dtype != CKV_BF16 && dtype != CKV_F16)
+        return set_error(ctx, CKV_E_UNSUPPORTED_DTYPE, "dtype");
+    if (count && (!gate || !input || !output))
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "gate, input and output are required");
+    return run_kernel(ctx, "sigmoid_mul", [&] {
+        return launch_sigmoid_mul(ctx->stream, dtype, gate, input, output, count);
+    });
 }
 
 int ckv_copy_blocks(ckv_pool* pool, const uint32_t* src, const uint32_t* dst, size_t n)

@@ -69,6 +69,11 @@ struct profile_total {
     uint64_t launches = 0;
 };
 
+// ---- elementwise (kernels_rope.hip) ------------------------------------------------
+// out[i] = in[i] * sigmoid(gate[i]) over n elements of dtype (src/tensor/tensor_ops.cc:289-296)
+hipError_t launch_sigmoid_mul(hipStream_t s, int dtype, const void* gate, const void* in,
+                              void* out, uint64_t n);
+
 // ---- launchers (kernels_rope.hip) --------------------------------------------------
 // theta^(-2j/rotary) in float for j < rotary/2 (src/metal/metal_kernels.mm:186-191)
 void rope_frequencies(float theta, uint32_t rotary, rope_table& out);
@@ -195,18 +200,21 @@ hipError_t launch_expand_batch(hipStream_t s, const uint32_t* items, uint32_t n_
 // Returns hipErrorInvalidValue when no kernel fits the geometry. The fast
 // path (decode_fast_applies) merges in the workgroup and needs no partials;
 // the generic path writes partials for rows with several chunks.
+// gate (optional, same shape and dtype as out): out = attention * sigmoid(gate),
+// the sigmoid_mul of src/qwen/qwen_layer.cc:204 in the epilogue.
 hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                          const void* q, uint32_t q_heads, float scale, void* out,
-                         float* partials, int cu_count);
+                         float* partials, int cu_count, const void* gate = nullptr);
 bool decode_fast_applies(const pool_view& p, uint32_t q_heads, const void* q, const void* out);
 // store_kv + fast decode in one launch; the caller has checked
 // decode_fast_applies, 16-byte aligned inputs, and that every row's slot is
 // its position's slot with no two rows on one table range.
 hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_view& m,
                                 uint32_t layer, const void* k_in, const void* v_in, const void* q,
-                                uint32_t q_heads, float scale, void* out);
+                                uint32_t q_heads, float scale, void* out,
+                                const void* gate = nullptr);
 hipError_t launch_merge(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t q_heads,
-                        void* out, const float* partials);
+                        void* out, const float* partials, const void* gate = nullptr);
 bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads);
 // Floats per (work item, q head) partial record: [max, denominator, 0, 0, acc[head_dim]].
 uint32_t partial_record_floats(uint32_t head_dim);
@@ -216,7 +224,8 @@ uint32_t partial_record_floats(uint32_t head_dim);
 // 16-byte aligned pools, queries and output.
 bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, const void* out);
 hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
-                          const void* q, uint32_t q_heads, float scale, void* out);
+                          const void* q, uint32_t q_heads, float scale, void* out,
+                          const void* gate = nullptr);
 
 // ---- launchers (kernels_rope.hip) --------------------------------------------------
 // theta^(-2j/rotary) in float for j < rotary/2 (src/metal/metal_kernels.mm:186-191)

@@ -61,6 +61,22 @@ __device__ __forceinline__ uint32_t f16_bits(float x)
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
 
+// 1 / (1 + e^-g) in float, the gate of silu_mul_f32 with sigmoid_only
+// (src/metal/kernels/tensor_ops.metal:108-124): 0 and 1 at the extremes.
+__device__ __forceinline__ float sigmoid(float g)
+{
+    return 1.0f / (1.0f + fast_exp2(-g * log2e));
+}
+
+template <bool F16>
+__device__ __forceinline__ float half_value(uint16_t bits)
+{
+    if constexpr (F16)
+        return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+    else
+        return __builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16);
+}
+
 template <bool F16>
 struct half2_ops;
 
@@ -135,12 +151,14 @@ __host__ __device__ constexpr uint32_t record_floats(uint32_t head_dim)
 // 4j + group of the page (j = 0..3): four 1 KiB wave loads per page for K and
 // four for V. The wave's four row-group softmax states are merged with
 // shuffles, the W wave states through LDS, and the workgroup writes the
-// normalised output of the group's q heads.
-template <int G, bool F16, bool FUSED>
+// normalised output of the group's q heads. GATED multiplies it by
+// sigmoid(gate) first; the gate values are loaded when the workgroup starts,
+// so their latency hides behind the page loads.
+template <int G, bool F16, bool FUSED, bool GATED>
 __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg_kernel(
     pool_view p, meta_view m, uint32_t layer, const uint16_t* __restrict__ q, uint32_t q_heads,
     float scale_log2, uint16_t* __restrict__ out, const char* __restrict__ k_in,
-    const char* __restrict__ v_in)
+    const char* __restrict__ v_in, const uint16_t* __restrict__ gate)
 {
     using ops = half2_ops<F16>;
     constexpr uint32_t D = 128;
@@ -157,6 +175,11 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
     const uint32_t position = m.positions[row];
     const uint32_t n_pages = position / BS + 1;
     const uint32_t last_in_page = position % BS;
+    uint32_t gate_early = 0; // the first epilogue iteration's gate value (one register)
+    if constexpr (GATED) {
+        if (threadIdx.x < G * D)
+            gate_early = gate[((uint64_t)row * q_heads + kv_head * G) * D + threadIdx.x];
+    }
     const uint32_t row_bytes = p.features * 2u;
     const uint64_t page_bytes = (uint64_t)BS * row_bytes;
     const char* kl = static_cast<const char*>(p.keys) + (uint64_t)layer * p.layer_elems * 2u;
@@ -312,7 +335,8 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
         }
     }
     __syncthreads();
-    for (uint32_t t = threadIdx.x; t < G * D; t += blockDim.x) {
+    uint32_t it = 0;
+    for (uint32_t t = threadIdx.x; t < G * D; t += blockDim.x, ++it) {
         const uint32_t g = t / D;
         const uint32_t f = t % D;
         float M = -INFINITY;
@@ -325,9 +349,13 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
             d += lds_ml[(w * G + g) * 2 + 1] * weight;
             a += lds_acc[(w * G + g) * D + f] * weight;
         }
-        const float o = a / d;
-        out[((uint64_t)row * q_heads + kv_head * G + g) * D + f] =
-            static_cast<uint16_t>(F16 ? f16_bits(o) : bf16_bits(o));
+        const uint64_t at = ((uint64_t)row * q_heads + kv_head * G + g) * D + f;
+        float o = a / d;
+        if constexpr (GATED) {
+            const uint16_t gb = it == 0 ? (uint16_t)gate_early : gate[at];
+            o *= sigmoid(half_value<F16>(gb));
+        }
+        out[at] = static_cast<uint16_t>(F16 ? f16_bits(o) : bf16_bits(o));
     }
 }
 
@@ -374,7 +402,8 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(pool_view p, meta_vi
                                                             const void* __restrict__ q,
                                                             uint32_t q_heads, float scale_log2,
                                                             void* __restrict__ out,
-                                                            float* __restrict__ partials)
+                                                            float* __restrict__ partials,
+                                                            const void* __restrict__ gate)
 {
     constexpr int NF = generic_max_features_per_lane;
     const uint32_t H = p.kv_heads;
@@ -430,8 +459,12 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(pool_view p, meta_vi
         if (single) {
             for (int k = 0; k < NF; ++k) {
                 const uint32_t f = lane + 64 * k;
-                if (f < D)
-                    store_elem<DT>(out, q_base + f, acc[k] / den);
+                if (f < D) {
+                    float o = acc[k] / den;
+                    if (gate)
+                        o *= sigmoid(load_elem<DT>(gate, q_base + f));
+                    store_elem<DT>(out, q_base + f, o);
+                }
             }
         } else {
             float* rec = partials + ((uint64_t)item * q_heads + qh) * record_floats(D);
@@ -452,7 +485,8 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(pool_view p, meta_vi
 template <int DT>
 __global__ __launch_bounds__(64) void merge_kernel(meta_view m, uint32_t q_heads, uint32_t D,
                                                    const float* __restrict__ partials,
-                                                   void* __restrict__ out)
+                                                   void* __restrict__ out,
+                                                   const void* __restrict__ gate)
 {
     const uint32_t row = blockIdx.x / q_heads;
     const uint32_t qh = blockIdx.x % q_heads;
@@ -475,7 +509,10 @@ __global__ __launch_bounds__(64) void merge_kernel(meta_view m, uint32_t q_heads
         float a = 0.0f;
         for (uint32_t c = 0; c < n; ++c)
             a += rec0[c * item_stride + 4 + f] * fast_exp2(rec0[c * item_stride] - M);
-        store_elem<DT>(out, o_base + f, a * inv);
+        float o = a * inv;
+        if (gate)
+            o *= sigmoid(load_elem<DT>(gate, o_base + f));
+        store_elem<DT>(out, o_base + f, o);
     }
 }
 
@@ -502,7 +539,7 @@ uint32_t fast_waves(uint32_t group)
 template <int G>
 hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                        const void* q, uint32_t q_heads, float scale_log2, void* out, bool f16,
-                       const void* k_in, const void* v_in)
+                       const void* k_in, const void* v_in, const void* gate)
 {
     const uint32_t units = m.rows * p.kv_heads;
     const uint32_t waves = fast_waves(G);
@@ -512,20 +549,24 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
     const auto oo = static_cast<uint16_t*>(out);
     const auto ki = static_cast<const char*>(k_in);
     const auto vi = static_cast<const char*>(v_in);
-    if (k_in) {
-        if (f16)
-            decode_wg_kernel<G, true, true>
-                <<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo, ki, vi);
-        else
-            decode_wg_kernel<G, false, true>
-                <<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo, ki, vi);
-    } else {
-        if (f16)
-            decode_wg_kernel<G, true, false>
-                <<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo, ki, vi);
-        else
-            decode_wg_kernel<G, false, false>
-                <<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo, ki, vi);
+    const auto gg = static_cast<const uint16_t*>(gate);
+    // one instantiation per (dtype, fused, gated)
+    const int variant = (f16 ? 4 : 0) | (k_in ? 2 : 0) | (gate ? 1 : 0);
+    switch (variant) {
+#define CKV_FAST_CASE(V, F16_, FUSED_, GATED_)                                                 \
+    case V:                                                                                    \
+        decode_wg_kernel<G, F16_, FUSED_, GATED_>                                              \
+            <<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo, ki, vi, gg); \
+        break;
+        CKV_FAST_CASE(0, false, false, false)
+        CKV_FAST_CASE(1, false, false, true)
+        CKV_FAST_CASE(2, false, true, false)
+        CKV_FAST_CASE(3, false, true, true)
+        CKV_FAST_CASE(4, true, false, false)
+        CKV_FAST_CASE(5, true, false, true)
+        CKV_FAST_CASE(6, true, true, false)
+        CKV_FAST_CASE(7, true, true, true)
+#undef CKV_FAST_CASE
     }
     return hipGetLastError();
 }
@@ -546,7 +587,7 @@ bool decode_fast_applies(const pool_view& p, uint32_t q_heads, const void* q, co
 
 hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                          const void* q, uint32_t q_heads, float scale, void* out,
-                         float* partials, int cu_count)
+                         float* partials, int cu_count, const void* gate)
 {
     if (!m.rows)
         return hipSuccess;
@@ -556,16 +597,16 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
         switch (q_heads / p.kv_heads) {
         case 1:
             return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr);
+                                  nullptr, gate);
         case 2:
             return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr);
+                                  nullptr, gate);
         case 4:
             return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr);
+                                  nullptr, gate);
         default:
             return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr);
+                                  nullptr, gate);
         }
     }
     if (p.head_dim > 64u * generic_max_features_per_lane)
@@ -574,15 +615,15 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
     switch (p.dtype) {
     case CKV_F32:
         decode_generic_kernel<CKV_F32><<<grid, block, 0, s>>>(p, m, layer, q, q_heads, scale_log2,
-                                                              out, partials);
+                                                              out, partials, gate);
         break;
     case CKV_BF16:
         decode_generic_kernel<CKV_BF16><<<grid, block, 0, s>>>(p, m, layer, q, q_heads,
-                                                               scale_log2, out, partials);
+                                                               scale_log2, out, partials, gate);
         break;
     default:
         decode_generic_kernel<CKV_F16><<<grid, block, 0, s>>>(p, m, layer, q, q_heads, scale_log2,
-                                                              out, partials);
+                                                              out, partials, gate);
         break;
     }
     return hipGetLastError();
@@ -590,7 +631,7 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
 
 hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_view& m,
                                 uint32_t layer, const void* k_in, const void* v_in, const void* q,
-                                uint32_t q_heads, float scale, void* out)
+                                uint32_t q_heads, float scale, void* out, const void* gate)
 {
     if (!m.rows)
         return hipSuccess;
@@ -598,29 +639,29 @@ hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_vi
     const bool f16 = p.dtype == CKV_F16;
     switch (q_heads / p.kv_heads) {
     case 1:
-        return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in);
+        return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate);
     case 2:
-        return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in);
+        return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate);
     case 4:
-        return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in);
+        return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate);
     default:
-        return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in);
+        return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate);
     }
 }
 
 hipError_t launch_merge(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t q_heads,
-                        void* out, const float* partials)
+                        void* out, const float* partials, const void* gate)
 {
     const dim3 grid(m.rows * q_heads), block(64);
     switch (p.dtype) {
     case CKV_F32:
-        merge_kernel<CKV_F32><<<grid, block, 0, s>>>(m, q_heads, p.head_dim, partials, out);
+        merge_kernel<CKV_F32><<<grid, block, 0, s>>>(m, q_heads, p.head_dim, partials, out, gate);
         break;
     case CKV_BF16:
-        merge_kernel<CKV_BF16><<<grid, block, 0, s>>>(m, q_heads, p.head_dim, partials, out);
+        merge_kernel<CKV_BF16><<<grid, block, 0, s>>>(m, q_heads, p.head_dim, partials, out, gate);
         break;
     default:
-        merge_kernel<CKV_F16><<<grid, block, 0, s>>>(m, q_heads, p.head_dim, partials, out);
+        merge_kernel<CKV_F16><<<grid, block, 0, s>>>(m, q_heads, p.head_dim, partials, out, gate);
         break;
     }
     return hipGetLastError();

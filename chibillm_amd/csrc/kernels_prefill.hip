@@ -90,6 +90,21 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi)
         return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+template <bool F16>
+__device__ __forceinline__ float half_value(uint16_t bits)
+{
+    if constexpr (F16)
+        return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+    else
+        return __builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16);
+}
+
+// 1 / (1 + e^-g) in float (src/metal/kernels/tensor_ops.metal:108-124 with sigmoid_only)
+__device__ __forceinline__ float sigmoid(float g)
+{
+    return 1.0f / (1.0f + __builtin_amdgcn_exp2f(-g * log2e));
+}
+
 // Growth of the running maximum (log2 units) that forces a rescale. Below it
 // the probabilities keep using the older, smaller maximum and may reach
 // 2^rescale_log2 (exact in fp32 and in the 16-bit P operand's exponent
@@ -133,7 +148,7 @@ constexpr uint32_t wg_threads = 64 * (8 / QB);
 template <int G, int QB, bool F16>
 __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kernel(
     pool_view p, meta_view md, uint32_t layer, const uint16_t* __restrict__ q,
-    uint16_t* __restrict__ out, uint32_t q_heads, float c)
+    uint16_t* __restrict__ out, uint32_t q_heads, float c, const uint16_t* __restrict__ gate)
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[3 * stage_bytes];
     constexpr uint32_t tile_rows = 256 / G;
@@ -442,9 +457,17 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
             for (int quad = 0; quad < 4; ++quad) {
                 const uint32_t f = 32 * mt + 8 * quad + 4 * g;
                 const f32x16_t& acc = o[sb][mt];
+                float x[4] = { acc[4 * quad] * inv, acc[4 * quad + 1] * inv,
+                               acc[4 * quad + 2] * inv, acc[4 * quad + 3] * inv };
+                if (gate) { // sigmoid_mul (src/qwen/qwen_layer.cc:204) in the epilogue
+                    const uint2 gv = *reinterpret_cast<const uint2*>(gate + qoff[sb] + f);
+                    const uint32_t w[2] = { gv.x, gv.y };
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        x[e] *= sigmoid(half_value<F16>((uint16_t)(w[e / 2] >> (16 * (e % 2)))));
+                }
                 *reinterpret_cast<uint2*>(dst + f) =
-                    make_uint2(pack2<F16>(acc[4 * quad] * inv, acc[4 * quad + 1] * inv),
-                               pack2<F16>(acc[4 * quad + 2] * inv, acc[4 * quad + 3] * inv));
+                    make_uint2(pack2<F16>(x[0], x[1]), pack2<F16>(x[2], x[3]));
             }
     }
 }
@@ -455,17 +478,19 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
 
 template <int G>
 hipError_t launch_g(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
-                    const void* q, uint32_t q_heads, float c, void* out, uint32_t grid)
+                    const void* q, uint32_t q_heads, float c, void* out, uint32_t grid,
+                    const void* gate)
 {
     constexpr int QB = CKV_PREFILL_QB;
     const auto* qq = static_cast<const uint16_t*>(q);
     auto* oo = static_cast<uint16_t*>(out);
+    const auto* gg = static_cast<const uint16_t*>(gate);
     if (p.dtype == CKV_F16)
         hipLaunchKernelGGL((prefill_kernel<G, QB, true>), dim3(grid), dim3(wg_threads<QB>), 0, s,
-                           p, m, layer, qq, oo, q_heads, c);
+                           p, m, layer, qq, oo, q_heads, c, gg);
     else
         hipLaunchKernelGGL((prefill_kernel<G, QB, false>), dim3(grid), dim3(wg_threads<QB>), 0, s,
-                           p, m, layer, qq, oo, q_heads, c);
+                           p, m, layer, qq, oo, q_heads, c, gg);
     return hipGetLastError();
 }
 
@@ -489,7 +514,8 @@ bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, cons
 }
 
 hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
-                          const void* q, uint32_t q_heads, float scale, void* out)
+                          const void* q, uint32_t q_heads, float scale, void* out,
+                          const void* gate)
 {
     const uint32_t group = q_heads / p.kv_heads;
     const uint64_t grid = (uint64_t)m.n_tiles * group * p.kv_heads;
@@ -500,13 +526,13 @@ hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m,
     const float c = scale * log2e;
     switch (group) {
     case 1:
-        return launch_g<1>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid);
+        return launch_g<1>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
     case 2:
-        return launch_g<2>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid);
+        return launch_g<2>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
     case 4:
-        return launch_g<4>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid);
+        return launch_g<4>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
     case 8:
-        return launch_g<8>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid);
+        return launch_g<8>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
     default:
         return hipErrorInvalidValue;
     }

@@ -15,6 +15,7 @@
 // pair, so consecutive threads read and write consecutive elements.
 #include "ckv_internal.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace ckv {
@@ -216,7 +217,45 @@ hipError_t launch(hipStream_t s, int dtype, const void* in, void* out, uint32_t 
     return hipGetLastError();
 }
 
+// out = in * sigmoid(gate), elementwise in float (silu_mul_f32 with
+// sigmoid_only, src/metal/kernels/tensor_ops.metal:108-124); out may be in.
+template <int DT>
+__global__ __launch_bounds__(block_threads) void sigmoid_mul_kernel(const void* gate,
+                                                                   const void* in, void* out,
+                                                                   uint64_t n)
+{
+    using E = element<DT>;
+    using T = typename E::type;
+    const uint64_t stride = (uint64_t)gridDim.x * block_threads;
+    for (uint64_t i = (uint64_t)blockIdx.x * block_threads + threadIdx.x; i < n; i += stride) {
+        const float g = E::load(static_cast<const T*>(gate)[i]);
+        const float x = E::load(static_cast<const T*>(in)[i]);
+        static_cast<T*>(out)[i] = E::store(1.0f / (1.0f + __expf(-g)) * x);
+    }
+}
+
 } // namespace
+
+hipError_t launch_sigmoid_mul(hipStream_t s, int dtype, const void* gate, const void* in,
+                              void* out, uint64_t n)
+{
+    if (!n)
+        return hipSuccess;
+    const uint64_t want = (n + block_threads - 1) / block_threads;
+    const dim3 grid((uint32_t)std::min<uint64_t>(want, 65536));
+    switch (dtype) {
+    case CKV_F32:
+        sigmoid_mul_kernel<CKV_F32><<<grid, block_threads, 0, s>>>(gate, in, out, n);
+        break;
+    case CKV_BF16:
+        sigmoid_mul_kernel<CKV_BF16><<<grid, block_threads, 0, s>>>(gate, in, out, n);
+        break;
+    default:
+        sigmoid_mul_kernel<CKV_F16><<<grid, block_threads, 0, s>>>(gate, in, out, n);
+        break;
+    }
+    return hipGetLastError();
+}
 
 void rope_frequencies(float theta, uint32_t rotary, rope_table& out)
 {

@@ -284,6 +284,75 @@ store_kv_and_attend(hip_kv_cache& cache, const device_tensor& keys, const device
     return {};
 }
 
+namespace {
+
+// The gate is shaped and typed like the output ([rows, q_heads * head_dim]).
+result<void, tensor_op_error>
+validate_gate(const hip_kv_cache& cache, const device_tensor& gate, const device_tensor& output)
+{
+    CL_TRY(validate_layouts({ { gate, 2, cache_dtype(cache) } }));
+    if (gate.dims != output.dims)
+        return fail(tensor_op_errc::input_shape_mismatch);
+    return {};
+}
+
+} // namespace
+
+result<void, tensor_op_error>
+paged_attention_gated(hip_kv_cache& cache, const device_tensor& queries,
+                      const device_tensor& gate, std::size_t layer, std::size_t q_heads,
+                      device_tensor& output)
+{
+    std::size_t rows = 0;
+    CL_TRY_ASSIGN(rows, validate_attention(cache, queries, layer, q_heads, output));
+    CL_TRY(validate_gate(cache, gate, output));
+    const int rc = ckv_attention_gated(cache.pool(), layer, queries.data, q_heads,
+                                       attention_scale(cache), gate.data, output.data, rows);
+    if (rc)
+        return from_ckv(cache, rc);
+    return {};
+}
+
+result<void, tensor_op_error>
+store_kv_and_attend_gated(hip_kv_cache& cache, const device_tensor& keys,
+                          const device_tensor& values, const device_tensor& queries,
+                          const device_tensor& gate, std::size_t layer, std::size_t q_heads,
+                          device_tensor& output)
+{
+    std::size_t rows = 0;
+    CL_TRY_ASSIGN(rows, validate_store(cache, keys, values, layer));
+    std::size_t q_rows = 0;
+    CL_TRY_ASSIGN(q_rows, validate_attention(cache, queries, layer, q_heads, output));
+    if (q_rows != rows)
+        return fail(tensor_op_errc::position_count_mismatch);
+    CL_TRY(validate_gate(cache, gate, output));
+    const int rc = ckv_append_decode_gated(cache.pool(), layer, keys.data, values.data,
+                                           queries.data, q_heads, attention_scale(cache),
+                                           gate.data, output.data, rows);
+    if (rc)
+        return from_ckv(cache, rc);
+    return {};
+}
+
+result<void, tensor_op_error>
+sigmoid_mul(hip_kv_cache& cache, const device_tensor& gate, const device_tensor& input,
+            device_tensor& output)
+{
+    // validate_elementwise_output (src/tensor/tensor_ops.cc:17-43): layouts,
+    // then the input shapes, then the output's
+    const dtype t = cache_dtype(cache);
+    CL_TRY(validate_layouts({ { gate, 2, t }, { input, 2, t }, { output, 2, t } }));
+    if (input.dims != gate.dims)
+        return fail(tensor_op_errc::input_shape_mismatch);
+    if (output.dims != gate.dims)
+        return fail(tensor_op_errc::output_shape_mismatch);
+    const int rc = ckv_sigmoid_mul(cache.context().get(), static_cast<int>(cache.type()),
+                                   gate.data, input.data, output.data, gate.element_count());
+    if (rc)
+        return from_ckv(cache, rc);
+    return {};
+}
+
 result<void, tensor_op_error>
 rope(hip_kv_cache& cache, const device_tensor& input, std::size_t head_count, float theta,
      device_tensor& output, std::size_t rotary_dimension)

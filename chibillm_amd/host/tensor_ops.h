@@ -158,6 +158,28 @@ result<void, tensor_op_error> store_kv_and_attend(hip_kv_cache& cache, const dev
                                                   std::size_t query_head_count,
                                                   device_tensor& output);
 
+// The attention output's consumer in Qwen3.5 layers (src/qwen/qwen_layer.cc:183-206):
+// paged_attention then sigmoid_mul(gate, attended, attended), with the gate
+// applied in the attention epilogue. gate: [rows, q_heads * head_dim] of the
+// cache dtype (input_shape_mismatch otherwise), checked after the attention.
+result<void, tensor_op_error> paged_attention_gated(hip_kv_cache& cache,
+                                                    const device_tensor& queries,
+                                                    const device_tensor& gate, std::size_t layer,
+                                                    std::size_t query_head_count,
+                                                    device_tensor& output);
+result<void, tensor_op_error> store_kv_and_attend_gated(hip_kv_cache& cache,
+                                                        const device_tensor& keys,
+                                                        const device_tensor& values,
+                                                        const device_tensor& queries,
+                                                        const device_tensor& gate,
+                                                        std::size_t layer,
+                                                        std::size_t query_head_count,
+                                                        device_tensor& output);
+// sigmoid_mul (src/tensor/tensor_ops.h:131-135): output = input * sigmoid(gate),
+// rank-2 tensors of the cache dtype; output may be input.
+result<void, tensor_op_error> sigmoid_mul(hip_kv_cache& cache, const device_tensor& gate,
+                                          const device_tensor& input, device_tensor& output);
+
 // rope (src/tensor/tensor_ops.cc:356-410) on [rows, heads * head_dim] rows of
 // the cache dtype and head dimension at the uploaded positions; input may be
 // output. rotary_dimension 0 means the whole head.

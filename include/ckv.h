@@ -137,7 +137,7 @@ int ckv_copy_to_host(ckv_context* ctx, void* host_dst, const void* device_src, s
  * "gather_kv", "paged_attention_decode", "paged_attention_merge", "append_decode",
  * "paged_attention_prefill", "copy_blocks", "checkpoint_pack",
  * "checkpoint_unpack", "tables_patch", "tables_fill", "batch_expand", "rope",
- * "rope_append". */
+ * "rope_append", "sigmoid_mul". */
 int ckv_profile_enable(ckv_context* ctx, int enabled);
 int ckv_profile_query(ckv_context* ctx, const char* kernel, double* total_ms,
                       uint64_t* launches);
@@ -279,6 +279,28 @@ int ckv_prefill_attention(ckv_pool* pool, size_t layer, const void* queries, siz
  * the prefill form when some query tile has more than one row, else decode. */
 int ckv_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
                   float scale, void* output, size_t rows);
+
+/* ---- The attention output's consumer: the Qwen3.5 sigmoid gate ---------------
+ * src/qwen/qwen_layer.cc:183-206 splits the projected query into query and
+ * gate (split_heads), attends, then sigmoid_mul(gate, attended, attended) and
+ * feeds the result to linear_add. The gated forms apply the gate in the
+ * attention epilogue, to the float result before its one rounding:
+ * output = attention * 1 / (1 + e^-gate) (silu_mul_f32 with sigmoid_only,
+ * src/metal/kernels/tensor_ops.metal:108-124). gate is a device array shaped
+ * like output ([rows, q_heads * head_dim], pool dtype); it must not be the
+ * queries' or the output's memory (unsupported_aliasing), and is required when
+ * rows > 0 (invalid_argument). Otherwise as ckv_attention / ckv_append_decode. */
+int ckv_attention_gated(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
+                        float scale, const void* gate, void* output, size_t rows);
+int ckv_append_decode_gated(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+                            const void* queries, size_t q_heads, float scale, const void* gate,
+                            void* output, size_t rows);
+/* sigmoid_mul (src/tensor/tensor_ops.h:131-135, src/tensor/tensor_ops.cc:289-296):
+ * output[i] = input[i] * sigmoid(gate[i]) over count device elements of dtype,
+ * computed in float; output may be input. The unfused form of the gate.
+ * Checks: unsupported_dtype, invalid_argument (null arrays with count > 0). */
+int ckv_sigmoid_mul(ckv_context* ctx, int dtype, const void* gate, const void* input,
+                    void* output, size_t count);
 
 /* ---- Rotary position embedding ------------------------------------------------------ */
 /* rope (src/tensor/tensor_ops.cc:356-410; kernel rope_f32,

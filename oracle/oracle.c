@@ -780,6 +780,28 @@ int orc_rope(const void* in, void* out, int dtype, size_t rows, size_t heads, si
     return 0;
 }
 
+/* ---- Attention-output gate -------------------------------------------------- */
+
+/* silu_mul_f32 with sigmoid_only (src/metal/kernels/tensor_ops.metal:108-124):
+ * out = (1 / (1 + exp(-gate))) * in, in float, elementwise. */
+void orc_sigmoid_mul(const void* gate, const void* in, void* out, size_t n, int dtype)
+{
+    float* g = malloc((n ? n : 1) * sizeof(float));
+    float* x = malloc((n ? n : 1) * sizeof(float));
+    if (!g || !x) {
+        free(g);
+        free(x);
+        return;
+    }
+    orc_convert_to_f32(gate, g, n, dtype);
+    orc_convert_to_f32(in, x, n, dtype);
+    for (size_t i = 0; i < n; ++i)
+        x[i] = (1.0f / (1.0f + expf(-g[i]))) * x[i];
+    orc_convert_from_f32(x, out, n, dtype);
+    free(g);
+    free(x);
+}
+
 /* ---- Threaded CPU baseline -------------------------------------------------- */
 
 typedef struct {

@@ -158,6 +158,18 @@ void orc_copy_prefix(void* paged, void* packed, const uint32_t* blocks, const or
 void orc_copy_blocks(void* key_cache, void* value_cache, const orc_geometry* g,
                      const uint32_t* src, const uint32_t* dst, size_t n, size_t elem_size);
 
+/* ---- Rotary position embedding (src/metal/kernels/tensor_ops.metal:158-195) */
+/* inv_freq[j] = theta^(-2j/rotary_dim) in float (src/metal/metal_kernels.mm:186-191). */
+void orc_rope_frequencies(float theta, size_t rotary_dim, float* out);
+/* Split-half rotation of [rows, heads*head_dim] rows of dtype at positions;
+ * rotary_dim 0 means head_dim. Returns -1 on invalid arguments. */
+int orc_rope(const void* in, void* out, int dtype, size_t rows, size_t heads, size_t head_dim,
+             const uint32_t* positions, float theta, size_t rotary_dim);
+
+/* ---- Attention-output gate (src/metal/kernels/tensor_ops.metal:108-124) -- */
+/* out = (1 / (1 + exp(-gate))) * in, float math, rounded once; out may be in. */
+void orc_sigmoid_mul(const void* gate, const void* in, void* out, size_t n, int dtype);
+
 /* ---- Timing helper for the CPU baseline --------------------------------- */
 /* Decode attention for every row, parallel over (row, kv_head) on `threads`
  * host threads, same arithmetic as orc_attention_online but the two q heads of

@@ -98,6 +98,8 @@ def lib() -> C.CDLL:
         L.orc_copy_blocks.argtypes = [_vp, _vp, C.POINTER(Geometry), _u32p, _u32p, _size_t,
                                       _size_t]
         L.orc_rope_frequencies.argtypes = [C.c_float, _size_t, _vp]
+        L.orc_sigmoid_mul.argtypes = [_vp, _vp, _vp, _size_t, C.c_int]
+        L.orc_sigmoid_mul.restype = None
         L.orc_rope.argtypes = [_vp, _vp, C.c_int, _size_t, _size_t, _size_t, _u32p, C.c_float,
                                _size_t]
         _lib = L
@@ -252,6 +254,17 @@ def copy_blocks(key_cache, value_cache, geom: tuple, src, dst) -> None:
 
 
 # ---- rotary position embedding ---------------------------------------------------
+
+def sigmoid_mul(gate: np.ndarray, x: np.ndarray, dtype: int) -> np.ndarray:
+    """sigmoid_mul (src/tensor/tensor_ops.cc:289-296): x * sigmoid(gate) in float,
+    arrays of `dtype` (float32 or 16-bit bit patterns), rounded once."""
+    g = np.ascontiguousarray(gate, dtype=_np_dtype(dtype))
+    a = np.ascontiguousarray(x, dtype=_np_dtype(dtype))
+    assert g.shape == a.shape
+    out = np.empty_like(a)
+    lib().orc_sigmoid_mul(g.ctypes.data, a.ctypes.data, out.ctypes.data, a.size, dtype)
+    return out
+
 
 def rope_frequencies(theta: float, rotary_dim: int) -> np.ndarray:
     out = np.empty(max(rotary_dim // 2, 1), dtype=np.float32)

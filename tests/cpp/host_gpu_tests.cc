@@ -302,6 +302,57 @@ TEST("tensor ops: paged attention validates inputs and metadata")
                    tensor_op_errc::cache_block_out_of_range));
 }
 
+TEST("tensor ops: attention gates use sigmoid and apply in the attention epilogue")
+{
+    // tests/tensor_ops_test.cc:513-539: sigmoid_mul of the gate {0, 1, -1, 2, -1000, 1000, 0, -2}
+    // on {1..8}, in place
+    auto c = make_cache(tiny());
+    const std::array<float, 8> g { 0, 1, -1, 2, -1000, 1000, 0, -2 };
+    const std::array<float, 8> x { 1, 2, 3, 4, 5, 6, 7, 8 };
+    auto gb = upload(g.data(), 32), xb = upload(x.data(), 32);
+    auto xv = view(xb, dtype::f32, { 2, 4 });
+    REQUIRE(sigmoid_mul(c, view(gb, dtype::f32, { 2, 4 }), xv, xv));
+    const auto got = download<float>(xb, 8);
+    const std::array<float, 8> want { 0.5f, 2 / (1 + std::exp(-1.0f)), 3 / (1 + std::exp(1.0f)),
+                                      4 / (1 + std::exp(-2.0f)), 0.0f, 6.0f, 3.5f,
+                                      8 / (1 + std::exp(2.0f)) };
+    for (int i = 0; i < 8; ++i)
+        CHECK(std::fabs(got[i] - want[i]) <= 1e-5f * std::fabs(want[i]));
+    CHECK(got[4] == 0.0f && got[5] == 6.0f);
+    auto packed = view(gb, dtype::f32, { 1, 8 });
+    CHECK(error_is(sigmoid_mul(c, packed, xv, xv), tensor_op_errc::input_shape_mismatch));
+    auto short_out = view(xb, dtype::f32, { 1, 4 });
+    CHECK(error_is(sigmoid_mul(c, view(gb, dtype::f32, { 2, 4 }), xv, short_out),
+                   tensor_op_errc::output_shape_mismatch));
+    CHECK(error_is(sigmoid_mul(c, view(gb, dtype::bf16, { 2, 4 }), xv, xv),
+                   tensor_op_errc::unsupported_dtype));
+
+    // the gated attention of the known answer above: output * sigmoid(gate)
+    write_cache(c, c.keys(), std::vector<float> { 1, 1, 0, 0, 1, 0, 0, 1, 0, 0, 0, 0, 0, 0, 0, 0 });
+    write_cache(c, c.values(), std::vector<float> { 30, 3, 0, 0, 10, 1, 20, 2, 0, 0, 0, 0, 0, 0, 0, 0 });
+    const std::array<float, 4> q { 1, 0, 0, 1 }, gate { 0, 1, -1, 1000 };
+    auto qb = upload(q.data(), 16), gateb = upload(gate.data(), 16);
+    auto ob = device_buffer::make(gpu(), 16);
+    REQUIRE(ob);
+    const std::vector<std::uint32_t> pos { 2 }, table { 1, 0 }, off { 0 }, len { 2 };
+    REQUIRE(upload_attention_metadata(c, { pos, {}, table, off, len }));
+    auto out = view(*ob, dtype::f32, { 1, 4 });
+    REQUIRE(paged_attention_gated(c, view(qb, dtype::f32, { 1, 4 }),
+                                  view(gateb, dtype::f32, { 1, 4 }), 0, 2, out));
+    const float e = std::exp(1.0f / std::sqrt(2.0f));
+    const float d = 2 * e + 1;
+    const std::array<float, 4> plain { (40 * e + 20) / d, (4 * e + 2) / d, (10 + 50 * e) / d,
+                                       (1 + 5 * e) / d };
+    const auto o = download<float>(*ob, 4);
+    for (int i = 0; i < 4; ++i) {
+        const float w = plain[i] / (1 + std::exp(-gate[i]));
+        CHECK(std::fabs(o[i] - w) <= 1e-5f * std::fabs(w));
+    }
+    CHECK(error_is(paged_attention_gated(c, view(qb, dtype::f32, { 1, 4 }),
+                                         view(gateb, dtype::f32, { 1, 2 }), 0, 2, out),
+                   tensor_op_errc::input_shape_mismatch));
+}
+
 // ---- shared prefixes on the device --------------------------------------------------------
 
 namespace {
@@ -463,7 +514,8 @@ close_rows(const std::vector<std::vector<float>>& a, const std::vector<std::vect
 TEST("shared prefix: a restored prefix attends like a cold prefill and copies only its tail")
 {
     for (std::size_t prefix : { 40, 48 }) { // a partial tail page, then an exact page boundary
-        for (auto sharing : { prefix_sharing::shared_pages, prefix_sharing::packed_copy }) {
+        for (auto sharing : { prefix_sharing::shared_pages, prefix_sharing::packed_copy,
+                              prefix_sharing::host_copy }) {
             kv_path_runner warm;
             warm.sharing = sharing;
             auto engine = inference_engine::make(shared_config(), warm);

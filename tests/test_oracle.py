@@ -514,3 +514,39 @@ def test_rope_frequencies_and_invariants():
     yb = orc.rope(xb, orc.BF16, 4, pos, 1e6)
     assert np.array_equal(yb, orc.from_f32(orc.rope(orc.to_f32(xb, orc.BF16), orc.F32, 4, pos,
                                                     1e6), orc.BF16))
+
+
+# ---- the attention-output gate -------------------------------------------------
+
+def test_sigmoid_mul_known_answer():
+    # tests/tensor_ops_test.cc:513-539: gate {0, 1, -1, 2, -1000, 1000, 0, -2} on
+    # query {1..8}; sigmoid(+-1000) is exactly 1 and 0
+    gate = np.array([0, 1, -1, 2, -1000, 1000, 0, -2], np.float32)
+    query = np.arange(1, 9, dtype=np.float32)
+    got = orc.sigmoid_mul(gate, query, orc.F32)
+    expected = [0.5, 2 / (1 + math.exp(-1)), 3 / (1 + math.exp(1)), 4 / (1 + math.exp(-2)),
+                0.0, 6.0, 3.5, 8 / (1 + math.exp(2))]
+    assert approx(got, expected, 1e-5)
+    assert got[4] == 0.0 and got[5] == 6.0
+
+
+def test_sigmoid_mul_against_torch_and_rounding():
+    # an independent routine: torch.sigmoid in float64, then one rounding to
+    # the storage type; 16-bit results within one unit in the last place
+    rng = np.random.default_rng(5)
+    g = rng.normal(0, 4, 4096).astype(np.float32)
+    x = rng.normal(0, 1, 4096).astype(np.float32)
+    ref = torch.sigmoid(torch.from_numpy(g).double()) * torch.from_numpy(x).double()
+    got = orc.sigmoid_mul(g, x, orc.F32)
+    assert np.allclose(got, ref.numpy(), rtol=4e-7, atol=1e-30)
+    for code in (orc.BF16, orc.F16):
+        gb, xb = orc.from_f32(g, code), orc.from_f32(x, code)
+        ref16 = (torch.sigmoid(torch.from_numpy(orc.to_f32(gb, code)).double())
+                 * torch.from_numpy(orc.to_f32(xb, code)).double()).numpy()
+        got16 = orc.sigmoid_mul(gb, xb, code)
+        expect_bits = orc.from_f32(ref16.astype(np.float32), code)
+        a = got16.astype(np.int32)
+        b = expect_bits.astype(np.int32)
+        a = np.where(a & 0x8000, -(a & 0x7FFF), a)
+        b = np.where(b & 0x8000, -(b & 0x7FFF), b)
+        assert np.abs(a - b).max() <= 1

@@ -52,7 +52,27 @@ constexpr uint32_t k_row_bytes = 272;  // 256 + 16: rows 0..7 start in distinct 
 constexpr uint32_t vt_row_bytes = 80;  // 64 + 16: likewise for 8 consecutive feature rows
 constexpr uint32_t k_bytes = block_keys * k_row_bytes;
 constexpr uint32_t vt_bytes = dim * vt_row_bytes;
-constexpr uint32_t stage_bytes = k_bytes + vt_bytes;
+
+#ifndef CKV_PREFILL_VDMA
+#define CKV_PREFILL_VDMA 1
+#endif
+// V staged by LDS DMA (global_load_lds_dwordx4) in its natural [key][feature]
+// layout and read transposed (ds_read_b64_tr_b16) into the A operand of
+// O^T += V^T P^T, instead of through registers and a transposing store.
+// A block's 32 key rows sit in 8 DMA groups of 4 rows (one 1 KiB wave
+// instruction each) with 64 bytes after each group: key k is row (k/4)%4 of
+// group k%4 + 4*(k/16), so the 8 keys one transposed read touches start at 4
+// different bank offsets.
+constexpr bool v_dma = CKV_PREFILL_VDMA != 0;
+constexpr uint32_t vg_bytes = 1024 + 64;
+constexpr uint32_t v_stage_bytes = v_dma ? 8 * vg_bytes : vt_bytes;
+constexpr uint32_t stage_bytes = k_bytes + v_stage_bytes;
+
+// The source of masked (past the tile's last position) V rows under DMA:
+// zeros, so that their zero probabilities multiply finite values.
+__device__ const uint4 zero_row[16] = {};
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
 // LDS row of physical key `key` in a block (an involution: bits 2 and 3 swapped).
 __device__ __forceinline__ uint32_t key_row(uint32_t key)
@@ -209,35 +229,64 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
     // Staging roles over 256 threads: K rows t/16 and 16 + t/16, chunk t%16;
     // V key pair t/16, chunk t%16. With 512 threads the first 256 stage V
     // and the other 256 stage K (wave-uniform).
-    const uint32_t st_tid = tid & 255;
-    const bool k_role = QB == 2 || tid >= 256;
-    const bool v_role = QB == 2 || tid < 256;
+    // With V by DMA, every one of the 512 threads stages one K chunk (row
+    // t/16, chunk t%16) and wave w issues V DMA group w.
+    static_assert(!v_dma || QB == 1, "V by DMA needs eight waves");
+    const uint32_t st_tid = v_dma ? tid : tid & 255;
+    const bool k_role = v_dma || QB == 2 || tid >= 256;
+    const bool v_role = !v_dma && (QB == 2 || tid < 256);
     const uint32_t srow = st_tid >> 4, chunk = st_tid & 15;
+    // V DMA: this lane's key of its wave's group and its LDS read offset
+    const uint32_t vd_key = 16 * (wave >> 2) + 4 * (lane >> 4) + (wave & 3);
+    const uint32_t vd_src = (vd_key & 15) * F + (lane & 15) * 8;
+    const uint32_t vr_off = ((lane & 15) >> 2) * vg_bytes + (lane >> 5) * 512
+        + ((lane >> 4) & 1) * 32 + (lane & 3) * 8;
 
     // Loads are unconditional so the compiler can keep them in flight across
     // the block's compute: a key past the tile's last position is read from a
     // slot of the block's first page (always in the table) and replaced by
     // zero when staged.
     uint4 kr[2], vr[2];
+    auto stage_of = [&](uint32_t kb) { return lds + (kb % 3) * stage_bytes; };
     // The block table entries of a block are read one block before its K/V
     // loads are issued, so that dependent load never stalls the wave.
+    // The loads are issued a block ahead and their values taken (made
+    // uniform) only when that block's K/V loads are issued, so the wait for
+    // them falls on the previous iteration's drain, not on this wave's path.
     uint32_t key0_next = 0;
-    uint32_t page_a = 0, page_b = 0; // pages of the next block to load
+    uint32_t page_a = 0, page_b = 0; // table entries of the next block to load, in flight
     auto fetch_pages = [&](uint32_t kb) {
         if (kb < n_blocks) {
             const uint32_t key0 = kb * block_keys;
-            page_a = __builtin_amdgcn_readfirstlane(table[2 * kb]);
-            page_b = key0 + page_tokens <= pos_last
-                ? __builtin_amdgcn_readfirstlane(table[2 * kb + 1])
-                : page_a;
+            page_a = table[2 * kb];
+            // the block's second page, or its first when the tile ends in the first
+            page_b = table[2 * kb + (key0 + page_tokens <= pos_last ? 1 : 0)];
         }
     };
     auto load_block = [&](uint32_t kb) {
         const uint32_t key0 = kb * block_keys;
         key0_next = key0;
-        const uint32_t pg0 = page_a, pg1 = page_b;
+        const uint32_t pg0 = __builtin_amdgcn_readfirstlane(page_a);
+        const uint32_t pg1 = __builtin_amdgcn_readfirstlane(page_b);
         fetch_pages(kb + 1);
-        if (k_role) {
+        if constexpr (v_dma) {
+            const size_t slot = (size_t)(srow < 16 ? pg0 : pg1) * page_tokens + (srow & 15);
+            kr[0] = *reinterpret_cast<const uint4*>(kbase + slot * F + chunk * 8);
+            // V straight into the block's stage (last read two iterations ago)
+            const uint16_t* src = key0 + vd_key <= pos_last
+                ? vbase + (size_t)(wave >> 2 ? pg1 : pg0) * page_tokens * F + vd_src
+                : reinterpret_cast<const uint16_t*>(zero_row) + (lane & 15) * 8;
+            // Issued as inline assembly: the compiler would otherwise wait for
+            // this asynchronous LDS write before every later LDS read. Its
+            // completion is awaited explicitly (vmcnt) before the barrier
+            // that publishes the stage; nothing reads the stage before that.
+            const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(
+                (__attribute__((address_space(3))) uint8_t*)(stage_of(kb) + k_bytes + wave * vg_bytes)));
+            asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                         :
+                         : "v"(src), "s"(dst)
+                         : "m0");
+        } else if (k_role) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const size_t slot = (size_t)(i ? pg1 : pg0) * page_tokens + srow;
@@ -261,6 +310,13 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
         return make_uint4(v.x & k, v.y & k, v.z & k, v.w & k);
     };
     auto store_block = [&](uint8_t* st) {
+        if constexpr (v_dma) {
+            *reinterpret_cast<uint4*>(st + key_row(srow) * k_row_bytes + chunk * 16) =
+                masked(kr[0], key0_next + srow <= pos_last);
+            // this wave's V DMA has landed before the barrier that follows
+            __builtin_amdgcn_s_waitcnt(0);
+            return;
+        }
         if (k_role) {
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -305,7 +361,6 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
     // the next block is staged. The two halves of each iteration have no
     // dependence between their matrix and vector work, so one wave keeps
     // both units busy.
-    auto stage_of = [&](uint32_t kb) { return lds + (kb % 3) * stage_bytes; };
     f32x16_t sc[QB];      // S^T(kb), written by the matrix core
     f32x16_t sp[QB];      // S^T(kb - 1), its maxima taken, awaiting exponentials
     float mx[QB];
@@ -326,6 +381,28 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
             ka[ks] = *reinterpret_cast<const uint4*>(krow + ks * 32);
     };
     auto read_v = [&](uint32_t kb, uint4 (&va)[4][2]) {
+        if constexpr (v_dma) {
+            // lane (n, g) of the A operand: features 32mt + n, keys 16h + 8g + 0..7,
+            // two transposed reads of keys 4 at a time
+            // one base register per block; the 16 reads add immediate offsets
+            uint32_t vaddr = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) uint8_t*)(
+                                 stage_of(kb) + k_bytes))
+                + vr_off;
+            asm volatile("" : "+v"(vaddr));
+            auto* vb = (__attribute__((address_space(3))) uint8_t*)(uintptr_t)vaddr;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) i16x4_t*)(vb + 4 * h * vg_bytes + 64 * mt));
+                    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) i16x4_t*)(vb + 4 * h * vg_bytes + 256 + 64 * mt));
+                    const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+                    va[mt][h] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+                }
+            return;
+        }
         const uint8_t* vt = stage_of(kb) + k_bytes + g * 16;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)

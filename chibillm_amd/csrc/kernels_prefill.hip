@@ -53,6 +53,12 @@ constexpr uint32_t vt_row_bytes = 80;  // 64 + 16: likewise for 8 consecutive fe
 constexpr uint32_t k_bytes = block_keys * k_row_bytes;
 constexpr uint32_t vt_bytes = dim * vt_row_bytes;
 
+#ifndef CKV_PREFILL_PRIO
+#define CKV_PREFILL_PRIO 0
+#endif
+#ifndef CKV_PREFILL_KSCALAR
+#define CKV_PREFILL_KSCALAR 1
+#endif
 #ifndef CKV_PREFILL_VDMA
 #define CKV_PREFILL_VDMA 1
 #endif
@@ -236,6 +242,7 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
     const bool k_role = v_dma || QB == 2 || tid >= 256;
     const bool v_role = !v_dma && (QB == 2 || tid < 256);
     const uint32_t srow = st_tid >> 4, chunk = st_tid & 15;
+    const uint32_t k_lane_off = (srow & 15) * F + chunk * 8;
     // V DMA: this lane's key of its wave's group and its LDS read offset
     const uint32_t vd_key = 16 * (wave >> 2) + 4 * (lane >> 4) + (wave & 3);
     const uint32_t vd_src = (vd_key & 15) * F + (lane & 15) * 8;
@@ -270,11 +277,17 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
         const uint32_t pg1 = __builtin_amdgcn_readfirstlane(page_b);
         fetch_pages(kb + 1);
         if constexpr (v_dma) {
+#if CKV_PREFILL_KSCALAR
+            // rows 0..15 (waves 0..3) read the first page, rows 16..31 the second
+            const uint16_t* kpage = kbase + (size_t)(wave < 4 ? pg0 : pg1) * (page_tokens * F);
+            kr[0] = *reinterpret_cast<const uint4*>(kpage + k_lane_off);
+#else
             const size_t slot = (size_t)(srow < 16 ? pg0 : pg1) * page_tokens + (srow & 15);
             kr[0] = *reinterpret_cast<const uint4*>(kbase + slot * F + chunk * 8);
+#endif
             // V straight into the block's stage (last read two iterations ago)
             const uint16_t* src = key0 + vd_key <= pos_last
-                ? vbase + (size_t)(wave >> 2 ? pg1 : pg0) * page_tokens * F + vd_src
+                ? vbase + (size_t)(wave >> 2 ? pg1 : pg0) * (page_tokens * F) + vd_src
                 : reinterpret_cast<const uint16_t*>(zero_row) + (lane & 15) * 8;
             // Issued as inline assembly: the compiler would otherwise wait for
             // this asynchronous LDS write before every later LDS read. Its
@@ -496,9 +509,15 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
             uint4 pt[QB][2];
             read_k(kb, ka);
             probabilities(pt); // vector: block kb - 1
+#if CKV_PREFILL_PRIO
+            __builtin_amdgcn_s_setprio(1);
+#endif
             qk(kb, ka);        // matrix: block kb
             read_v(kb - 1, va);
             pv(va, pt);        // matrix: block kb - 1
+#if CKV_PREFILL_PRIO
+            __builtin_amdgcn_s_setprio(0);
+#endif
             grew = stats(kb);  // vector: block kb
             if (kb + 1 < n_blocks)
                 store_block(stage_of(kb + 1));

@@ -53,12 +53,6 @@ constexpr uint32_t vt_row_bytes = 80;  // 64 + 16: likewise for 8 consecutive fe
 constexpr uint32_t k_bytes = block_keys * k_row_bytes;
 constexpr uint32_t vt_bytes = dim * vt_row_bytes;
 
-#ifndef CKV_PREFILL_PRIO
-#define CKV_PREFILL_PRIO 0
-#endif
-#ifndef CKV_PREFILL_KSCALAR
-#define CKV_PREFILL_KSCALAR 1
-#endif
 #ifndef CKV_PREFILL_VDMA
 #define CKV_PREFILL_VDMA 1
 #endif
@@ -72,13 +66,37 @@ constexpr uint32_t vt_bytes = dim * vt_row_bytes;
 constexpr bool v_dma = CKV_PREFILL_VDMA != 0;
 constexpr uint32_t vg_bytes = 1024 + 64;
 constexpr uint32_t v_stage_bytes = v_dma ? 8 * vg_bytes : vt_bytes;
-constexpr uint32_t stage_bytes = k_bytes + v_stage_bytes;
+// K by DMA: already in the A-operand order of S^T = K.Q^T. Region ks (1 KiB)
+// holds, at 16-byte slot l, what lane l = 32g + n reads for step ks: features
+// 16ks + 8g .. +7 of LDS row n (physical key key_row(n)). Each wave fills
+// one region with one DMA instruction, and every operand read is
+// lane * 16 + ks * 1024, 256 contiguous bytes per 16 lanes.
+constexpr uint32_t k_stage_bytes = v_dma ? 8 * 1024 : k_bytes;
+constexpr uint32_t stage_bytes = k_stage_bytes + v_stage_bytes;
 
 // The source of masked (past the tile's last position) V rows under DMA:
 // zeros, so that their zero probabilities multiply finite values.
 __device__ const uint4 zero_row[16] = {};
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+// One 16-byte LDS DMA per lane: lane l's 16 bytes at `src` land at LDS byte
+// address lds + 16 * l. Written out rather than through the compiler builtin,
+// which makes the compiler wait for every outstanding DMA before any later
+// LDS read; here completion is awaited explicitly (vmcnt) before the barrier
+// that publishes the data. M0 (the LDS base) is saved and restored around
+// the load, with the wait state its write needs before the load reads it.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds)
+{
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %2\n\t"
+                 "s_nop 0\n\t"
+                 "global_load_lds_dwordx4 %1, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(src), "s"(lds));
+}
 
 // LDS row of physical key `key` in a block (an involution: bits 2 and 3 swapped).
 __device__ __forceinline__ uint32_t key_row(uint32_t key)
@@ -242,7 +260,10 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
     const bool k_role = v_dma || QB == 2 || tid >= 256;
     const bool v_role = !v_dma && (QB == 2 || tid < 256);
     const uint32_t srow = st_tid >> 4, chunk = st_tid & 15;
-    const uint32_t k_lane_off = (srow & 15) * F + chunk * 8;
+    // K DMA: this lane's key (LDS row lane % 32) and features in its wave's region
+    const uint32_t k_key = key_row(lane & 31);
+    const uint32_t k_feat = 16 * wave + 8 * (lane >> 5);
+    const uint32_t k_src = (k_key & 15) * F + k_feat;
     // V DMA: this lane's key of its wave's group and its LDS read offset
     const uint32_t vd_key = 16 * (wave >> 2) + 4 * (lane >> 4) + (wave & 3);
     const uint32_t vd_src = (vd_key & 15) * F + (lane & 15) * 8;
@@ -277,28 +298,19 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
         const uint32_t pg1 = __builtin_amdgcn_readfirstlane(page_b);
         fetch_pages(kb + 1);
         if constexpr (v_dma) {
-#if CKV_PREFILL_KSCALAR
-            // rows 0..15 (waves 0..3) read the first page, rows 16..31 the second
-            const uint16_t* kpage = kbase + (size_t)(wave < 4 ? pg0 : pg1) * (page_tokens * F);
-            kr[0] = *reinterpret_cast<const uint4*>(kpage + k_lane_off);
-#else
-            const size_t slot = (size_t)(srow < 16 ? pg0 : pg1) * page_tokens + (srow & 15);
-            kr[0] = *reinterpret_cast<const uint4*>(kbase + slot * F + chunk * 8);
-#endif
+            // K region `wave` of the block's stage
+            const uint16_t* ksrc = key0 + k_key <= pos_last
+                ? kbase + (size_t)((lane & 31) < 16 ? pg0 : pg1) * (page_tokens * F) + k_src
+                : reinterpret_cast<const uint16_t*>(zero_row) + k_feat;
+            dma16(ksrc, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(
+                            (__attribute__((address_space(3))) uint8_t*)(stage_of(kb) + wave * 1024))));
             // V straight into the block's stage (last read two iterations ago)
             const uint16_t* src = key0 + vd_key <= pos_last
                 ? vbase + (size_t)(wave >> 2 ? pg1 : pg0) * (page_tokens * F) + vd_src
                 : reinterpret_cast<const uint16_t*>(zero_row) + (lane & 15) * 8;
-            // Issued as inline assembly: the compiler would otherwise wait for
-            // this asynchronous LDS write before every later LDS read. Its
-            // completion is awaited explicitly (vmcnt) before the barrier
-            // that publishes the stage; nothing reads the stage before that.
-            const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(
-                (__attribute__((address_space(3))) uint8_t*)(stage_of(kb) + k_bytes + wave * vg_bytes)));
-            asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-                         :
-                         : "v"(src), "s"(dst)
-                         : "m0");
+            dma16(src, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(
+                           (__attribute__((address_space(3))) uint8_t*)(
+                               stage_of(kb) + k_stage_bytes + wave * vg_bytes))));
         } else if (k_role) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -324,9 +336,8 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
     };
     auto store_block = [&](uint8_t* st) {
         if constexpr (v_dma) {
-            *reinterpret_cast<uint4*>(st + key_row(srow) * k_row_bytes + chunk * 16) =
-                masked(kr[0], key0_next + srow <= pos_last);
-            // this wave's V DMA has landed before the barrier that follows
+            (void)st;
+            // this wave's K and V DMA have landed before the barrier that follows
             __builtin_amdgcn_s_waitcnt(0);
             return;
         }
@@ -388,6 +399,13 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
                 sc[sb] = mfma<F16>(ka[ks], qr[sb][ks], sc[sb]);
     };
     auto read_k = [&](uint32_t kb, uint4 (&ka)[8]) {
+        if constexpr (v_dma) {
+            const uint8_t* kl = stage_of(kb) + lane * 16;
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks)
+                ka[ks] = *reinterpret_cast<const uint4*>(kl + ks * 1024);
+            return;
+        }
         const uint8_t* krow = stage_of(kb) + n * k_row_bytes + g * 16;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks)
@@ -399,7 +417,7 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
             // two transposed reads of keys 4 at a time
             // one base register per block; the 16 reads add immediate offsets
             uint32_t vaddr = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) uint8_t*)(
-                                 stage_of(kb) + k_bytes))
+                                 stage_of(kb) + k_stage_bytes))
                 + vr_off;
             asm volatile("" : "+v"(vaddr));
             auto* vb = (__attribute__((address_space(3))) uint8_t*)(uintptr_t)vaddr;
@@ -509,15 +527,9 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
             uint4 pt[QB][2];
             read_k(kb, ka);
             probabilities(pt); // vector: block kb - 1
-#if CKV_PREFILL_PRIO
-            __builtin_amdgcn_s_setprio(1);
-#endif
             qk(kb, ka);        // matrix: block kb
             read_v(kb - 1, va);
             pv(va, pt);        // matrix: block kb - 1
-#if CKV_PREFILL_PRIO
-            __builtin_amdgcn_s_setprio(0);
-#endif
             grew = stats(kb);  // vector: block kb
             if (kb + 1 < n_blocks)
                 store_block(stage_of(kb + 1));

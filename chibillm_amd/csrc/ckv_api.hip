@@ -1448,7 +1448,8 @@ int append_decode_impl(ckv_pool* pool, size_t layer, const void* keys, const voi
             return status;
         return run_kernel(ctx, "append_decode", [&] {
             return launch_append_decode(ctx->stream, view, pool->meta, (uint32_t)layer, keys,
-                                        values, queries, (uint32_t)q_heads, scale, output, gate);
+                                        values, queries, (uint32_t)q_heads, scale, output, gate,
+                                        ctx->cu_count);
         });
     }
     status = ckv_append(pool, layer, keys, values, rows);

@@ -211,8 +211,8 @@ bool decode_fast_applies(const pool_view& p, uint32_t q_heads, const void* q, co
 // its position's slot with no two rows on one table range.
 hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_view& m,
                                 uint32_t layer, const void* k_in, const void* v_in, const void* q,
-                                uint32_t q_heads, float scale, void* out,
-                                const void* gate = nullptr);
+                                uint32_t q_heads, float scale, void* out, const void* gate,
+                                int cu_count);
 hipError_t launch_merge(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t q_heads,
                         void* out, const float* partials, const void* gate = nullptr);
 bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads);

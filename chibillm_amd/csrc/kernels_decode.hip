@@ -525,7 +525,12 @@ bool aligned16(const void* ptr)
 // (the longest rows are dispatched first and short ones fill the gaps), so
 // the largest count the kernel's occupancy allows is used: 16 for GQA groups
 // of at most 2 (a full compute unit), else 8. CKV_DECODE_WAVES overrides.
-uint32_t fast_waves(uint32_t group)
+// Waves per workgroup. With one or two q heads per KV head the workgroup
+// may hold 16 waves; when the batch has at least one (row, kv head) unit
+// per compute unit, 10 waves measured fastest (config 3, MI355X: 371 us per
+// layer against 378 at 16), while a small batch keeps all 16 so each row
+// streams as fast as one CU allows. CKV_DECODE_WAVES overrides.
+uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count)
 {
     const uint32_t limit = group <= 2 ? 16u : 8u;
     if (const char* forced = std::getenv("CKV_DECODE_WAVES")) {
@@ -533,16 +538,18 @@ uint32_t fast_waves(uint32_t group)
         if (v >= 1 && v <= (long)limit)
             return (uint32_t)v;
     }
+    if (group <= 2 && cu_count > 0 && units >= (uint32_t)cu_count)
+        return 10;
     return limit;
 }
 
 template <int G>
 hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                        const void* q, uint32_t q_heads, float scale_log2, void* out, bool f16,
-                       const void* k_in, const void* v_in, const void* gate)
+                       const void* k_in, const void* v_in, const void* gate, int cu_count)
 {
     const uint32_t units = m.rows * p.kv_heads;
-    const uint32_t waves = fast_waves(G);
+    const uint32_t waves = fast_waves(G, units, cu_count);
     const dim3 grid(units), block(64 * waves);
     const size_t lds = (size_t)waves * G * (128 + 2) * sizeof(float);
     const auto qq = static_cast<const uint16_t*>(q);
@@ -597,16 +604,16 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
         switch (q_heads / p.kv_heads) {
         case 1:
             return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr, gate);
+                                  nullptr, gate, cu_count);
         case 2:
             return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr, gate);
+                                  nullptr, gate, cu_count);
         case 4:
             return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr, gate);
+                                  nullptr, gate, cu_count);
         default:
             return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr, gate);
+                                  nullptr, gate, cu_count);
         }
     }
     if (p.head_dim > 64u * generic_max_features_per_lane)
@@ -631,7 +638,8 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
 
 hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_view& m,
                                 uint32_t layer, const void* k_in, const void* v_in, const void* q,
-                                uint32_t q_heads, float scale, void* out, const void* gate)
+                                uint32_t q_heads, float scale, void* out, const void* gate,
+                                int cu_count)
 {
     if (!m.rows)
         return hipSuccess;
@@ -639,13 +647,17 @@ hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_vi
     const bool f16 = p.dtype == CKV_F16;
     switch (q_heads / p.kv_heads) {
     case 1:
-        return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate);
+        return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
+                                cu_count);
     case 2:
-        return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate);
+        return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
+                                cu_count);
     case 4:
-        return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate);
+        return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
+                                cu_count);
     default:
-        return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate);
+        return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
+                                cu_count);
     }
 }
 

@@ -1179,7 +1179,8 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
     for (size_t i = 0, first_row = 0; i < n_items;) {
         size_t end = i + 1, span = token_count[i]; // items [i, end) continue one another
         while (end < n_items && seq[end] == seq[i]
-               && first_position[end] == first_position[end - 1] + token_count[end - 1])
+               && first_position[end]
+                   == (uint64_t)first_position[end - 1] + token_count[end - 1])
             span += token_count[end++];
         for (size_t at = 0; at < span; at += prefill_tile_rows) {
             const size_t n = std::min<size_t>(prefill_tile_rows, span - at);

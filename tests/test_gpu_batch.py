@@ -251,3 +251,49 @@ def test_sequence_table_validation_codes(ctx):
     pool.patch([0], [1])  # a host-uploaded batch is patchable again
     ctx.sync()
     pool.close()
+
+
+def test_batch_edge_cases_long_items_empty_batch_gather_and_rope(ctx):
+    """A 600-row prompt chunk (three query tiles), an empty batch, gather and
+    RoPE through the sequence tables, all against the host-uploaded equivalent."""
+    geom = (1, 96, BS, H, D)
+    (pa, ka, va), (pb, kb, vb) = random_pools(ctx, geom, 2, seed=9)
+    cap = 48
+    mirror = Tables(pb, 3, cap)
+    tables = {0: list(range(3, 3 + 40)), 1: list(range(50, 52)), 2: [90]}
+    for s, t in tables.items():
+        mirror.set(s, t)
+    items = [(0, 10, 600), (1, 20, 1), (2, 3, 2)]
+    (offsets, lengths, positions, slots), (ref_table, ref_offsets) = host_rows(items, tables, cap)
+    rows = len(positions)
+    pa.upload(mirror.flat(), offsets, lengths, positions, slots)
+    upload_items(pb, items)
+    q = orc.Mt64(4).normal(rows * HQ * D, orc.BF16).reshape(rows, HQ * D)
+    outs = []
+    for pool in (pa, pb):
+        out = torch.empty(rows, HQ * D, dtype=torch.bfloat16, device="cuda")
+        pool.attention(0, to_dev(q, orc.BF16), HQ, SCALE, out)  # shared tiles: prefill
+        rq = to_dev(q, orc.BF16)
+        pool.rope(rq, rq, HQ, 1e6)
+        outs.append((out, rq))
+    ctx.sync()
+    assert torch.equal(outs[0][0], outs[1][0]), "prefill over three tiles differs"
+    assert torch.equal(outs[0][1], outs[1][1]), "rope positions differ"
+    expected = orc.Attention(geom, to_host(kb, orc.BF16), to_host(vb, orc.BF16), orc.BF16, q,
+                             orc.BF16, positions, ref_table, ref_offsets, lengths, HQ, 0,
+                             SCALE).online_threads(8)
+    assert_close(to_f32(outs[1][0]), expected, what="600-row chunk vs oracle")
+    # gather of sequence 0's first 610 tokens through the arena row
+    n_tok = 610
+    ga = [torch.empty(n_tok * F, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    gb = [torch.empty(n_tok * F, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    pa.gather(0, 0, 40, n_tok, ga[0], ga[1])
+    pb.gather(0, 0, 40, n_tok, gb[0], gb[1])
+    ctx.sync()
+    assert torch.equal(ga[0], gb[0]) and torch.equal(ga[1], gb[1])
+    # an empty batch uploads and attends nothing
+    pb.upload_batch([], [], [], True)
+    assert pb.decode(0, torch.empty(0, HQ * D, dtype=torch.bfloat16, device="cuda"), HQ, SCALE,
+                     torch.empty(0, HQ * D, dtype=torch.bfloat16, device="cuda")) is None
+    pa.close()
+    pb.close()

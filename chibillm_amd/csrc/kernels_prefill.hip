@@ -7,13 +7,13 @@
 // scalar FMAs; here the dense products run on the matrix cores.
 //
 // Decomposition. A query tile is a run of rows of one sequence at consecutive
-// positions (built at upload, at most 256 rows). One workgroup of four waves
-// owns (256/G rows of a tile, one kv head) and all G query heads of that
-// head's GQA group: 256 query vectors, 64 per wave in two q-blocks of 32
-// (q-block b: head b % G, rows 32*(b / G)..). Every K/V byte of a key block
+// positions (built at upload, at most 256 rows). One workgroup of eight waves
+// (two per SIMD) owns (256/G rows of a tile, one kv head) and all G query
+// heads of that head's GQA group: 256 query vectors, one q-block of 32 per
+// wave (wave w: head w % G, rows 32*(w / G)..). Every K/V byte of a key block
 // is staged once per workgroup in LDS and used by all 256 query vectors.
 //
-// Per 32-key block (two pages) and q-block:
+// Per 32-key block (two pages) and wave:
 //   S^T[key][query] = K . Q^T    8 x v_mfma_f32_32x32x16 (A = K rows from
 //                                LDS, B = Q held in registers)
 //   online softmax              lane-local: lane l holds query l%32 and 16
@@ -25,12 +25,17 @@
 // physical keys with bits 2 and 3 swapped. Then the 8 probabilities a lane
 // needs as the B operand of the next product (k = 8*(l/32) + e) are its own
 // accumulator elements r = 8*step + e, physical keys 16*step + 8*(l/32) + e:
-// no data moves between S and P. K rows are stored at row key_row(key);
-// V is stored transposed ([feature][key], 2 keys per dword).
+// no data moves between S and P.
 //
-// Keys past the tile's last position are zero-filled (never read from the
-// pool), so no page outside a row's table is touched and masked keys carry
-// finite zeros into P.V.
+// Staging. K and V reach LDS by DMA (global_load_lds_dwordx4): each wave
+// moves one 1 KiB K region and one V row group per block, no registers
+// involved. Four LDS stages; the loads of block kb + 2 are issued while block
+// kb is scored, so each block's loads have a whole iteration in flight. The
+// block table entries are scalar loads, issued a block before their use.
+//
+// Keys past the tile's last position are read from a zero row (never from
+// the pool), so no page outside a row's table is touched and masked keys
+// carry finite zeros into P.V.
 #include "ckv_internal.h"
 
 namespace ckv {
@@ -44,41 +49,32 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t dim = 128;
 constexpr uint32_t page_tokens = 16;
 constexpr uint32_t block_keys = 32;
-constexpr uint32_t k_row_bytes = 272;  // 256 + 16: rows 0..7 start in distinct 16-byte bank groups
-constexpr uint32_t vt_row_bytes = 80;  // 64 + 16: likewise for 8 consecutive feature rows
-constexpr uint32_t k_bytes = block_keys * k_row_bytes;
-constexpr uint32_t vt_bytes = dim * vt_row_bytes;
+constexpr uint32_t waves = 8;
 
-#ifndef CKV_PREFILL_VDMA
-#define CKV_PREFILL_VDMA 1
-#endif
-// V staged by LDS DMA (global_load_lds_dwordx4) in its natural [key][feature]
-// layout and read transposed (ds_read_b64_tr_b16) into the A operand of
-// O^T += V^T P^T, instead of through registers and a transposing store.
-// A block's 32 key rows sit in 8 DMA groups of 4 rows (one 1 KiB wave
-// instruction each) with 64 bytes after each group: key k is row (k/4)%4 of
-// group k%4 + 4*(k/16), so the 8 keys one transposed read touches start at 4
-// different bank offsets.
-constexpr bool v_dma = CKV_PREFILL_VDMA != 0;
-constexpr uint32_t vg_bytes = 1024 + 64;
-constexpr uint32_t v_stage_bytes = v_dma ? 8 * vg_bytes : vt_bytes;
-// K by DMA: already in the A-operand order of S^T = K.Q^T. Region ks (1 KiB)
-// holds, at 16-byte slot l, what lane l = 32g + n reads for step ks: features
-// 16ks + 8g .. +7 of LDS row n (physical key key_row(n)). Each wave fills
-// one region with one DMA instruction, and every operand read is
+// K stage: already in the A-operand order of S^T = K.Q^T. Region ks (1 KiB)
+// holds, at 16-byte slot l, what lane l = 32g + n reads for step ks:
+// features 16ks + 8g .. +7 of LDS row n (physical key key_row(n)). Each wave
+// fills one region with one DMA instruction, and every operand read is
 // lane * 16 + ks * 1024, 256 contiguous bytes per 16 lanes.
-constexpr uint32_t k_stage_bytes = v_dma ? 8 * 1024 : k_bytes;
+constexpr uint32_t k_stage_bytes = 8 * 1024;
+// V stage: the natural [key][feature] layout, read transposed
+// (ds_read_b64_tr_b16) into the A operand of O^T += V^T P^T. A block's 32 key
+// rows sit in 8 DMA groups of 4 rows (one 1 KiB wave instruction each) with
+// 64 bytes after each group: key k is row (k/4)%4 of group k%4 + 4*(k/16),
+// so the 8 keys one transposed read touches start at 4 different bank offsets.
+constexpr uint32_t vg_bytes = 1024 + 64;
+constexpr uint32_t v_stage_bytes = 8 * vg_bytes;
 constexpr uint32_t stage_bytes = k_stage_bytes + v_stage_bytes;
+constexpr uint32_t n_stages = 4; // block kb in stage kb % 4
 
-// The source of masked (past the tile's last position) V rows under DMA:
-// zeros, so that their zero probabilities multiply finite values.
+// The source of masked (past the tile's last position) K and V rows: zeros,
+// so that their zero probabilities multiply finite values.
 __device__ const uint4 zero_row[16] = {};
-
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
 // One 16-byte LDS DMA per lane: lane l's 16 bytes at `src` land at LDS byte
 // address lds + 16 * l. Written out rather than through the compiler builtin,
@@ -98,18 +94,42 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds)
                  : "v"(src), "s"(lds));
 }
 
+// The same with a scalar 64-bit base and a per-lane 32-bit byte offset: no
+// vector address arithmetic.
+__device__ __forceinline__ void dma16_s(const void* base, uint32_t voff, uint32_t lds)
+{
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %3\n\t"
+                 "s_nop 0\n\t"
+                 "global_load_lds_dwordx4 %1, %2\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(voff), "s"(base), "s"(lds));
+}
+
+// vmcnt waits (the other counters left alone): the DMA of the block needed
+// next, with or without the newest block's two loads still in flight.
+__device__ __forceinline__ void wait_dma(bool newer_in_flight)
+{
+    if (newer_in_flight)
+        __builtin_amdgcn_s_waitcnt(0x0F72); // vmcnt(2)
+    else
+        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
+}
+
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* ptr)
+{
+    const uint64_t v = (uint64_t)(uintptr_t)ptr;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 // LDS row of physical key `key` in a block (an involution: bits 2 and 3 swapped).
 __device__ __forceinline__ uint32_t key_row(uint32_t key)
 {
     return (key & ~12u) | ((key & 4u) << 1) | ((key & 8u) >> 1);
-}
-
-// LDS row of feature f in the transposed V tile: rotated inside each group of
-// 8 by the group index, so the 16 chunks written by one instruction spread
-// over the banks while 8 consecutive features still occupy 8 distinct rows.
-__device__ __forceinline__ uint32_t vt_row(uint32_t f)
-{
-    return (f & ~7u) | ((f + (f >> 3)) & 7u);
 }
 
 template <bool F16>
@@ -153,7 +173,7 @@ __device__ __forceinline__ float sigmoid(float g)
 // the probabilities keep using the older, smaller maximum and may reach
 // 2^rescale_log2 (exact in fp32 and in the 16-bit P operand's exponent
 // range); the final division by the denominator, accumulated with the same
-// maximum, removes the offset exactly. Skipping the rescale of 128 fp32
+// maximum, removes the offset exactly. Skipping the rescale of 64 fp32
 // accumulators per block matters because on random data some lane of a
 // 32-query block sees a new maximum in most key blocks.
 constexpr float rescale_log2 = 8.0f;
@@ -183,18 +203,12 @@ __device__ __forceinline__ void exponentiate(f32x16_t& s, float m, float& l, flo
     l += sum;
 }
 
-// QB q-blocks (32 queries each) per wave: QB = 2 runs four waves of 64
-// queries, one wave per SIMD; QB = 1 runs eight waves of 32 queries, two
-// per SIMD, so one wave's softmax overlaps the other's matrix products.
-template <int QB>
-constexpr uint32_t wg_threads = 64 * (8 / QB);
-
-template <int G, int QB, bool F16>
-__global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kernel(
+template <int G, bool F16>
+__global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
     pool_view p, meta_view md, uint32_t layer, const uint16_t* __restrict__ q,
     uint16_t* __restrict__ out, uint32_t q_heads, float c, const uint16_t* __restrict__ gate)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[3 * stage_bytes];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[n_stages * stage_bytes];
     constexpr uint32_t tile_rows = 256 / G;
 
     const uint32_t kv_heads = p.kv_heads;
@@ -219,249 +233,140 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
     const uint32_t F = p.features;
     const size_t q_stride = (size_t)q_heads * dim;
 
-    // this wave's q-blocks
-    uint32_t qpos[QB];
-    size_t qoff[QB];
-    bool valid[QB];
-    uint32_t row_lo = ~0u;
-#pragma unroll
-    for (int sb = 0; sb < QB; ++sb) {
-        const uint32_t b = QB * wave + sb;
-        const uint32_t rb = b / G;
-        const uint32_t head = kvh * G + b % G;
-        const uint32_t row = rb * 32 + n;
-        valid[sb] = row < nrows;
-        qpos[sb] = pos0 + min(row, nrows - 1);
-        qoff[sb] = (size_t)(row0 + min(row, nrows - 1)) * q_stride + (size_t)head * dim;
-        row_lo = min(row_lo, rb * 32);
-    }
-    const bool active = row_lo < nrows;
-    const uint32_t pos_lo = pos0 + row_lo;
+    // this wave's q-block: head kvh * G + wave % G, tile rows 32 * (wave / G) + n
+    const uint32_t rb = wave / G;
+    const uint32_t head = kvh * G + wave % G;
+    const uint32_t row = rb * 32 + n;
+    const bool valid = row < nrows;
+    const bool active = rb * 32 < nrows;
+    const uint32_t qpos = pos0 + min(row, nrows - 1);
+    const size_t qoff = (size_t)(row0 + min(row, nrows - 1)) * q_stride + (size_t)head * dim;
+    const uint32_t pos_lo = pos0 + rb * 32;
 
     // Q^T operands: lane (n, g) holds features 16*ks + 8*g .. +7 of its query
-    uint4 qr[QB][8];
+    uint4 qr[8];
 #pragma unroll
-    for (int sb = 0; sb < QB; ++sb)
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks)
-            qr[sb][ks] = valid[sb] && active
-                ? *reinterpret_cast<const uint4*>(q + qoff[sb] + ks * 16 + g * 8)
-                : make_uint4(0, 0, 0, 0);
+    for (int ks = 0; ks < 8; ++ks)
+        qr[ks] = valid ? *reinterpret_cast<const uint4*>(q + qoff + ks * 16 + g * 8)
+                       : make_uint4(0, 0, 0, 0);
 
     const uint16_t* kbase = static_cast<const uint16_t*>(p.keys) + layer * p.layer_elems + kvh * dim;
     const uint16_t* vbase = static_cast<const uint16_t*>(p.values) + layer * p.layer_elems + kvh * dim;
-    // Staging roles over 256 threads: K rows t/16 and 16 + t/16, chunk t%16;
-    // V key pair t/16, chunk t%16. With 512 threads the first 256 stage V
-    // and the other 256 stage K (wave-uniform).
-    // With V by DMA, every one of the 512 threads stages one K chunk (row
-    // t/16, chunk t%16) and wave w issues V DMA group w.
-    static_assert(!v_dma || QB == 1, "V by DMA needs eight waves");
-    const uint32_t st_tid = v_dma ? tid : tid & 255;
-    const bool k_role = v_dma || QB == 2 || tid >= 256;
-    const bool v_role = !v_dma && (QB == 2 || tid < 256);
-    const uint32_t srow = st_tid >> 4, chunk = st_tid & 15;
     // K DMA: this lane's key (LDS row lane % 32) and features in its wave's region
     const uint32_t k_key = key_row(lane & 31);
     const uint32_t k_feat = 16 * wave + 8 * (lane >> 5);
-    const uint32_t k_src = (k_key & 15) * F + k_feat;
+    const uint32_t k_off = ((k_key & 15) * F + k_feat) * 2; // bytes into the key's page
+    const bool k_hi = (lane & 31) >= 16;                    // the key is in the block's second page
     // V DMA: this lane's key of its wave's group and its LDS read offset
     const uint32_t vd_key = 16 * (wave >> 2) + 4 * (lane >> 4) + (wave & 3);
-    const uint32_t vd_src = (vd_key & 15) * F + (lane & 15) * 8;
+    const uint32_t v_off = ((vd_key & 15) * F + (lane & 15) * 8) * 2;
     const uint32_t vr_off = ((lane & 15) >> 2) * vg_bytes + (lane >> 5) * 512
         + ((lane >> 4) & 1) * 32 + (lane & 3) * 8;
+    // DMA operands that do not change from block to block
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+    const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const size_t page_bytes = (size_t)page_tokens * F * 2;
+    const uint8_t* kbytes = uniform_ptr(reinterpret_cast<const uint8_t*>(kbase));
+    const uint8_t* vbytes = uniform_ptr(reinterpret_cast<const uint8_t*>(vbase));
+    const uint8_t* zbytes = reinterpret_cast<const uint8_t*>(zero_row);
+    auto stage_of = [&](uint32_t kb) { return lds + (kb % n_stages) * stage_bytes; };
 
-    // Loads are unconditional so the compiler can keep them in flight across
-    // the block's compute: a key past the tile's last position is read from a
-    // slot of the block's first page (always in the table) and replaced by
-    // zero when staged.
-    uint4 kr[2], vr[2];
-    auto stage_of = [&](uint32_t kb) { return lds + (kb % 3) * stage_bytes; };
-    // The block table entries of a block are read one block before its K/V
-    // loads are issued, so that dependent load never stalls the wave.
-    // The loads are issued a block ahead and their values taken (made
-    // uniform) only when that block's K/V loads are issued, so the wait for
-    // them falls on the previous iteration's drain, not on this wave's path.
-    uint32_t key0_next = 0;
-    uint32_t page_a = 0, page_b = 0; // table entries of the next block to load, in flight
+    // Block table entries through the constant address space (scalar loads),
+    // read one block before that block's loads are issued.
+    uint32_t page_a = 0, page_b = 0;
     auto fetch_pages = [&](uint32_t kb) {
         if (kb < n_blocks) {
+            const auto* ct = (const __attribute__((address_space(4))) uint32_t*)(uintptr_t)table;
             const uint32_t key0 = kb * block_keys;
-            page_a = table[2 * kb];
+            page_a = ct[2 * kb];
             // the block's second page, or its first when the tile ends in the first
-            page_b = table[2 * kb + (key0 + page_tokens <= pos_last ? 1 : 0)];
+            page_b = ct[2 * kb + (key0 + page_tokens <= pos_last ? 1 : 0)];
         }
     };
+    // K region `wave` and V group `wave` of block kb, into its stage
     auto load_block = [&](uint32_t kb) {
         const uint32_t key0 = kb * block_keys;
-        key0_next = key0;
         const uint32_t pg0 = __builtin_amdgcn_readfirstlane(page_a);
         const uint32_t pg1 = __builtin_amdgcn_readfirstlane(page_b);
         fetch_pages(kb + 1);
-        if constexpr (v_dma) {
-            // K region `wave` of the block's stage
-            const uint16_t* ksrc = key0 + k_key <= pos_last
-                ? kbase + (size_t)((lane & 31) < 16 ? pg0 : pg1) * (page_tokens * F) + k_src
-                : reinterpret_cast<const uint16_t*>(zero_row) + k_feat;
-            dma16(ksrc, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(
-                            (__attribute__((address_space(3))) uint8_t*)(stage_of(kb) + wave * 1024))));
-            // V straight into the block's stage (last read two iterations ago)
-            const uint16_t* src = key0 + vd_key <= pos_last
-                ? vbase + (size_t)(wave >> 2 ? pg1 : pg0) * (page_tokens * F) + vd_src
-                : reinterpret_cast<const uint16_t*>(zero_row) + (lane & 15) * 8;
-            dma16(src, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(
-                           (__attribute__((address_space(3))) uint8_t*)(
-                               stage_of(kb) + k_stage_bytes + wave * vg_bytes))));
-        } else if (k_role) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const size_t slot = (size_t)(i ? pg1 : pg0) * page_tokens + srow;
-                kr[i] = *reinterpret_cast<const uint4*>(kbase + slot * F + chunk * 8);
-            }
-        }
-        if (v_role) {
-            const uint32_t vpg = srow < 8 ? pg0 : pg1;
-            const uint32_t vtok = (2 * srow) & 15;
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const size_t slot = (size_t)vpg * page_tokens + vtok + i;
-                vr[i] = *reinterpret_cast<const uint4*>(vbase + slot * F + chunk * 8);
-            }
-        }
-    };
-    // all-ones when `keep`, else zero (element-wise masks keep the staging
-    // registers out of private memory, which a select of whole vectors does not)
-    auto masked = [](const uint4& v, bool keep) {
-        const uint32_t k = keep ? ~0u : 0u;
-        return make_uint4(v.x & k, v.y & k, v.z & k, v.w & k);
-    };
-    auto store_block = [&](uint8_t* st) {
-        if constexpr (v_dma) {
-            (void)st;
-            // this wave's K and V DMA have landed before the barrier that follows
-            __builtin_amdgcn_s_waitcnt(0);
-            return;
-        }
-        if (k_role) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                *reinterpret_cast<uint4*>(st + key_row(16 * i + srow) * k_row_bytes + chunk * 16) =
-                    masked(kr[i], key0_next + 16 * i + srow <= pos_last);
-        }
-        if (v_role) {
-            uint8_t* vt = st + k_bytes;
-            const uint4 v0 = masked(vr[0], key0_next + 2 * srow <= pos_last);
-            const uint4 v1 = masked(vr[1], key0_next + 2 * srow + 1 <= pos_last);
-            const uint32_t w0[4] = { v0.x, v0.y, v0.z, v0.w };
-            const uint32_t w1[4] = { v1.x, v1.y, v1.z, v1.w };
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                // features 8*chunk + 2d (low halves) and + 2d + 1 (high halves), keys (2*srow, +1)
-                const uint32_t even = __builtin_amdgcn_perm(w1[d], w0[d], 0x05040100u);
-                const uint32_t odd = __builtin_amdgcn_perm(w1[d], w0[d], 0x07060302u);
-                const uint32_t f = 8 * chunk + 2 * d;
-                *reinterpret_cast<uint32_t*>(vt + vt_row(f) * vt_row_bytes + 4 * srow) = even;
-                *reinterpret_cast<uint32_t*>(vt + vt_row(f + 1) * vt_row_bytes + 4 * srow) = odd;
-            }
+        const uint32_t st = lds_base + (kb % n_stages) * stage_bytes;
+        const uint8_t* k0 = kbytes + pg0 * page_bytes;
+        const uint8_t* k1 = kbytes + pg1 * page_bytes;
+        const uint8_t* vp = vbytes + (wave_u >= 4 ? pg1 : pg0) * page_bytes;
+        if (key0 + block_keys - 1 <= pos_last) { // every key of the block is in the tile
+            dma16((k_hi ? k1 : k0) + k_off, st + wave_u * 1024);
+            dma16_s(vp, v_off, st + k_stage_bytes + wave_u * vg_bytes);
+        } else {
+            const uint8_t* ksrc = key0 + k_key <= pos_last ? (k_hi ? k1 : k0) + k_off : zbytes + k_feat * 2;
+            dma16(ksrc, st + wave_u * 1024);
+            const uint8_t* vsrc = key0 + vd_key <= pos_last ? vp + v_off : zbytes + (lane & 15) * 16;
+            dma16(vsrc, st + k_stage_bytes + wave_u * vg_bytes);
         }
     };
 
-    f32x16_t o[QB][4];
+    f32x16_t o[4];
 #pragma unroll
-    for (int sb = 0; sb < QB; ++sb)
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-            o[sb][mt] = f32x16_t {};
-    float m[QB], l[QB];
-#pragma unroll
-    for (int sb = 0; sb < QB; ++sb) {
-        m[sb] = -__builtin_inff();
-        l[sb] = 0.0f;
-    }
+    for (int mt = 0; mt < 4; ++mt)
+        o[mt] = f32x16_t {};
+    float m = -__builtin_inff(), l = 0.0f;
 
-    // Software pipeline over key blocks, three LDS stages (block kb in stage
-    // kb % 3). Iteration kb issues S(kb) = K(kb) Q^T on the matrix core while
-    // the vector ALU turns S(kb-1) into probabilities, then P.V(kb-1) on the
-    // matrix core while the vector ALU masks S(kb) and takes its maxima and
-    // the next block is staged. The two halves of each iteration have no
-    // dependence between their matrix and vector work, so one wave keeps
+    // Software pipeline over key blocks. Iteration kb issues S(kb) = K(kb) Q^T
+    // on the matrix core while the vector ALU turns S(kb-1) into
+    // probabilities, then P.V(kb-1) on the matrix core while the vector ALU
+    // masks S(kb) and takes its maxima. The two halves of each iteration have
+    // no dependence between their matrix and vector work, so one wave keeps
     // both units busy.
-    f32x16_t sc[QB];      // S^T(kb), written by the matrix core
-    f32x16_t sp[QB];      // S^T(kb - 1), its maxima taken, awaiting exponentials
-    float mx[QB];
-    auto qk = [&](uint32_t kb, const uint4 (&ka)[8]) {
-#pragma unroll
-        for (int sb = 0; sb < QB; ++sb)
-            sc[sb] = f32x16_t {};
+    f32x16_t sc; // S^T(kb), written by the matrix core
+    f32x16_t sp; // S^T(kb - 1), its maxima taken, awaiting exponentials
+    float mx = 0.0f;
+    auto qk = [&](const uint4 (&ka)[8]) {
+        sc = f32x16_t {};
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-            for (int sb = 0; sb < QB; ++sb)
-                sc[sb] = mfma<F16>(ka[ks], qr[sb][ks], sc[sb]);
+            sc = mfma<F16>(ka[ks], qr[ks], sc);
     };
     auto read_k = [&](uint32_t kb, uint4 (&ka)[8]) {
-        if constexpr (v_dma) {
-            const uint8_t* kl = stage_of(kb) + lane * 16;
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks)
-                ka[ks] = *reinterpret_cast<const uint4*>(kl + ks * 1024);
-            return;
-        }
-        const uint8_t* krow = stage_of(kb) + n * k_row_bytes + g * 16;
+        const uint8_t* kl = stage_of(kb) + lane * 16;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks)
-            ka[ks] = *reinterpret_cast<const uint4*>(krow + ks * 32);
+            ka[ks] = *reinterpret_cast<const uint4*>(kl + ks * 1024);
     };
     auto read_v = [&](uint32_t kb, uint4 (&va)[4][2]) {
-        if constexpr (v_dma) {
-            // lane (n, g) of the A operand: features 32mt + n, keys 16h + 8g + 0..7,
-            // two transposed reads of keys 4 at a time
-            // one base register per block; the 16 reads add immediate offsets
-            uint32_t vaddr = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) uint8_t*)(
-                                 stage_of(kb) + k_stage_bytes))
-                + vr_off;
-            asm volatile("" : "+v"(vaddr));
-            auto* vb = (__attribute__((address_space(3))) uint8_t*)(uintptr_t)vaddr;
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) i16x4_t*)(vb + 4 * h * vg_bytes + 64 * mt));
-                    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) i16x4_t*)(vb + 4 * h * vg_bytes + 256 + 64 * mt));
-                    const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
-                    va[mt][h] = make_uint4(l2.x, l2.y, h2.x, h2.y);
-                }
-            return;
-        }
-        const uint8_t* vt = stage_of(kb) + k_bytes + g * 16;
+        // lane (n, g) of the A operand: features 32mt + n, keys 16h + 8g + 0..7,
+        // two transposed reads of keys 4 at a time; one base register per
+        // block, the 16 reads add immediate offsets
+        uint32_t vaddr = (uint32_t)(uintptr_t)((__attribute__((address_space(3))) uint8_t*)(
+                             stage_of(kb) + k_stage_bytes))
+            + vr_off;
+        asm volatile("" : "+v"(vaddr));
+        auto* vb = (__attribute__((address_space(3))) uint8_t*)(uintptr_t)vaddr;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-                va[mt][h] = *reinterpret_cast<const uint4*>(
-                    vt + vt_row(32 * mt + n) * vt_row_bytes + h * 32);
+            for (int h = 0; h < 2; ++h) {
+                const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) i16x4_t*)(vb + 4 * h * vg_bytes + 64 * mt));
+                const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) i16x4_t*)(vb + 4 * h * vg_bytes + 256 + 64 * mt));
+                const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+                va[mt][h] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+            }
     };
-    auto probabilities = [&](uint4 (&pt)[QB][2]) {
+    auto probabilities = [&](uint4 (&pt)[2]) {
+        exponentiate(sp, m, l, c);
 #pragma unroll
-        for (int sb = 0; sb < QB; ++sb) {
-            exponentiate(sp[sb], m[sb], l[sb], c);
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-                pt[sb][h] = make_uint4(pack2<F16>(sp[sb][8 * h + 0], sp[sb][8 * h + 1]),
-                                       pack2<F16>(sp[sb][8 * h + 2], sp[sb][8 * h + 3]),
-                                       pack2<F16>(sp[sb][8 * h + 4], sp[sb][8 * h + 5]),
-                                       pack2<F16>(sp[sb][8 * h + 6], sp[sb][8 * h + 7]));
-        }
+        for (int h = 0; h < 2; ++h)
+            pt[h] = make_uint4(pack2<F16>(sp[8 * h + 0], sp[8 * h + 1]),
+                               pack2<F16>(sp[8 * h + 2], sp[8 * h + 3]),
+                               pack2<F16>(sp[8 * h + 4], sp[8 * h + 5]),
+                               pack2<F16>(sp[8 * h + 6], sp[8 * h + 7]));
     };
-    auto pv = [&](const uint4 (&va)[4][2], const uint4 (&pt)[QB][2]) {
+    auto pv = [&](const uint4 (&va)[4][2], const uint4 (&pt)[2]) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-                for (int sb = 0; sb < QB; ++sb)
-                    o[sb][mt] = mfma<F16>(va[mt][h], pt[sb][h], o[sb][mt]);
+                o[mt] = mfma<F16>(va[mt][h], pt[h], o[mt]);
     };
     // causal mask and maxima of S(kb); moves it to sp; true when some lane's
     // maximum grew past the rescale threshold (m = -inf before block 0)
@@ -471,134 +376,111 @@ __global__ __launch_bounds__(wg_threads<QB>, QB == 1 ? 2 : 1) void prefill_kerne
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t kpos = key0 + 16 * (r >> 3) + 8 * g + (r & 7);
-#pragma unroll
-                for (int sb = 0; sb < QB; ++sb)
-                    if (kpos > qpos[sb])
-                        sc[sb][r] = -__builtin_inff();
+                if (kpos > qpos)
+                    sc[r] = -__builtin_inff();
             }
         }
-        bool grow = false;
-#pragma unroll
-        for (int sb = 0; sb < QB; ++sb) {
-            sp[sb] = sc[sb];
-            mx[sb] = block_max(sp[sb]);
-            grow = grow || (mx[sb] - m[sb]) * c > rescale_log2;
-        }
-        return __any(grow);
+        sp = sc;
+        mx = block_max(sp);
+        return __any((mx - m) * c > rescale_log2);
     };
     auto rescale = [&]() {
+        const float m_new = fmaxf(m, mx);
+        const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c); // 0 at the start
+        l *= alpha;
+        m = m_new;
 #pragma unroll
-        for (int sb = 0; sb < QB; ++sb) {
-            const float m_new = fmaxf(m[sb], mx[sb]);
-            const float alpha = __builtin_amdgcn_exp2f((m[sb] - m_new) * c); // 0 at the start
-            l[sb] *= alpha;
-            m[sb] = m_new;
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-                o[sb][mt] *= alpha;
-        }
+        for (int mt = 0; mt < 4; ++mt)
+            o[mt] *= alpha;
     };
 
     fetch_pages(0);
     load_block(0);
-    store_block(stage_of(0));
+    if (1 < n_blocks)
+        load_block(1);
+    wait_dma(1 < n_blocks);
     __syncthreads();
     // block 0: its scores and maxima (the first block always sets the maxima)
     {
-        if (1 < n_blocks)
-            load_block(1);
+        if (2 < n_blocks)
+            load_block(2);
         uint4 ka[8];
         read_k(0, ka);
-        qk(0, ka);
+        qk(ka);
         stats(0);
         if (1 < n_blocks)
-            store_block(stage_of(1));
+            wait_dma(2 < n_blocks);
         __syncthreads();
         rescale();
     }
-    // steady state: iteration kb finishes block kb - 1 and scores block kb
-    uint32_t kb = 1;
-    while (kb < n_blocks) {
-        bool grew = false;
-        for (; kb < n_blocks; ++kb) {
-            if (kb + 1 < n_blocks)
-                load_block(kb + 1);
-            uint4 ka[8], va[4][2];
-            uint4 pt[QB][2];
-            read_k(kb, ka);
-            probabilities(pt); // vector: block kb - 1
-            qk(kb, ka);        // matrix: block kb
-            read_v(kb - 1, va);
-            pv(va, pt);        // matrix: block kb - 1
-            grew = stats(kb);  // vector: block kb
-            if (kb + 1 < n_blocks)
-                store_block(stage_of(kb + 1));
-            __syncthreads();
-            if (grew)
-                break;
-        }
-        if (!grew)
-            break;
-        rescale(); // before block kb's probabilities are formed
-        ++kb;
+    // steady state: iteration kb finishes block kb - 1 and scores block kb;
+    // the stage block kb + 2 is loaded into was last read in iteration kb - 1
+    for (uint32_t kb = 1; kb < n_blocks; ++kb) {
+        if (kb + 2 < n_blocks)
+            load_block(kb + 2);
+        uint4 ka[8], va[4][2];
+        uint4 pt[2];
+        read_k(kb, ka);
+        // the K operand reads go out before the exponentials
+        __builtin_amdgcn_sched_barrier(0);
+        probabilities(pt); // vector: block kb - 1
+        qk(ka);            // matrix: block kb
+        read_v(kb - 1, va);
+        pv(va, pt);                  // matrix: block kb - 1
+        const bool grew = stats(kb); // vector: block kb
+        if (kb + 1 < n_blocks)
+            wait_dma(kb + 2 < n_blocks); // this wave's loads of block kb + 1
+        __syncthreads();
+        if (grew)
+            rescale(); // before block kb's probabilities are formed
     }
     // the last block's probabilities and product
     {
         uint4 va[4][2];
-        uint4 pt[QB][2];
+        uint4 pt[2];
         probabilities(pt);
         read_v(n_blocks - 1, va);
         pv(va, pt);
     }
 
-    if (!active)
+    if (!active || !valid)
         return;
+    const float inv = 1.0f / (l + __shfl_xor(l, 32));
+    uint16_t* dst = out + qoff;
 #pragma unroll
-    for (int sb = 0; sb < QB; ++sb) {
-        const float inv = 1.0f / (l[sb] + __shfl_xor(l[sb], 32));
-        if (!valid[sb])
-            continue;
-        uint16_t* dst = out + qoff[sb];
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int quad = 0; quad < 4; ++quad) {
+            const uint32_t f = 32 * mt + 8 * quad + 4 * g;
+            const f32x16_t& acc = o[mt];
+            float x[4] = { acc[4 * quad] * inv, acc[4 * quad + 1] * inv,
+                           acc[4 * quad + 2] * inv, acc[4 * quad + 3] * inv };
+            if (gate) { // sigmoid_mul (src/qwen/qwen_layer.cc:204) in the epilogue
+                const uint2 gv = *reinterpret_cast<const uint2*>(gate + qoff + f);
+                const uint32_t w[2] = { gv.x, gv.y };
 #pragma unroll
-            for (int quad = 0; quad < 4; ++quad) {
-                const uint32_t f = 32 * mt + 8 * quad + 4 * g;
-                const f32x16_t& acc = o[sb][mt];
-                float x[4] = { acc[4 * quad] * inv, acc[4 * quad + 1] * inv,
-                               acc[4 * quad + 2] * inv, acc[4 * quad + 3] * inv };
-                if (gate) { // sigmoid_mul (src/qwen/qwen_layer.cc:204) in the epilogue
-                    const uint2 gv = *reinterpret_cast<const uint2*>(gate + qoff[sb] + f);
-                    const uint32_t w[2] = { gv.x, gv.y };
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        x[e] *= sigmoid(half_value<F16>((uint16_t)(w[e / 2] >> (16 * (e % 2)))));
-                }
-                *reinterpret_cast<uint2*>(dst + f) =
-                    make_uint2(pack2<F16>(x[0], x[1]), pack2<F16>(x[2], x[3]));
+                for (int e = 0; e < 4; ++e)
+                    x[e] *= sigmoid(half_value<F16>((uint16_t)(w[e / 2] >> (16 * (e % 2)))));
             }
-    }
+            *reinterpret_cast<uint2*>(dst + f) =
+                make_uint2(pack2<F16>(x[0], x[1]), pack2<F16>(x[2], x[3]));
+        }
 }
-
-#ifndef CKV_PREFILL_QB
-#define CKV_PREFILL_QB 1
-#endif
 
 template <int G>
 hipError_t launch_g(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                     const void* q, uint32_t q_heads, float c, void* out, uint32_t grid,
                     const void* gate)
 {
-    constexpr int QB = CKV_PREFILL_QB;
     const auto* qq = static_cast<const uint16_t*>(q);
     auto* oo = static_cast<uint16_t*>(out);
     const auto* gg = static_cast<const uint16_t*>(gate);
     if (p.dtype == CKV_F16)
-        hipLaunchKernelGGL((prefill_kernel<G, QB, true>), dim3(grid), dim3(wg_threads<QB>), 0, s,
-                           p, m, layer, qq, oo, q_heads, c, gg);
+        hipLaunchKernelGGL((prefill_kernel<G, true>), dim3(grid), dim3(64 * waves), 0, s, p, m,
+                           layer, qq, oo, q_heads, c, gg);
     else
-        hipLaunchKernelGGL((prefill_kernel<G, QB, false>), dim3(grid), dim3(wg_threads<QB>), 0, s,
-                           p, m, layer, qq, oo, q_heads, c, gg);
+        hipLaunchKernelGGL((prefill_kernel<G, false>), dim3(grid), dim3(64 * waves), 0, s, p, m,
+                           layer, qq, oo, q_heads, c, gg);
     return hipGetLastError();
 }
 

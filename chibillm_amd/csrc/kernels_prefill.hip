@@ -29,9 +29,10 @@
 //
 // Staging. K and V reach LDS by DMA (global_load_lds_dwordx4): each wave
 // moves one 1 KiB K region and one V row group per block, no registers
-// involved. Four LDS stages; the loads of block kb + 2 are issued while block
-// kb is scored, so each block's loads have a whole iteration in flight. The
-// block table entries are scalar loads, issued a block before their use.
+// involved. Eight LDS stages; block kb + 4 is loaded while block kb is
+// scored, and one barrier every two blocks publishes the next two, so each
+// load has two to three iterations in flight. The block table entries are
+// scalar loads, issued a block before their use.
 //
 // Keys past the tile's last position are read from a zero row (never from
 // the pool), so no page outside a row's table is touched and masked keys
@@ -70,7 +71,7 @@ constexpr uint32_t k_stage_bytes = 8 * 1024;
 constexpr uint32_t vg_bytes = 1024 + 64;
 constexpr uint32_t v_stage_bytes = 8 * vg_bytes;
 constexpr uint32_t stage_bytes = k_stage_bytes + v_stage_bytes;
-constexpr uint32_t n_stages = 4; // block kb in stage kb % 4
+constexpr uint32_t n_stages = 8; // block kb in stage kb % 8
 
 // The source of masked (past the tile's last position) K and V rows: zeros,
 // so that their zero probabilities multiply finite values.
@@ -108,11 +109,13 @@ __device__ __forceinline__ void dma16_s(const void* base, uint32_t voff, uint32_
                  : "v"(voff), "s"(base), "s"(lds));
 }
 
-// vmcnt waits (the other counters left alone): the DMA of the block needed
-// next, with or without the newest block's two loads still in flight.
-__device__ __forceinline__ void wait_dma(bool newer_in_flight)
+// vmcnt wait (the other counters left alone) that lets `outstanding` of this
+// wave's newest DMA loads (two per block: K and V) stay in flight.
+__device__ __forceinline__ void wait_dma(uint32_t outstanding)
 {
-    if (newer_in_flight)
+    if (outstanding >= 4)
+        __builtin_amdgcn_s_waitcnt(0x0F74); // vmcnt(4)
+    else if (outstanding >= 2)
         __builtin_amdgcn_s_waitcnt(0x0F72); // vmcnt(2)
     else
         __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
@@ -394,30 +397,36 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
             o[mt] *= alpha;
     };
 
+    // This wave's loads newer than block b once it has issued block `last`.
+    auto newer = [&](uint32_t b, uint32_t last) {
+        const uint32_t top = min(last, n_blocks - 1);
+        return top > b ? 2 * (top - b) : 0u;
+    };
+    // Blocks are loaded four ahead and published two at a time: the barrier
+    // after an odd iteration kb waits for blocks kb + 1 and kb + 2, which the
+    // next two iterations read. Block b is loaded in iteration b - 4 into the
+    // stage of block b - 8, whose last read (V, iteration b - 7) precedes the
+    // barrier after iteration b - 7 or b - 6.
     fetch_pages(0);
-    load_block(0);
-    if (1 < n_blocks)
-        load_block(1);
-    wait_dma(1 < n_blocks);
+    for (uint32_t b = 0; b < 4; ++b)
+        if (b < n_blocks)
+            load_block(b);
+    wait_dma(newer(1, 3));
     __syncthreads();
     // block 0: its scores and maxima (the first block always sets the maxima)
     {
-        if (2 < n_blocks)
-            load_block(2);
+        if (4 < n_blocks)
+            load_block(4);
         uint4 ka[8];
         read_k(0, ka);
         qk(ka);
         stats(0);
-        if (1 < n_blocks)
-            wait_dma(2 < n_blocks);
-        __syncthreads();
         rescale();
     }
-    // steady state: iteration kb finishes block kb - 1 and scores block kb;
-    // the stage block kb + 2 is loaded into was last read in iteration kb - 1
+    // steady state: iteration kb finishes block kb - 1 and scores block kb
     for (uint32_t kb = 1; kb < n_blocks; ++kb) {
-        if (kb + 2 < n_blocks)
-            load_block(kb + 2);
+        if (kb + 4 < n_blocks)
+            load_block(kb + 4);
         uint4 ka[8], va[4][2];
         uint4 pt[2];
         read_k(kb, ka);
@@ -428,9 +437,10 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
         read_v(kb - 1, va);
         pv(va, pt);                  // matrix: block kb - 1
         const bool grew = stats(kb); // vector: block kb
-        if (kb + 1 < n_blocks)
-            wait_dma(kb + 2 < n_blocks); // this wave's loads of block kb + 1
-        __syncthreads();
+        if (kb & 1) {
+            wait_dma(newer(kb + 2, kb + 4)); // this wave's loads of blocks kb + 1, kb + 2
+            __syncthreads();
+        }
         if (grew)
             rescale(); // before block kb's probabilities are formed
     }

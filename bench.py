@@ -176,6 +176,10 @@ def bench_config3(args):
             if args.no_fuse:
                 pool.append(layer, k_new[layer], v_new[layer])
                 pool.decode(layer, q[layer], Q_HEADS, scale, out[layer])
+            elif args.rope:
+                pool.rope_append_decode(layer, k_new[layer], v_new[layer], q[layer], Q_HEADS,
+                                        scale, ROPE_THETA, out[layer],
+                                        gate=gate[layer] if args.gate else None)
             elif args.gate:
                 pool.append_decode_gated(layer, k_new[layer], v_new[layer], q[layer], Q_HEADS,
                                          scale, gate[layer], out[layer])
@@ -202,7 +206,8 @@ def bench_config3(args):
         pages_read += pages
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    dominant = "paged_attention_decode" if args.no_fuse else "append_decode"
+    dominant = ("paged_attention_decode" if args.no_fuse
+                else "rope_append_decode" if args.rope else "append_decode")
     decode_ms, decode_n = ctx.profile_query(dominant)
     merge_ms, merge_n = ctx.profile_query("paged_attention_merge")
     store_ms, store_n = ctx.profile_query("store_kv")
@@ -238,6 +243,9 @@ def bench_config3(args):
             "workload": "config3: 28-layer decode step (append 1 token/seq/layer + paged GQA "
                         "decode attention), batch 128, context U[1024,8192] growing 1/step",
             "launches": "two per layer (ckv_append, ckv_decode_attention)" if args.no_fuse
+                        else ("one per layer (ckv_rope_append_decode: queries and new keys "
+                              "rotated in the kernel, Qwen3 theta 1e6"
+                              + (", sigmoid gate" if args.gate else "") + ")") if args.rope
                         else ("one per layer (ckv_append_decode_gated: sigmoid gate in the "
                               "epilogue)" if args.gate else "one per layer (ckv_append_decode)"),
             "layers": LAYERS, "batch": BATCH, "kv_heads": KV_HEADS, "q_heads": Q_HEADS,
@@ -647,8 +655,10 @@ def main():
                     help="config3: the Qwen3.5 sigmoid gate applied in the decode epilogue "
                          "(ckv_append_decode_gated)")
     ap.add_argument("--rope", action="store_true",
-                    help="config4: rotate the chunk's keys inside the append (ckv_rope_append) "
-                         "and the queries in place (ckv_rope), Qwen3 theta 1e6")
+                    help="config3: queries and new keys rotated inside the fused decode "
+                         "(ckv_rope_append_decode); config4: rotate the chunk's keys inside the "
+                         "append (ckv_rope_append) and the queries in place (ckv_rope); Qwen3 "
+                         "theta 1e6")
     ap.add_argument("--prefix", type=int, default=2008,
                     help="config4 shared prefix tokens (2008 leaves a partial tail page, "
                          "so every sequence copies it on write; 2000 does not); spill: the "

@@ -65,6 +65,8 @@ _SIGNATURES = [
     ("ckv_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
     ("ckv_rope", _i, [_vp, _vp, _vp, _sz, C.c_float, _sz, _sz]),
     ("ckv_rope_append", _i, [_vp, _sz, _vp, _vp, C.c_float, _sz, _sz]),
+    ("ckv_rope_append_decode", _i, [_vp, _sz, _vp, _vp, _vp, _sz, C.c_float, C.c_float, _sz,
+                                    _vp, _vp, _sz]),
     ("ckv_copy_blocks", _i, [_vp, _u32p, _u32p, _sz]),
     ("ckv_checkpoint_pack", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
     ("ckv_checkpoint_unpack", _i, [_vp, _u32p, _sz, _sz, _vp, _vp]),
@@ -340,6 +342,16 @@ class Pool:
         rows = keys.shape[0] if rows is None else rows
         self.ctx.check(load().ckv_rope_append(self.handle, layer, _ptr(keys), _ptr(values),
                                               theta, rotary_dim, rows))
+
+    def rope_append_decode(self, layer: int, keys, values, queries, q_heads: int, scale: float,
+                           theta: float, output, rotary_dim: int = 0, gate=None,
+                           rows: Optional[int] = None) -> None:
+        """rope(queries), rope(keys) + append, decode attention (* sigmoid(gate)) in one
+        call (ckv_rope_append_decode)."""
+        rows = queries.shape[0] if rows is None else rows
+        self.ctx.check(load().ckv_rope_append_decode(
+            self.handle, layer, _ptr(keys), _ptr(values), _ptr(queries), q_heads, scale, theta,
+            rotary_dim, None if gate is None else _ptr(gate), _ptr(output), rows))
 
     def copy_blocks(self, src, dst) -> None:
         s, d = _u32(src), _u32(dst)

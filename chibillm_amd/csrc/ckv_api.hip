@@ -873,6 +873,8 @@ int ckv_pool_destroy(ckv_pool* pool)
         (void)hipFree(pool->d_work);
     if (pool->d_spill)
         (void)hipFree(pool->d_spill);
+    if (pool->d_rope_q)
+        (void)hipFree(pool->d_rope_q);
     delete pool;
     return CKV_OK;
 }
@@ -1539,6 +1541,59 @@ int ckv_append_decode_gated(ckv_pool* pool, size_t layer, const void* keys, cons
         return status;
     return append_decode_impl(pool, layer, keys, values, queries, q_heads, scale, output, rows,
                               gate);
+}
+
+int ckv_rope_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+                           const void* queries, size_t q_heads, float scale, float theta,
+                           size_t rotary_dim, const void* gate, void* output, size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    if (rows && (!keys || !values))
+        return set_error(ctx, CKV_E_INVALID_ARGUMENT, "keys and values are required");
+    if (!pool->uploaded || !pool->has_slots)
+        return set_error(ctx, CKV_E_NO_TABLES, "append before slots were uploaded");
+    if (rows != pool->slot_rows)
+        return set_error(ctx, CKV_E_CACHE_SLOT_COUNT_MISMATCH, "rows != uploaded slots");
+    int status = check_attention(pool, layer, queries, q_heads, output, rows);
+    if (status)
+        return status;
+    if (gate && (gate == queries || gate == output))
+        return set_error(ctx, CKV_E_UNSUPPORTED_ALIASING, "gate overlaps queries or output");
+    ckv::rope_table freq;
+    uint32_t rotary = 0;
+    status = check_rope(pool, q_heads, theta, rotary_dim, freq, rotary);
+    if (status || !rows)
+        return status;
+    const pool_view view = view_of(pool);
+    const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    // the fused kernel rotates in lane pairs part ^ (rotary / 16) of a 128-wide head
+    const bool lane_pairs = rotary >= 16 && rotary <= 128 && (rotary & (rotary - 1)) == 0;
+    if (pool->fusable && lane_pairs && decode_fast_applies(view, (uint32_t)q_heads, queries, output)
+        && aligned(keys) && aligned(values) && (!gate || aligned(gate))) {
+        status = ensure_order(pool);
+        if (status)
+            return status;
+        return run_kernel(ctx, "rope_append_decode", [&] {
+            return launch_append_decode(ctx->stream, view, pool->meta, (uint32_t)layer, keys,
+                                        values, queries, (uint32_t)q_heads, scale, output, gate,
+                                        ctx->cu_count, &freq, rotary);
+        });
+    }
+    // unfused: queries rotated into a pool buffer, keys rotated into their
+    // slots, then the attention over the rotated queries
+    const size_t q_bytes = rows * q_heads * pool->head_dim * pool->elem_size;
+    status = ensure_device(ctx, &pool->d_rope_q, &pool->d_rope_q_bytes, q_bytes, "rotated queries");
+    if (status)
+        return status;
+    status = ckv_rope(pool, queries, pool->d_rope_q, q_heads, theta, rotary_dim, rows);
+    if (status)
+        return status;
+    status = ckv_rope_append(pool, layer, keys, values, theta, rotary_dim, rows);
+    if (status)
+        return status;
+    return run_decode(pool, layer, pool->d_rope_q, q_heads, scale, output, gate);
 }
 
 int ckv_sigmoid_mul(ckv_context* ctx, int dtype, const void* gate, const void* input,

@@ -57,6 +57,20 @@ constexpr uint32_t max_rope_pairs = 512;
 struct rope_table {
     float inv_freq[max_rope_pairs];
 };
+// The first 64 of them, all that a 128-wide head uses: the fused decode's
+// kernel argument.
+struct rope_table64 {
+    float inv_freq[64];
+};
+
+// One rotary pair (a, b) -> (a cos - b sin, b cos + a sin), written once with
+// explicit fused multiply-adds for every kernel that rotates (ckv_rope,
+// ckv_rope_append, the fused decode).
+__device__ __forceinline__ void rope_pair(float a, float b, float c, float s, float& ra, float& rb)
+{
+    ra = __builtin_fmaf(a, c, -(b * s));
+    rb = __builtin_fmaf(b, c, a * s);
+}
 
 struct pending_timing {
     const char* name;
@@ -170,6 +184,8 @@ struct ckv_pool {
     size_t d_pairs_words = 0;
     char* d_spill = nullptr; // staging of checkpoint export/import
     size_t d_spill_bytes = 0;
+    char* d_rope_q = nullptr; // rotated queries of the unfused ckv_rope_append_decode
+    size_t d_rope_q_bytes = 0;
 };
 
 namespace ckv {
@@ -209,10 +225,13 @@ bool decode_fast_applies(const pool_view& p, uint32_t q_heads, const void* q, co
 // store_kv + fast decode in one launch; the caller has checked
 // decode_fast_applies, 16-byte aligned inputs, and that every row's slot is
 // its position's slot with no two rows on one table range.
+// With `rope` (rotary a multiple of 16 up to 128, rotary/16 a power of two)
+// the queries and the new keys are rotated inside the kernel first.
 hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_view& m,
                                 uint32_t layer, const void* k_in, const void* v_in, const void* q,
                                 uint32_t q_heads, float scale, void* out, const void* gate,
-                                int cu_count);
+                                int cu_count, const rope_table* rope = nullptr,
+                                uint32_t rotary = 0);
 hipError_t launch_merge(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t q_heads,
                         void* out, const float* partials, const void* gate = nullptr);
 bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads);

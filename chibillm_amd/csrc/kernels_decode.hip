@@ -153,12 +153,17 @@ __host__ __device__ constexpr uint32_t record_floats(uint32_t head_dim)
 // shuffles, the W wave states through LDS, and the workgroup writes the
 // normalised output of the group's q heads. GATED multiplies it by
 // sigmoid(gate) first; the gate values are loaded when the workgroup starts,
-// so their latency hides behind the page loads.
-template <int G, bool F16, bool FUSED, bool GATED>
+// so their latency hides behind the page loads. ROPE (with FUSED) rotates the
+// queries and the new token's key by the row's position first, as rope_f32
+// (src/metal/kernels/tensor_ops.metal:158-195) would: feature f < rotary/2
+// pairs with f + rotary/2, which sits in the lane part ^ (rotary/16) of the
+// same 16-lane group, so one lane exchange per register rotates a head.
+template <int G, bool F16, bool FUSED, bool GATED, bool ROPE>
 __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg_kernel(
     pool_view p, meta_view m, uint32_t layer, const uint16_t* __restrict__ q, uint32_t q_heads,
     float scale_log2, uint16_t* __restrict__ out, const char* __restrict__ k_in,
-    const char* __restrict__ v_in, const uint16_t* __restrict__ gate)
+    const char* __restrict__ v_in, const uint16_t* __restrict__ gate, rope_table64 freq,
+    uint32_t rotary)
 {
     using ops = half2_ops<F16>;
     constexpr uint32_t D = 128;
@@ -193,6 +198,57 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
         qv[g] = *reinterpret_cast<const uint4*>(
             q + ((uint64_t)row * q_heads + kv_head * G + g) * D + part * 8);
 
+    // ROPE: this lane's 8 features (pairs j0 .. j0 + 7) and their rotation;
+    // every lane of the wave takes part in the exchanges. The queries and the
+    // new token's key share the row's position: both are rotated while the
+    // wave's first page loads, and the rotated key (this lane's 16 bytes of
+    // it) takes the new token's place when the last page is processed. The
+    // row's rotary/2 angles are computed once, by wave 0, into LDS past the
+    // merge area.
+    const uint32_t rot_mask = ROPE ? rotary / 16 : 1; // lane parts per half of the rotary width
+    const bool rot_on = ROPE && part < 2 * rot_mask;
+    const bool rot_first = part < rot_mask;
+    auto angles = [&](float (&rc)[8], float (&rs)[8]) {
+        float* table = lds + W * G * (D + 2); // (cos, sin) per pair
+        if (wave == 0 && lane < rotary / 2) {
+            float sn, cs;
+            sincosf(static_cast<float>(position) * freq.inv_freq[lane], &sn, &cs);
+            table[2 * lane] = cs;
+            table[2 * lane + 1] = sn;
+        }
+        __syncthreads();
+        const uint32_t j0 = 8 * (part & (rot_mask - 1));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            rc[e] = rot_on ? table[2 * (j0 + e)] : 1.0f;
+            rs[e] = rot_on ? table[2 * (j0 + e) + 1] : 0.0f;
+        }
+    };
+    auto rotate = [&](const uint4& w, const float (&rc)[8], const float (&rs)[8]) {
+        const uint32_t in[4] = { w.x, w.y, w.z, w.w };
+        uint32_t r[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t pw = __shfl_xor(in[d], (int)rot_mask);
+            const float own[2] = { ops::lo(in[d]), ops::hi(in[d]) };
+            const float par[2] = { ops::lo(pw), ops::hi(pw) };
+            float x[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float ra, rb;
+                rope_pair(rot_first ? own[h] : par[h], rot_first ? par[h] : own[h], rc[2 * d + h],
+                          rs[2 * d + h], ra, rb);
+                x[h] = rot_first ? ra : rb;
+            }
+            r[d] = rot_on ? ops::pack(x[0], x[1]) : in[d];
+        }
+        return make_uint4(r[0], r[1], r[2], r[3]);
+    };
+    const uint64_t in_row = (uint64_t)row * row_bytes + head_off;
+    uint4 k_new = make_uint4(0, 0, 0, 0); // ROPE: the new token's key, rotated once loaded
+    if constexpr (ROPE)
+        k_new = *reinterpret_cast<const uint4*>(k_in + in_row);
+
     float mx[G], den[G], acc[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -204,7 +260,6 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
     }
 
     // rows past the row's last token re-read that token (in bounds, written)
-    const uint64_t in_row = (uint64_t)row * row_bytes + head_off;
     auto load_page = [&](uint32_t pg, uint4* k, uint4* v) {
         const uint64_t base = (uint64_t)tbl[pg] * page_bytes;
         const char* kb = kl + base;
@@ -216,14 +271,21 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
             const uint32_t r = min(4u * j + group, last);
             const uint32_t off = r * row_bytes + head_off;
             const bool fresh = FUSED && last_page && r == last_in_page;
-            k[j] = load_stream(fresh ? k_in + in_row : kb + off);
+            // ROPE: the new token's slot is read too and replaced in process
+            k[j] = load_stream(fresh && !ROPE ? k_in + in_row : kb + off);
             v[j] = load_stream(fresh ? v_in + in_row : vb + off);
         }
     };
 
-    auto process = [&](const uint4* k, const uint4* v, uint32_t pg) {
+    auto process = [&](uint4* k, const uint4* v, uint32_t pg) {
         const uint32_t valid = pg == n_pages - 1 ? last_in_page + 1 : BS;
         if (FUSED && pg == n_pages - 1) {
+            if constexpr (ROPE) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (4u * j + group == last_in_page)
+                        k[j] = k_new;
+            }
             // append: the lanes holding the new token write it into its slot
             const uint64_t base = (uint64_t)tbl[pg] * page_bytes;
             const uint32_t off = last_in_page * row_bytes + head_off;
@@ -285,6 +347,15 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
     uint32_t pg = wave;
     if (pg < n_pages)
         load_page(pg, ka, va);
+    // ROPE: rotate the queries and the new key while the first page loads
+    if constexpr (ROPE) {
+        float rc[8], rs[8];
+        angles(rc, rs);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            qv[g] = rotate(qv[g], rc, rs);
+        k_new = rotate(k_new, rc, rs);
+    }
     while (pg < n_pages) {
         uint32_t next = pg + W;
         if (next < n_pages)
@@ -546,34 +617,46 @@ uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count)
 template <int G>
 hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                        const void* q, uint32_t q_heads, float scale_log2, void* out, bool f16,
-                       const void* k_in, const void* v_in, const void* gate, int cu_count)
+                       const void* k_in, const void* v_in, const void* gate, int cu_count,
+                       const rope_table* rope = nullptr, uint32_t rotary = 0)
 {
     const uint32_t units = m.rows * p.kv_heads;
     const uint32_t waves = fast_waves(G, units, cu_count);
     const dim3 grid(units), block(64 * waves);
-    const size_t lds = (size_t)waves * G * (128 + 2) * sizeof(float);
+    // the merge's (acc, max, denominator) per wave, then the rope angle table
+    const size_t lds = ((size_t)waves * G * (128 + 2) + (rope ? 2 * 64 : 0)) * sizeof(float);
     const auto qq = static_cast<const uint16_t*>(q);
     const auto oo = static_cast<uint16_t*>(out);
     const auto ki = static_cast<const char*>(k_in);
     const auto vi = static_cast<const char*>(v_in);
     const auto gg = static_cast<const uint16_t*>(gate);
-    // one instantiation per (dtype, fused, gated)
-    const int variant = (f16 ? 4 : 0) | (k_in ? 2 : 0) | (gate ? 1 : 0);
+    rope_table64 f64 = {};
+    if (rope)
+        for (uint32_t j = 0; j < rotary / 2; ++j)
+            f64.inv_freq[j] = rope->inv_freq[j];
+    // one instantiation per (dtype, fused, gated, rope); rope only when fused
+    const int variant = (rope ? 8 : 0) | (f16 ? 4 : 0) | (k_in ? 2 : 0) | (gate ? 1 : 0);
     switch (variant) {
-#define CKV_FAST_CASE(V, F16_, FUSED_, GATED_)                                                 \
+#define CKV_FAST_CASE(V, F16_, FUSED_, GATED_, ROPE_)                                          \
     case V:                                                                                    \
-        decode_wg_kernel<G, F16_, FUSED_, GATED_>                                              \
-            <<<grid, block, lds, s>>>(p, m, layer, qq, q_heads, scale_log2, oo, ki, vi, gg); \
+        decode_wg_kernel<G, F16_, FUSED_, GATED_, ROPE_><<<grid, block, lds, s>>>(            \
+            p, m, layer, qq, q_heads, scale_log2, oo, ki, vi, gg, f64, rotary);                \
         break;
-        CKV_FAST_CASE(0, false, false, false)
-        CKV_FAST_CASE(1, false, false, true)
-        CKV_FAST_CASE(2, false, true, false)
-        CKV_FAST_CASE(3, false, true, true)
-        CKV_FAST_CASE(4, true, false, false)
-        CKV_FAST_CASE(5, true, false, true)
-        CKV_FAST_CASE(6, true, true, false)
-        CKV_FAST_CASE(7, true, true, true)
+        CKV_FAST_CASE(0, false, false, false, false)
+        CKV_FAST_CASE(1, false, false, true, false)
+        CKV_FAST_CASE(2, false, true, false, false)
+        CKV_FAST_CASE(3, false, true, true, false)
+        CKV_FAST_CASE(4, true, false, false, false)
+        CKV_FAST_CASE(5, true, false, true, false)
+        CKV_FAST_CASE(6, true, true, false, false)
+        CKV_FAST_CASE(7, true, true, true, false)
+        CKV_FAST_CASE(10, false, true, false, true)
+        CKV_FAST_CASE(11, false, true, true, true)
+        CKV_FAST_CASE(14, true, true, false, true)
+        CKV_FAST_CASE(15, true, true, true, true)
 #undef CKV_FAST_CASE
+    default:
+        return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -639,25 +722,27 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
 hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_view& m,
                                 uint32_t layer, const void* k_in, const void* v_in, const void* q,
                                 uint32_t q_heads, float scale, void* out, const void* gate,
-                                int cu_count)
+                                int cu_count, const rope_table* rope, uint32_t rotary)
 {
     if (!m.rows)
         return hipSuccess;
+    if (rope && (rotary < 16 || rotary > 128 || (rotary & (rotary - 1)) != 0))
+        return hipErrorInvalidValue;
     const float scale_log2 = scale * log2e;
     const bool f16 = p.dtype == CKV_F16;
     switch (q_heads / p.kv_heads) {
     case 1:
         return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
-                                cu_count);
+                              cu_count, rope, rotary);
     case 2:
         return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
-                                cu_count);
+                              cu_count, rope, rotary);
     case 4:
         return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
-                                cu_count);
+                              cu_count, rope, rotary);
     default:
         return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
-                                cu_count);
+                              cu_count, rope, rotary);
     }
 }
 

@@ -92,8 +92,8 @@ __global__ __launch_bounds__(block_threads) void rope_kernel(
             const float angle = static_cast<float>(positions[row]) * freq.inv_freq[pair];
             float sine, cosine;
             sincosf(angle, &sine, &cosine);
-            const float r1 = x1 * cosine - x2 * sine;
-            const float r2 = x2 * cosine + x1 * sine;
+            float r1, r2;
+            rope_pair(x1, x2, cosine, sine, r1, r2);
             x1 = r1;
             x2 = r2;
         }
@@ -149,8 +149,10 @@ __global__ __launch_bounds__(block_threads) void rope_kernel_x8(
             const float x2 = E::load(static_cast<uint16_t>(wb[d] >> (16 * h)));
             float sine, cosine;
             sincosf(pos * freq.inv_freq[p0 + 2 * d + h], &sine, &cosine);
-            oa |= static_cast<uint32_t>(E::store(x1 * cosine - x2 * sine)) << (16 * h);
-            ob |= static_cast<uint32_t>(E::store(x2 * cosine + x1 * sine)) << (16 * h);
+            float r1, r2;
+            rope_pair(x1, x2, cosine, sine, r1, r2);
+            oa |= static_cast<uint32_t>(E::store(r1)) << (16 * h);
+            ob |= static_cast<uint32_t>(E::store(r2)) << (16 * h);
         }
         ra[d] = oa;
         rb[d] = ob;

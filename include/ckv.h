@@ -137,7 +137,8 @@ int ckv_copy_to_host(ckv_context* ctx, void* host_dst, const void* device_src, s
  * "gather_kv", "paged_attention_decode", "paged_attention_merge", "append_decode",
  * "paged_attention_prefill", "copy_blocks", "checkpoint_pack",
  * "checkpoint_unpack", "tables_patch", "tables_fill", "batch_expand", "rope",
- * "rope_append", "sigmoid_mul". */
+ * "rope_append", "rope_append_decode", "sigmoid_mul", "checkpoint_export",
+ * "checkpoint_import". */
 int ckv_profile_enable(ckv_context* ctx, int enabled);
 int ckv_profile_query(ckv_context* ctx, const char* kernel, double* total_ms,
                       uint64_t* launches);
@@ -322,6 +323,23 @@ int ckv_rope(ckv_pool* pool, const void* input, void* output, size_t heads, floa
  * ckv_rope. */
 int ckv_rope_append(ckv_pool* pool, size_t layer, const void* keys, const void* values,
                     float theta, size_t rotary_dim, size_t rows);
+/* The decode step of an attention layer from unrotated rows: rope of the
+ * queries and of the new keys, store_kv, paged_attention (and, with a gate,
+ * sigmoid_mul) — src/qwen/qwen_layer.cc:20-30, :43-49 (Qwen3) and :183-206
+ * (Qwen3.5 full attention) — in one launch where ckv_append_decode's fused
+ * kernel applies and rotary_dim (0 = head_dim) is 16, 32, 64 or 128; otherwise
+ * as ckv_rope into a pool-owned buffer, ckv_rope_append and the attention.
+ * keys/values: [rows, kv_heads*head_dim]; queries: [rows, q_heads*head_dim];
+ * queries and keys are read unrotated and not modified; gate may be NULL (no
+ * gate), else as ckv_append_decode_gated's. The rotated keys and the values
+ * land in the uploaded slots of `layer`: values bit-exact, rotated 16-bit
+ * elements within one unit in the last place of ckv_rope_append's (both
+ * within one of rope_f32 in float, rounded). Checks: those of
+ * ckv_append_decode, unsupported_aliasing for the gate, then those of ckv_rope
+ * (with q_heads). */
+int ckv_rope_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+                           const void* queries, size_t q_heads, float scale, float theta,
+                           size_t rotary_dim, const void* gate, void* output, size_t rows);
 
 /* ---- Pages: copy-on-write and checkpoints ------------------------------------------ */
 /* For every layer, keys and values: page dst[i] := page src[i]. The copy-on-write

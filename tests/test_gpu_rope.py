@@ -169,3 +169,137 @@ def test_rope_append_matches_rope_then_store(ctx, code, rotary):
         assert ulps(to_host(qo, code), rq, code).max() <= 1
     pool.close()
     pool2.close()
+
+
+def gated_f32(expected, gate_bits, code):
+    g = orc.to_f32(gate_bits, code).astype(np.float64) if code != orc.F32 else gate_bits
+    return expected * (1.0 / (1.0 + np.exp(-np.asarray(g, np.float64))))
+
+
+def decode_rows(rng, code, batch, H, Hq, bs=16, D=128):
+    """Decode rows over permuted pages (the new token is each row's last),
+    including rows of 1, 16 and 17 tokens."""
+    lengths = [1, 16, 17] + [rng.uniform_int(1, 3000) for _ in range(batch - 3)]
+    pages = [-(-n // bs) for n in lengths]
+    blocks = sum(pages) + 5
+    perm = rng.permutation(blocks)
+    tables, at = [], 0
+    for p in pages:
+        tables.append(perm[at:at + p])
+        at += p
+    F = H * D
+    case = dict(
+        geom=(1, blocks, bs, H, D), flat=np.concatenate(tables),
+        offsets=np.cumsum([0] + pages[:-1]), pages=pages,
+        positions=[n - 1 for n in lengths],
+        kc=rng.normal(blocks * bs * F, code), vc=rng.normal(blocks * bs * F, code),
+        q=rng.normal(batch * Hq * D, code).reshape(batch, Hq * D),
+        kn=rng.normal(batch * F, code).reshape(batch, F),
+        vn=rng.normal(batch * F, code).reshape(batch, F))
+    case["slots"] = [orc.slot(t, p, bs) for t, p in zip(tables, case["positions"])]
+    return case
+
+
+@pytest.mark.parametrize("code,group,rotary,gated", [
+    (orc.BF16, 2, 0, False), (orc.F16, 2, 0, False), (orc.BF16, 1, 64, False),
+    (orc.BF16, 8, 32, False), (orc.BF16, 2, 0, True), (orc.F16, 4, 16, True),
+    (orc.BF16, 2, 48, False), (orc.F32, 2, 0, True)])
+def test_rope_append_decode_equals_unfused_sequence(ctx, code, group, rotary, gated):
+    """ckv_rope_append_decode (the fused decode kernel rotating queries and the
+    new keys in registers; rotary 48 and f32 take the unfused form) against
+    ckv_rope + ckv_rope_append + the attention, and against the oracle
+    (rope_f32, store_kv, paged attention, gate). Values land bit-exact; a
+    rotated 16-bit element may differ by one unit in the last place between the
+    two kernels that rotate it (each is within one of the oracle), so rotated
+    keys are compared within one ulp and outputs within the attention tolerance
+    (the unfused form's own outputs are compared bit for bit: same kernels)."""
+    print(f"rope_append_decode dtype {code} group {group} rotary {rotary} gated {gated}",
+          flush=True)
+    rng = orc.Mt64(60 + 7 * group + code + rotary + gated)
+    H = 8 if group <= 2 else 2
+    Hq = H * group
+    D, batch, theta = 128, 24, 1e6
+    c = decode_rows(rng, code, batch, H, Hq)
+    gate = rng.normal(batch * Hq * D, code).reshape(batch, Hq * D) if gated else None
+    scale = float(np.float32(1 / math.sqrt(D)))
+    outs, caches = [], []
+    for fused in (True, False):
+        pool, kd, vd = new_pool(ctx, c["geom"], code)
+        kd.copy_(to_dev(c["kc"], code))
+        vd.copy_(to_dev(c["vc"], code))
+        pool.upload(c["flat"], c["offsets"], c["pages"], c["positions"], c["slots"])
+        qd, knd, vnd = to_dev(c["q"], code), to_dev(c["kn"], code), to_dev(c["vn"], code)
+        gd = to_dev(gate, code) if gated else None
+        out = torch.full((batch, Hq * D), float("nan"), dtype=qd.dtype, device="cuda")
+        if fused:
+            pool.rope_append_decode(0, knd, vnd, qd, Hq, scale, theta, out, rotary, gd)
+        else:
+            qr = torch.empty_like(qd)
+            pool.rope(qd, qr, Hq, theta, rotary)
+            pool.rope_append(0, knd, vnd, theta, rotary)
+            if gated:
+                pool.attention_gated(0, qr, Hq, scale, gd, out)
+            else:
+                pool.attention(0, qr, Hq, scale, out)
+        ctx.sync()
+        assert np.array_equal(to_host(qd, code), c["q"]), "queries must not be modified"
+        assert np.array_equal(to_host(knd, code), c["kn"]), "keys must not be modified"
+        outs.append(to_host(out, code))
+        caches.append((to_host(kd, code), to_host(vd, code)))
+        pool.close()
+    assert np.array_equal(caches[0][1], caches[1][1]), "values differ from ckv_rope_append"
+    fused_path = code != orc.F32 and rotary in (0, 16, 32, 64, 128)
+    if fused_path:
+        assert ulps(caches[0][0], caches[1][0], code).max() <= 1, "keys vs ckv_rope_append"
+        assert_close(orc.to_f32(outs[0], code), orc.to_f32(outs[1], code),
+                     what="fused vs unfused sequence")
+    else:  # the unfused form runs the very same kernels
+        assert np.array_equal(caches[0][0], caches[1][0])
+        assert np.array_equal(outs[0], outs[1])
+
+    rk = orc.rope(c["kn"], code, H, c["positions"], theta, rotary)
+    want_k, want_v = c["kc"].copy(), c["vc"].copy()
+    orc.store_kv(want_k, want_v, rk, c["vn"], c["slots"], 0, c["geom"][1] * 16)
+    assert np.array_equal(caches[0][1], want_v), "values must land bit-exact"
+    if code == orc.F32:
+        assert_close(caches[0][0], want_k, atol=1e-5, rtol=1e-5, what="rotated keys (f32)")
+    else:
+        assert ulps(caches[0][0], want_k, code).max() <= 1
+    rq = orc.rope(c["q"], code, Hq, c["positions"], theta, rotary)
+    expected = orc.Attention(c["geom"], caches[0][0], caches[0][1], code, rq, code,
+                             c["positions"], c["flat"], c["offsets"], c["pages"], Hq, 0,
+                             scale).online_threads(8)
+    if gated:
+        expected = gated_f32(expected, gate, code)
+    got = outs[0] if code == orc.F32 else orc.to_f32(outs[0], code)
+    assert_close(got, expected, what="rope_append_decode vs oracle")
+
+
+def test_rope_append_decode_validation_codes(ctx):
+    D = 128
+    pool, kd, vd = new_pool(ctx, (1, 4, 16, 2, D), orc.BF16)
+    q = torch.zeros(2, 4 * D, dtype=torch.bfloat16, device="cuda")
+    k = torch.zeros(2, 2 * D, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty_like(q)
+    with pytest.raises(ckv.CkvError) as e:
+        pool.rope_append_decode(0, k, k, q, 4, 0.1, 1e4, out)
+    assert e.value.code == 403  # nothing uploaded
+    pool.upload([0, 1, 2, 3], [0, 2], [2, 2], [20, 5], slots=[20, 37])
+    cases = [
+        (dict(rows=1), "tensor_op.cache_slot_count_mismatch"),
+        (dict(layer=1), "tensor_op.cache_layer_out_of_range"),
+        (dict(q_heads=3), "tensor_op.invalid_kv_head_mapping"),
+        (dict(theta=0.0), "tensor_op.invalid_rope_theta"),
+        (dict(theta=float("nan")), "tensor_op.invalid_rope_theta"),
+        (dict(rotary_dim=3), "tensor_op.invalid_head_dimension"),
+        (dict(rotary_dim=256), "tensor_op.invalid_head_dimension"),
+        (dict(gate=q), "tensor_op.unsupported_aliasing"),
+    ]
+    for kwargs, name in cases:
+        args = dict(layer=0, q_heads=4, theta=1e4, rotary_dim=0, gate=None, rows=None)
+        args.update(kwargs)
+        with pytest.raises(ckv.CkvError) as e:
+            pool.rope_append_decode(args["layer"], k, k, q, args["q_heads"], 0.1, args["theta"],
+                                    out, args["rotary_dim"], args["gate"], args["rows"])
+        assert e.value.name == name, kwargs
+    pool.close()

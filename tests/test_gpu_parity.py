@@ -317,6 +317,58 @@ def test_config2_bf16_decode_over_permuted_pages(ctx, chunk, monkeypatch):
     pool.close()
 
 
+@pytest.mark.parametrize("waves", ["1", "3", "12"])
+def test_decode_wave_counts_and_long_rows(ctx, waves, monkeypatch):
+    """The fused decode kernel at forced wave counts. A wave walks every W-th
+    page of its row in runs of 64 (one table read per run): at one wave the
+    5,000-token row takes five runs. Rows end on, just past and inside page
+    boundaries. The fused step equals append-then-decode bit for bit and the
+    oracle within tolerance."""
+    monkeypatch.setenv("CKV_DECODE_WAVES", waves)
+    rng = orc.Mt64(23)
+    lengths = [5000, 1, 16, 17, 1025, 2049, 300]
+    B = sum(-(-n // 16) for n in lengths) + 5
+    perm = rng.permutation(B)
+    tables, at = [], 0
+    for n in lengths:
+        tables.append(perm[at:at + -(-n // 16)])
+        at += len(tables[-1])
+    F = 8 * 128
+    ks = [rng.normal(n * F, orc.BF16).reshape(n, F) for n in lengths]
+    vs = [rng.normal(n * F, orc.BF16).reshape(n, F) for n in lengths]
+    q = rng.normal(len(lengths) * 16 * 128, orc.BF16).reshape(len(lengths), -1)
+    flat = np.concatenate(tables)
+    offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
+    positions = [n - 1 for n in lengths]
+    slots = [orc.slot(t, p, 16) for t, p in zip(tables, positions)]
+    scale = float(np.float32(1 / math.sqrt(128)))
+    pools, outs = [], []
+    for fused in (True, False):
+        pool, keys, values = new_pool(ctx, (1, B, 16, 8, 128), orc.BF16, fill=float("nan"))
+        fill_by_append(pool, [n - 1 for n in lengths], tables,
+                       [k[:-1] for k in ks], [v[:-1] for v in vs])
+        pool.upload(flat, offsets, [len(t) for t in tables], positions, slots)
+        k_new = to_dev(np.stack([k[-1] for k in ks]), orc.BF16)
+        v_new = to_dev(np.stack([v[-1] for v in vs]), orc.BF16)
+        out = torch.empty(len(lengths), 16 * 128, dtype=torch.bfloat16, device="cuda")
+        if fused:
+            pool.append_decode(0, k_new, v_new, to_dev(q, orc.BF16), 16, scale, out)
+        else:
+            pool.append(0, k_new, v_new)
+            pool.decode(0, to_dev(q, orc.BF16), 16, scale, out)
+        pools.append((pool, keys, values))
+        outs.append(out)
+    ctx.sync()
+    # slots never written hold NaN: nothing past a row's last token reaches the output
+    assert torch.equal(pools[0][1].view(torch.int16), pools[1][1].view(torch.int16))
+    assert torch.equal(pools[0][2].view(torch.int16), pools[1][2].view(torch.int16))
+    assert torch.equal(outs[0], outs[1])
+    expected = compact_oracle((8, 128), lengths, tables, ks, vs, q, 16)
+    assert_close(to_f32(outs[0]), expected, what=f"{waves} waves")
+    for pool, _, _ in pools:
+        pool.close()
+
+
 def test_edge_positions_and_gqa_groups(ctx):
     """Single-token rows, rows ending exactly on page and chunk boundaries, and
     every GQA group size the fast kernel specialises."""

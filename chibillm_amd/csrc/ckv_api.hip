@@ -319,9 +319,11 @@ int run_decode(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads
             * partial_record_floats((uint32_t)pool->head_dim);
         status = ensure_device(ctx, &pool->d_partials, &capacity_floats, needed,
                                "decode partials");
+        // stored whatever the outcome: a failed regrow leaves no buffer and
+        // no capacity, so the next launch allocates again
+        pool->d_partials_bytes = capacity_floats * sizeof(float);
         if (status)
             return status;
-        pool->d_partials_bytes = capacity_floats * sizeof(float);
         partials = pool->d_partials;
     }
     status = run_kernel(ctx, "paged_attention_decode", [&] {
@@ -1031,6 +1033,9 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     put(s_tiles, tiles.data(), tiles.size());
     if (with_order)
         decode_order(pool->positions, pool->sort_keys, w + s_order);
+    // from here the previous batch's metadata may be freed: until this batch
+    // is adopted, launches report no tables instead of reading stale pointers
+    pool->uploaded = false;
     status = ensure_device(ctx, &pool->d_meta, &pool->d_meta_words, words, "metadata buffer");
     if (status)
         return status;
@@ -1089,6 +1094,8 @@ int ckv_seq_tables_reserve(ckv_pool* pool, size_t max_sequences, size_t pages_pe
         || (uint64_t)max_sequences * pages_per_sequence > UINT32_MAX)
         return set_error(ctx, CKV_E_INVALID_ARGUMENT, "sequence table arena size");
     const size_t words = max_sequences * pages_per_sequence;
+    if (pool->device_tables)
+        pool->uploaded = false; // the batch indexes the arena, which may be replaced
     int status = ensure_device(ctx, &pool->d_seq, &pool->d_seq_words, words, "sequence tables");
     if (status)
         return status;
@@ -1104,8 +1111,6 @@ int ckv_seq_tables_reserve(ckv_pool* pool, size_t max_sequences, size_t pages_pe
     pool->seq_host.assign(words, 0);
     pool->seq_dirty.assign(words, 0);
     pool->dirty.clear();
-    if (pool->device_tables)
-        pool->uploaded = false; // the batch indexed the old arena
     return CKV_OK;
 }
 
@@ -1228,9 +1233,7 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
         const uint32_t at = pool->dirty[k];
         pairs[2 * k] = at;
         pairs[2 * k + 1] = pool->seq_host[at];
-        pool->seq_dirty[at] = 0;
     }
-    pool->dirty.clear();
     uint32_t* b = section(s_batch);
     for (size_t i = 0, r = 0; i < n_items; ++i) {
         b[i] = seq[i];
@@ -1244,6 +1247,9 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
         std::memcpy(section(s_tiles), tiles.data(), tiles.size() * sizeof(uint32_t));
     if (with_order)
         decode_order(positions, pool->sort_keys, section(s_order));
+    // from here the previous batch's metadata may be freed: until this batch
+    // is adopted, launches report no tables instead of reading stale pointers
+    pool->uploaded = false;
     status = ensure_device(ctx, &pool->d_meta, &pool->d_meta_words, s_pairs + up_words,
                            "metadata buffer");
     if (status)
@@ -1259,6 +1265,11 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
         });
         if (status)
             return status;
+        // the entries are on their way: no longer pending (a failure before
+        // this point leaves them pending for the next upload)
+        for (size_t k = 0; k < n_pairs; ++k)
+            pool->seq_dirty[pool->dirty[k]] = 0;
+        pool->dirty.clear();
     }
     status = run_kernel(ctx, "batch_expand", [&] {
         return launch_expand_batch(ctx->stream, d + s_batch, (uint32_t)n_items, (uint32_t)rows,

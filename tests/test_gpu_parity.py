@@ -369,6 +369,60 @@ def test_decode_wave_counts_and_long_rows(ctx, waves, monkeypatch):
         pool.close()
 
 
+@pytest.mark.parametrize("group,waves", [(2, None), (2, "3"), (4, None)])
+def test_decode_large_batch_many_units_per_cu(ctx, group, waves, monkeypatch):
+    """96 rows of 1 to 700 tokens: several (row, kv head) units per compute
+    unit, at the default and a forced wave count, with eight and with four KV
+    heads. Unwritten slots hold NaN. The fused step equals append-then-decode
+    bit for bit and the oracle within tolerance."""
+    if waves:
+        monkeypatch.setenv("CKV_DECODE_WAVES", waves)
+    rng = orc.Mt64(31 + group)
+    rows = 96
+    lengths = [rng.uniform_int(1, 700) for _ in range(rows - 4)] + [16, 17, 32, 1]
+    H = 16 // group
+    q_heads = H * group
+    F = H * 128
+    B = sum(-(-n // 16) for n in lengths) + 5
+    perm = rng.permutation(B)
+    tables, at = [], 0
+    for n in lengths:
+        tables.append(perm[at:at + -(-n // 16)])
+        at += len(tables[-1])
+    ks = [rng.normal(n * F, orc.BF16).reshape(n, F) for n in lengths]
+    vs = [rng.normal(n * F, orc.BF16).reshape(n, F) for n in lengths]
+    q = rng.normal(rows * q_heads * 128, orc.BF16).reshape(rows, -1)
+    flat = np.concatenate(tables)
+    offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
+    positions = [n - 1 for n in lengths]
+    slots = [orc.slot(t, p, 16) for t, p in zip(tables, positions)]
+    scale = float(np.float32(1 / math.sqrt(128)))
+    pools, outs = [], []
+    for fused in (True, False):
+        pool, keys, values = new_pool(ctx, (1, B, 16, H, 128), orc.BF16, fill=float("nan"))
+        fill_by_append(pool, [n - 1 for n in lengths], tables,
+                       [k[:-1] for k in ks], [v[:-1] for v in vs])
+        pool.upload(flat, offsets, [len(t) for t in tables], positions, slots)
+        k_new = to_dev(np.stack([k[-1] for k in ks]), orc.BF16)
+        v_new = to_dev(np.stack([v[-1] for v in vs]), orc.BF16)
+        out = torch.empty(rows, q_heads * 128, dtype=torch.bfloat16, device="cuda")
+        if fused:
+            pool.append_decode(0, k_new, v_new, to_dev(q, orc.BF16), q_heads, scale, out)
+        else:
+            pool.append(0, k_new, v_new)
+            pool.decode(0, to_dev(q, orc.BF16), q_heads, scale, out)
+        pools.append((pool, keys, values))
+        outs.append(out)
+    ctx.sync()
+    assert torch.equal(pools[0][1].view(torch.int16), pools[1][1].view(torch.int16))
+    assert torch.equal(pools[0][2].view(torch.int16), pools[1][2].view(torch.int16))
+    assert torch.equal(outs[0], outs[1])
+    expected = compact_oracle((H, 128), lengths, tables, ks, vs, q, q_heads)
+    assert_close(to_f32(outs[0]), expected, what=f"group {group}, waves {waves}")
+    for pool, _, _ in pools:
+        pool.close()
+
+
 def test_edge_positions_and_gqa_groups(ctx):
     """Single-token rows, rows ending exactly on page and chunk boundaries, and
     every GQA group size the fast kernel specialises."""

@@ -926,6 +926,10 @@ void adopt_batch(ckv_pool* pool, size_t rows, size_t n_entries, bool with_slots,
     meta_view& m = pool->meta;
     m.n_entries = (uint32_t)n_entries;
     m.rows = (uint32_t)rows;
+    uint64_t pages = 0;
+    for (const uint32_t position : pool->positions)
+        pages += position / pool->block_size + 1;
+    m.mean_pages = rows ? (uint32_t)(pages / rows) : 0;
     m.items = m.row_first = m.row_count = nullptr;
     m.n_items = 0;
     m.chunk = 0;

@@ -45,6 +45,7 @@ struct meta_view {
     uint32_t n_items;
     uint32_t chunk; // tokens per decode work item, a multiple of 16
     uint32_t n_tiles;
+    uint32_t mean_pages; // pages attended per row, mean over the batch (host side)
 };
 
 // Largest query tile, in rows (positions): the prefill kernel covers a tile

@@ -592,16 +592,16 @@ bool aligned16(const void* ptr)
     return reinterpret_cast<uintptr_t>(ptr) % 16 == 0;
 }
 
-// Waves per workgroup of the fast path. Shorter workgroups balance better
-// (the longest rows are dispatched first and short ones fill the gaps), so
-// the largest count the kernel's occupancy allows is used: 16 for GQA groups
-// of at most 2 (a full compute unit), else 8. CKV_DECODE_WAVES overrides.
-// Waves per workgroup. With one or two q heads per KV head the workgroup
-// may hold 16 waves; when the batch has at least one (row, kv head) unit
-// per compute unit, 10 waves measured fastest (config 3, MI355X: 371 us per
-// layer against 378 at 16), while a small batch keeps all 16 so each row
-// streams as fast as one CU allows. CKV_DECODE_WAVES overrides.
-uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count)
+// Waves per workgroup of the fast path. With one or two q heads per KV head
+// and at least one (row, kv head) unit per compute unit: 10 waves (one
+// workgroup per CU) for rows of at least 256 pages on average, else 8 (two
+// workgroups per CU, so one's start and merge overlap the other's page
+// reads). Measured on MI355X (one layer, batches of 128-512 rows): 8 waves is
+// 0.6-9.5 % faster for mean rows of 50-160 pages, the two tie at 256 and 10
+// is 2.7 % faster at 288 (config 3). A smaller batch takes the maximum (16, or
+// 8 for larger groups) so each row streams as fast as one CU allows.
+// CKV_DECODE_WAVES overrides.
+uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count, uint32_t mean_pages)
 {
     const uint32_t limit = group <= 2 ? 16u : 8u;
     if (const char* forced = std::getenv("CKV_DECODE_WAVES")) {
@@ -610,7 +610,7 @@ uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count)
             return (uint32_t)v;
     }
     if (group <= 2 && cu_count > 0 && units >= (uint32_t)cu_count)
-        return 10;
+        return mean_pages >= 256 ? 10 : 8;
     return limit;
 }
 
@@ -621,7 +621,7 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
                        const rope_table* rope = nullptr, uint32_t rotary = 0)
 {
     const uint32_t units = m.rows * p.kv_heads;
-    const uint32_t waves = fast_waves(G, units, cu_count);
+    const uint32_t waves = fast_waves(G, units, cu_count, m.mean_pages);
     const dim3 grid(units), block(64 * waves);
     // the merge's (acc, max, denominator) per wave, then the rope angle table
     const size_t lds = ((size_t)waves * G * (128 + 2) + (rope ? 2 * 64 : 0)) * sizeof(float);

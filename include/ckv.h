@@ -178,7 +178,10 @@ int ckv_element_offset(const ckv_pool* pool, size_t layer, size_t block, size_t 
  * here, once per batch, and reused by every layer; so is the decode kernel's
  * row order when every tile is a single row. The split-KV decode work list
  * (and the row order of other batches) are derived and uploaded by the
- * batch's first decode launch that needs them. */
+ * batch's first decode launch that needs them. A batch that fails the checks
+ * leaves the previous batch current; one that fails after them (device
+ * allocation or copy) leaves no batch: launches report no_tables until the
+ * next upload succeeds. The same holds for ckv_batch_upload. */
 int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entries,
                       const uint32_t* offsets, const uint32_t* lengths,
                       const uint32_t* positions, const uint32_t* slots, size_t rows);
@@ -202,7 +205,8 @@ int ckv_tables_patch(ckv_pool* pool, const uint32_t* idx, const uint32_t* val, s
 
 /* Allocates the arena (kept until the pool is destroyed; a second call
  * resizes it) and sets every entry to page 0 and every table length to 0.
- * A batch uploaded from the previous arena must be uploaded again. */
+ * A batch uploaded from the previous arena must be uploaded again (launches
+ * report no_tables until then). */
 int ckv_seq_tables_reserve(ckv_pool* pool, size_t max_sequences, size_t pages_per_sequence);
 /* Mirrors block_manager changes (src/block_manager.cc:5-64: pages appended
  * to a reservation, a release; and a copy-on-write page replacement):

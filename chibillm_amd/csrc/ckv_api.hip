@@ -1005,6 +1005,10 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
         fusable = own == slots[r];
     }
     fusable = fusable && all_distinct(pool, offsets, rows, n_entries + 1);
+    // the checks passed: from here the batch's host state and device metadata
+    // are replaced, so until this batch is adopted launches report no tables
+    // (never the previous batch's pointers with this batch's positions)
+    pool->uploaded = false;
     pool->positions.assign(positions, positions + rows);
     // a batch of single-row tiles goes to the decode kernel: its row order
     // goes up now
@@ -1037,9 +1041,6 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     put(s_tiles, tiles.data(), tiles.size());
     if (with_order)
         decode_order(pool->positions, pool->sort_keys, w + s_order);
-    // from here the previous batch's metadata may be freed: until this batch
-    // is adopted, launches report no tables instead of reading stale pointers
-    pool->uploaded = false;
     status = ensure_device(ctx, &pool->d_meta, &pool->d_meta_words, words, "metadata buffer");
     if (status)
         return status;
@@ -1205,6 +1206,9 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
     // one decode row per sequence at its own position's slot: fusable
     bool fusable = with_slots != 0 && rows == n_items; // every item a single row
     fusable = fusable && all_distinct(pool, seq, n_items, pool->seq_max);
+    // the checks passed: from here the batch's host state and device metadata
+    // are replaced, so until this batch is adopted launches report no tables
+    pool->uploaded = false;
     std::vector<uint32_t>& positions = pool->positions;
     positions.resize(rows);
     for (size_t i = 0, r = 0; i < n_items; ++i)
@@ -1251,9 +1255,6 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
         std::memcpy(section(s_tiles), tiles.data(), tiles.size() * sizeof(uint32_t));
     if (with_order)
         decode_order(positions, pool->sort_keys, section(s_order));
-    // from here the previous batch's metadata may be freed: until this batch
-    // is adopted, launches report no tables instead of reading stale pointers
-    pool->uploaded = false;
     status = ensure_device(ctx, &pool->d_meta, &pool->d_meta_words, s_pairs + up_words,
                            "metadata buffer");
     if (status)

@@ -784,3 +784,101 @@ TEST("spill: a sequence that needs the pool spills a cached prefix; a later hit 
     for (seq_id id : { 2, 3 })
         CHECK(close_rows(outputs[0][id], outputs[1][id]));
 }
+
+// tests/qwen3_5_model_state_test.cc:329-417 without the DeltaNet layers: two-token batches over
+// two-token pages; every attempted batch writes K = V = position + 1 for its rows at every layer
+// through store_kv. After an abort, every committed position still holds its value, and the
+// retried batch rewrites the same slots.
+TEST("transactions: an aborted append never overwrites the committed KV prefix")
+{
+    auto made = hip_model_state::make(gpu(), kv_cache_config { 2, 8, 2, 1, 2 }, kv_dtype::f32,
+                                      prefix_sharing::shared_pages);
+    REQUIRE(made);
+    hip_model_state* state = made->get();
+    auto& cache = state->cache();
+    write_cache(cache, cache.keys(), std::vector<float>(cache.element_count(), 0.0f));
+    write_cache(cache, cache.values(), std::vector<float>(cache.element_count(), 0.0f));
+    scheduler_config config;
+    config.max_sequences = 2;
+    config.max_batch_tokens = 2;
+    config.kv_block_count = 8;
+    config.kv_block_size = 2;
+    auto engine = scheduler::make(config, 99, std::move(*made));
+    REQUIRE(engine);
+    auto sequence = seq::make(1, { 1, 2, 3 }, { .max_new_tokens = 2 });
+    REQUIRE(sequence);
+    REQUIRE(engine->add(std::move(*sequence)));
+
+    const auto execute = [&](const model_batch& batch) {
+        auto md = prepare_paged_batch(batch, 512, cache.block_count(), cache.block_size());
+        REQUIRE(md);
+        const std::vector<std::uint32_t> positions(batch.positions.begin(), batch.positions.end());
+        REQUIRE(upload_attention_metadata(cache, { positions, md->slots, md->block_table,
+                                                   md->table_offsets, md->table_lengths }));
+        const std::size_t rows = batch.tokens.size();
+        std::vector<float> rows_kv(rows * 2);
+        for (std::size_t r = 0; r < rows; ++r)
+            rows_kv[2 * r] = rows_kv[2 * r + 1] = float(batch.positions[r] + 1);
+        auto kb = upload(rows_kv.data(), rows_kv.size() * 4);
+        auto vb = upload(rows_kv.data(), rows_kv.size() * 4);
+        for (std::size_t layer = 0; layer < 2; ++layer)
+            REQUIRE(store_kv(cache, view(kb, dtype::f32, { rows, 2 }), view(vb, dtype::f32, { rows, 2 }),
+                             layer));
+    };
+    const auto committed_prefix_intact = [&](std::size_t committed) {
+        const auto keys = read_cache<float>(cache, cache.keys());
+        const auto values = read_cache<float>(cache, cache.values());
+        const auto table = state->resources(1).blocks;
+        for (std::size_t layer = 0; layer < 2; ++layer)
+            for (std::size_t pos = 0; pos < committed; ++pos)
+                for (std::size_t f = 0; f < 2; ++f) {
+                    const auto offset = cache.element_offset(layer, table[pos / 2], pos % 2, 0, f);
+                    REQUIRE(offset);
+                    CHECK(keys[*offset] == float(pos + 1));
+                    CHECK(values[*offset] == float(pos + 1));
+                }
+    };
+
+    // a partial prefill, aborted, then retried and committed
+    auto scheduled = engine->schedule();
+    REQUIRE(scheduled);
+    auto batch = build_model_batch(*scheduled, *engine);
+    REQUIRE(batch);
+    REQUIRE(engine->begin_execution(*batch));
+    execute(*batch);
+    REQUIRE(engine->abort(scheduled->id));
+    CHECK(engine->find_sequence(1)->processed_token_count() == 0);
+    scheduled = engine->schedule();
+    REQUIRE(scheduled);
+    batch = build_model_batch(*scheduled, *engine);
+    REQUIRE(batch);
+    REQUIRE(engine->begin_execution(*batch));
+    execute(*batch);
+    REQUIRE(engine->complete(scheduled->id, {}));
+    CHECK(engine->find_sequence(1)->processed_token_count() == 2);
+    committed_prefix_intact(2);
+
+    // the rest of the prefill, then one decode; each attempted once and aborted first
+    for (int step = 0; step < 2; ++step) {
+        scheduled = engine->schedule();
+        REQUIRE(scheduled);
+        batch = build_model_batch(*scheduled, *engine);
+        REQUIRE(batch);
+        const std::size_t committed = engine->find_sequence(1)->processed_token_count();
+        REQUIRE(engine->begin_execution(*batch));
+        execute(*batch);
+        REQUIRE(engine->abort(scheduled->id));
+        CHECK(engine->find_sequence(1)->processed_token_count() == committed);
+        committed_prefix_intact(committed);
+        scheduled = engine->schedule();
+        REQUIRE(scheduled);
+        batch = build_model_batch(*scheduled, *engine);
+        REQUIRE(batch);
+        REQUIRE(engine->begin_execution(*batch));
+        execute(*batch);
+        const std::vector<token_id> samples { 42 };
+        REQUIRE(engine->complete(scheduled->id, samples));
+    }
+    // the sequence has finished: its pages are released
+    CHECK(engine->state().resources(1).blocks.empty());
+}

@@ -594,13 +594,14 @@ bool aligned16(const void* ptr)
 
 // Waves per workgroup of the fast path. With one or two q heads per KV head
 // and at least one (row, kv head) unit per compute unit: 10 waves (one
-// workgroup per CU) for rows of at least 256 pages on average, else 8 (two
-// workgroups per CU, so one's start and merge overlap the other's page
-// reads). Measured on MI355X (one layer, batches of 128-512 rows): 8 waves is
-// 0.6-9.5 % faster for mean rows of 50-160 pages, the two tie at 256 and 10
-// is 2.7 % faster at 288 (config 3). A smaller batch takes the maximum (16, or
-// 8 for larger groups) so each row streams as fast as one CU allows.
-// CKV_DECODE_WAVES overrides.
+// workgroup per CU), except for batches of at least 6 units per CU whose rows
+// average under 256 pages, which take 8 (two workgroups per CU, so one's
+// start and merge overlap the other's page reads). Measured on MI355X (one
+// layer): with 6-16 units per CU, 8 waves is 0.6-9.5 % faster for mean rows
+// of 50-160 pages, the two tie at 256 pages and 10 is 2.7 % faster at 288
+// (config 3); with 1-2 units per CU, 8 waves is 7-16 % slower. A smaller
+// batch takes the maximum (16, or 8 for larger groups) so each row streams
+// as fast as one CU allows. CKV_DECODE_WAVES overrides.
 uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count, uint32_t mean_pages)
 {
     const uint32_t limit = group <= 2 ? 16u : 8u;
@@ -610,7 +611,7 @@ uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count, uint32_t mean_
             return (uint32_t)v;
     }
     if (group <= 2 && cu_count > 0 && units >= (uint32_t)cu_count)
-        return mean_pages >= 256 ? 10 : 8;
+        return units / (uint32_t)cu_count >= 6 && mean_pages < 256 ? 8 : 10;
     return limit;
 }
 

@@ -57,6 +57,7 @@ _SIGNATURES = [
     ("ckv_seq_tables_reserve", _i, [_vp, _sz, _sz]),
     ("ckv_seq_tables_update", _i, [_vp, _u32p, _u32p, _u32p, _sz, _u32p, _u32p, _sz]),
     ("ckv_batch_upload", _i, [_vp, _u32p, _u32p, _u32p, _sz, _i]),
+    ("ckv_decode_plan", _i, [_vp, _u32p, _u32p, _u32p]),
     ("ckv_append", _i, [_vp, _sz, _vp, _vp, _sz]),
     ("ckv_gather", _i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp]),
     ("ckv_decode_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
@@ -288,6 +289,14 @@ class Pool:
         s, f, c = _u32(seq), _u32(first_position), _u32(token_count)
         self.ctx.check(load().ckv_batch_upload(self.handle, _p(s), _p(f), _p(c), s.size,
                                                1 if with_slots else 0))
+
+    def decode_plan(self):
+        """(pages per chunk, work items, partial records) of the current batch's
+        fast decode plan (ckv_decode_plan); pages per chunk 0 = one chunk per row."""
+        span, items, records = C.c_uint32(), C.c_uint32(), C.c_uint32()
+        self.ctx.check(load().ckv_decode_plan(self.handle, C.byref(span), C.byref(items),
+                                              C.byref(records)))
+        return span.value, items.value, records.value
 
     def append(self, layer: int, keys, values, rows: Optional[int] = None) -> None:
         rows = keys.shape[0] if rows is None else rows

@@ -12,6 +12,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <new>
+#include <unordered_map>
 #include <unordered_set>
 
 using namespace ckv;
@@ -189,21 +190,6 @@ int check_attention(const ckv_pool* pool, size_t layer, const void* queries, siz
     return CKV_OK;
 }
 
-// Rows by decreasing position, ties in row order: the decode kernel
-// dispatches the longest work first. Sorted as 64-bit keys (inverted
-// position above the row), which needs no comparator indirection.
-void decode_order(const std::vector<uint32_t>& positions, std::vector<uint64_t>& keys,
-                  uint32_t* order)
-{
-    const size_t rows = positions.size();
-    keys.resize(rows);
-    for (size_t r = 0; r < rows; ++r)
-        keys[r] = ((uint64_t)(UINT32_MAX - positions[r]) << 32) | r;
-    std::sort(keys.begin(), keys.end());
-    for (size_t r = 0; r < rows; ++r)
-        order[r] = (uint32_t)keys[r];
-}
-
 // Whether keys[0..n) (each < bound) are distinct: a generation-stamped
 // table, cleared only when the generation counter wraps.
 bool all_distinct(ckv_pool* pool, const uint32_t* keys, size_t n, size_t bound)
@@ -223,28 +209,74 @@ bool all_distinct(ckv_pool* pool, const uint32_t* keys, size_t n, size_t bound)
     return true;
 }
 
-// The row order of a batch uploaded without it (one served by the prefill
-// kernel), at its first decode launch.
-int ensure_order(ckv_pool* pool)
+// Words of the fast decode plan in the metadata block: (row, chunk) pairs,
+// each row's first partial record, then the cut rows.
+size_t plan_words(const decode_plan_shape& shape, size_t rows)
 {
-    if (pool->order_ready)
+    return round4(2 * (size_t)shape.n_items) + round4(rows) + shape.n_cut;
+}
+
+// Writes the plan at `words` (plan_words long) and points the batch's
+// meta_view at `device`, its device copy.
+void put_plan(ckv_pool* pool, const decode_plan_shape& shape, uint32_t* words,
+              const uint32_t* device)
+{
+    const size_t s_first = round4(2 * (size_t)shape.n_items);
+    const size_t s_cut = s_first + round4(pool->positions.size());
+    write_decode_plan(pool->positions, (uint32_t)pool->block_size, shape, pool->sort_keys, words,
+                      words + s_first, words + s_cut);
+    meta_view& m = pool->meta;
+    m.plan = device;
+    m.split_first = device + s_first;
+    m.cut = device + s_cut;
+    m.n_plan = shape.n_items;
+    m.split_pages = shape.split_pages;
+    m.n_records = shape.n_records;
+    m.n_cut = shape.n_cut;
+}
+
+// The fast decode plan of a batch uploaded without it (one served by the
+// prefill kernel), at its first decode launch.
+int ensure_plan(ckv_pool* pool)
+{
+    if (pool->plan_ready)
         return CKV_OK;
     ckv_context* ctx = pool->ctx;
-    const size_t rows = pool->positions.size();
+    const decode_plan_shape shape = shape_decode_plan(
+        pool->positions, (uint32_t)pool->block_size, (uint32_t)pool->kv_heads, ctx->cu_count);
+    const size_t words = std::max<size_t>(plan_words(shape, pool->positions.size()), 4);
     void* host = nullptr;
-    int status = stage(ctx, std::max<size_t>(rows, 4) * sizeof(uint32_t), &host);
+    int status = stage(ctx, words * sizeof(uint32_t), &host);
     if (status)
         return status;
-    decode_order(pool->positions, pool->sort_keys, static_cast<uint32_t*>(host));
-    status = ensure_device(ctx, &pool->d_order, &pool->d_order_words, std::max<size_t>(rows, 4),
-                           "row order");
+    status = ensure_device(ctx, &pool->d_plan, &pool->d_plan_words, words, "decode plan");
     if (status)
         return status;
-    status = upload_staged(ctx, pool->d_order, rows * sizeof(uint32_t));
+    put_plan(pool, shape, static_cast<uint32_t*>(host), pool->d_plan);
+    status = upload_staged(ctx, pool->d_plan, words * sizeof(uint32_t));
     if (status)
         return status;
-    pool->meta.order = pool->d_order;
-    pool->order_ready = true;
+    pool->plan_ready = true;
+    return CKV_OK;
+}
+
+// Scratch of the fast decode when its plan cuts rows into chunks: a partial
+// record for every (record, q head).
+int ensure_split(ckv_pool* pool, size_t q_heads, split_scratch& split)
+{
+    split = {};
+    const meta_view& m = pool->meta;
+    if (!m.n_cut)
+        return CKV_OK;
+    size_t capacity_floats = pool->d_partials_bytes / sizeof(float);
+    const size_t floats = (size_t)m.n_records * q_heads
+        * partial_record_floats((uint32_t)pool->head_dim);
+    const int status = ensure_device(pool->ctx, &pool->d_partials, &capacity_floats, floats,
+                                     "decode partials");
+    pool->d_partials_bytes = capacity_floats * sizeof(float);
+    if (status)
+        return status;
+    split.records = pool->d_partials;
     return CKV_OK;
 }
 
@@ -308,8 +340,11 @@ int run_decode(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads
     ckv_context* ctx = pool->ctx;
     const pool_view view = view_of(pool);
     float* partials = nullptr;
+    split_scratch split {};
     const bool fast = decode_fast_applies(view, (uint32_t)q_heads, queries, output);
-    int status = fast ? ensure_order(pool) : ensure_work(pool);
+    int status = fast ? ensure_plan(pool) : ensure_work(pool);
+    if (!status && fast)
+        status = ensure_split(pool, q_heads, split);
     if (status)
         return status;
     const bool needs_merge = !fast && pool->work_multi;
@@ -328,7 +363,8 @@ int run_decode(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads
     }
     status = run_kernel(ctx, "paged_attention_decode", [&] {
         return launch_decode(ctx->stream, view, pool->meta, (uint32_t)layer, queries,
-                             (uint32_t)q_heads, scale, output, partials, ctx->cu_count, gate);
+                             (uint32_t)q_heads, scale, output, partials, ctx->cu_count, gate,
+                             split);
     });
     if (status || !needs_merge)
         return status;
@@ -869,8 +905,8 @@ int ckv_pool_destroy(ckv_pool* pool)
         (void)hipFree(pool->d_pairs);
     if (pool->d_seq)
         (void)hipFree(pool->d_seq);
-    if (pool->d_order)
-        (void)hipFree(pool->d_order);
+    if (pool->d_plan)
+        (void)hipFree(pool->d_plan);
     if (pool->d_work)
         (void)hipFree(pool->d_work);
     if (pool->d_spill)
@@ -919,9 +955,9 @@ int ckv_element_offset(const ckv_pool* pool, size_t layer, size_t block, size_t 
 namespace {
 
 // The host state of a batch just uploaded; the work list (and, unless it
-// was uploaded, the row order) are derived on first use.
+// was uploaded, the decode plan) are derived on first use.
 void adopt_batch(ckv_pool* pool, size_t rows, size_t n_entries, bool with_slots, bool shared,
-                 bool fusable, bool order_uploaded, bool device_tables)
+                 bool fusable, bool plan_uploaded, bool device_tables)
 {
     meta_view& m = pool->meta;
     m.n_entries = (uint32_t)n_entries;
@@ -933,15 +969,17 @@ void adopt_batch(ckv_pool* pool, size_t rows, size_t n_entries, bool with_slots,
     m.items = m.row_first = m.row_count = nullptr;
     m.n_items = 0;
     m.chunk = 0;
-    if (!order_uploaded)
-        m.order = nullptr;
+    if (!plan_uploaded) {
+        m.plan = m.split_first = m.cut = nullptr;
+        m.n_plan = m.split_pages = m.n_records = m.n_cut = 0;
+    }
     pool->has_slots = with_slots;
     pool->slot_rows = with_slots ? rows : 0;
     pool->n_entries = n_entries;
     pool->device_tables = device_tables;
     pool->shared_tile = shared;
     pool->fusable = fusable;
-    pool->order_ready = order_uploaded;
+    pool->plan_ready = plan_uploaded;
     pool->work_ready = false;
     pool->uploaded = true;
 }
@@ -1010,19 +1048,28 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     // (never the previous batch's pointers with this batch's positions)
     pool->uploaded = false;
     pool->positions.assign(positions, positions + rows);
-    // a batch of single-row tiles goes to the decode kernel: its row order
-    // goes up now
-    const bool with_order = !shared;
+    if (fusable) {
+        pool->own_index.resize(rows);
+        for (size_t r = 0; r < rows; ++r)
+            pool->own_index[r] = (uint32_t)(offsets[r] + positions[r] / bs);
+        pool->own_slot.assign(slots, slots + rows);
+    }
+    // a batch of single-row tiles goes to the decode kernel: its plan goes
+    // up now
+    const bool with_plan = !shared;
+    const decode_plan_shape plan_shape = with_plan
+        ? shape_decode_plan(pool->positions, (uint32_t)bs, (uint32_t)pool->kv_heads, ctx->cu_count)
+        : decode_plan_shape {};
 
-    // pack: table | offsets | lengths | positions | slots | tiles | order
+    // pack: table | offsets | lengths | positions | slots | tiles | plan
     const size_t s_table = 0;
     const size_t s_offsets = s_table + round4(n_entries);
     const size_t s_lengths = s_offsets + round4(rows);
     const size_t s_positions = s_lengths + round4(rows);
     const size_t s_slots = s_positions + round4(rows);
     const size_t s_tiles = s_slots + round4(rows);
-    const size_t s_order = s_tiles + round4(tiles.size());
-    const size_t words = std::max<size_t>(s_order + (with_order ? rows : 0), 4);
+    const size_t s_plan = s_tiles + round4(tiles.size());
+    const size_t words = std::max<size_t>(s_plan + (with_plan ? plan_words(plan_shape, rows) : 0), 4);
     void* host = nullptr;
     int status = stage(ctx, words * sizeof(uint32_t), &host);
     if (status)
@@ -1039,11 +1086,11 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     if (slots)
         put(s_slots, slots, rows);
     put(s_tiles, tiles.data(), tiles.size());
-    if (with_order)
-        decode_order(pool->positions, pool->sort_keys, w + s_order);
     status = ensure_device(ctx, &pool->d_meta, &pool->d_meta_words, words, "metadata buffer");
     if (status)
         return status;
+    if (with_plan)
+        put_plan(pool, plan_shape, w + s_plan, pool->d_meta + s_plan);
     status = upload_staged(ctx, pool->d_meta, words * sizeof(uint32_t));
     if (status)
         return status;
@@ -1055,9 +1102,8 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     m.positions = pool->d_meta + s_positions;
     m.slots = pool->d_meta + s_slots;
     m.tiles = pool->d_meta + s_tiles;
-    m.order = pool->d_meta + s_order;
     m.n_tiles = (uint32_t)(tiles.size() / 2);
-    adopt_batch(pool, rows, n_entries, slots != nullptr, shared, fusable, with_order, false);
+    adopt_batch(pool, rows, n_entries, slots != nullptr, shared, fusable, with_plan, false);
     return CKV_OK;
 }
 
@@ -1085,9 +1131,31 @@ int ckv_tables_patch(ckv_pool* pool, const uint32_t* idx, const uint32_t* val, s
     if (status)
         return status;
     uint32_t* table = pool->d_meta; // the table section starts the metadata block
-    return run_kernel(ctx, "tables_patch", [&] {
+    status = run_kernel(ctx, "tables_patch", [&] {
         return launch_table_patch(ctx->stream, table, pool->d_pairs, (uint32_t)n);
     });
+    if (status) {
+        pool->uploaded = false; // the device table may hold part of the patch
+        return status;
+    }
+    // The fused append writes a row's token through the table (its own
+    // position's page), ckv_append through the uploaded slot: once a patch
+    // moves a row's own page elsewhere, only the unfused pair keeps the
+    // semantics of store_kv followed by paged_attention. The last write of
+    // an index wins, as on the device.
+    if (pool->fusable) {
+        std::unordered_map<uint32_t, uint32_t> patched;
+        for (size_t i = 0; i < n; ++i)
+            patched[idx[i]] = val[i];
+        const size_t bs = pool->block_size;
+        for (size_t r = 0; r < pool->own_index.size() && pool->fusable; ++r) {
+            const auto at = patched.find(pool->own_index[r]);
+            if (at != patched.end())
+                pool->fusable = (uint64_t)at->second * bs + pool->positions[r] % bs
+                    == pool->own_slot[r];
+        }
+    }
+    return CKV_OK;
 }
 
 int ckv_seq_tables_reserve(ckv_pool* pool, size_t max_sequences, size_t pages_per_sequence)
@@ -1214,10 +1282,13 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
     for (size_t i = 0, r = 0; i < n_items; ++i)
         for (uint32_t j = 0; j < token_count[i]; ++j)
             positions[r++] = first_position[i] + j;
-    const bool with_order = !shared;
+    const bool with_plan = !shared;
+    const decode_plan_shape plan_shape = with_plan
+        ? shape_decode_plan(positions, (uint32_t)bs, (uint32_t)pool->kv_heads, ctx->cu_count)
+        : decode_plan_shape {};
 
     // d_meta: offsets | lengths | positions | slots (written by the expand
-    // kernel) | pending (index, block) pairs | items (5 sections) | tiles | order;
+    // kernel) | pending (index, block) pairs | items (5 sections) | tiles | plan;
     // the upload starts at the pairs
     const size_t n_pairs = pool->dirty.size();
     const size_t s_offsets = 0;
@@ -1227,8 +1298,8 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
     const size_t s_pairs = s_slots + round4(rows);
     const size_t s_batch = s_pairs + round4(2 * n_pairs);
     const size_t s_tiles = s_batch + round4(5 * n_items);
-    const size_t s_order = s_tiles + round4(tiles.size());
-    const size_t words = s_order + (with_order ? rows : 0);
+    const size_t s_plan = s_tiles + round4(tiles.size());
+    const size_t words = s_plan + (with_plan ? plan_words(plan_shape, rows) : 0);
     const size_t up_words = std::max<size_t>(words - s_pairs, 4);
     void* host = nullptr;
     int status = stage(ctx, up_words * sizeof(uint32_t), &host);
@@ -1253,13 +1324,13 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
     }
     if (!tiles.empty())
         std::memcpy(section(s_tiles), tiles.data(), tiles.size() * sizeof(uint32_t));
-    if (with_order)
-        decode_order(positions, pool->sort_keys, section(s_order));
     status = ensure_device(ctx, &pool->d_meta, &pool->d_meta_words, s_pairs + up_words,
                            "metadata buffer");
     if (status)
         return status;
     uint32_t* d = pool->d_meta;
+    if (with_plan)
+        put_plan(pool, plan_shape, section(s_plan), d + s_plan);
     status = upload_staged(ctx, d + s_pairs, up_words * sizeof(uint32_t));
     if (status)
         return status;
@@ -1291,10 +1362,28 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
     m.positions = d + s_positions;
     m.slots = d + s_slots;
     m.tiles = d + s_tiles;
-    m.order = d + s_order;
     m.n_tiles = (uint32_t)(tiles.size() / 2);
     adopt_batch(pool, rows, pool->seq_max * pool->seq_cap, with_slots != 0, shared, fusable,
-                with_order, true);
+                with_plan, true);
+    return CKV_OK;
+}
+
+int ckv_decode_plan(ckv_pool* pool, uint32_t* split_pages, uint32_t* work_items,
+                    uint32_t* records)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    if (!pool->uploaded)
+        return set_error(pool->ctx, CKV_E_NO_TABLES, "plan before ckv_tables_upload");
+    const int status = ensure_plan(pool);
+    if (status)
+        return status;
+    if (split_pages)
+        *split_pages = pool->meta.split_pages;
+    if (work_items)
+        *work_items = pool->meta.n_plan;
+    if (records)
+        *records = pool->meta.n_records;
     return CKV_OK;
 }
 
@@ -1334,6 +1423,10 @@ int check_rope(ckv_pool* pool, size_t heads, float theta, size_t rotary_dim,
     if (head_dim % 2 != 0 || rotary_dim % 2 != 0 || rotary_dim > head_dim)
         return set_error(ctx, CKV_E_INVALID_HEAD_DIMENSION,
                          "head_dim and rotary_dim must be even, rotary_dim <= head_dim");
+    // the kernels take the frequencies of at most max_rope_pairs pairs
+    if (rotary_dim / 2 > ckv::max_rope_pairs)
+        return set_error(ctx, CKV_E_INVALID_HEAD_DIMENSION,
+                         "rotary_dim must be at most " + std::to_string(2 * ckv::max_rope_pairs));
     if (!std::isfinite(theta) || theta <= 0.0f)
         return set_error(ctx, CKV_E_INVALID_ROPE_THETA, "theta must be positive and finite");
     if ((uint64_t)heads * head_dim > UINT32_MAX)
@@ -1462,13 +1555,16 @@ int append_decode_impl(ckv_pool* pool, size_t layer, const void* keys, const voi
     const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     if (pool->fusable && decode_fast_applies(view, (uint32_t)q_heads, queries, output)
         && aligned(keys) && aligned(values)) {
-        status = ensure_order(pool);
+        split_scratch split {};
+        status = ensure_plan(pool);
+        if (!status)
+            status = ensure_split(pool, q_heads, split);
         if (status)
             return status;
         return run_kernel(ctx, "append_decode", [&] {
             return launch_append_decode(ctx->stream, view, pool->meta, (uint32_t)layer, keys,
                                         values, queries, (uint32_t)q_heads, scale, output, gate,
-                                        ctx->cu_count);
+                                        ctx->cu_count, split);
         });
     }
     status = ckv_append(pool, layer, keys, values, rows);
@@ -1588,13 +1684,16 @@ int ckv_rope_append_decode(ckv_pool* pool, size_t layer, const void* keys, const
     const bool lane_pairs = rotary >= 16 && rotary <= 128 && (rotary & (rotary - 1)) == 0;
     if (pool->fusable && lane_pairs && decode_fast_applies(view, (uint32_t)q_heads, queries, output)
         && aligned(keys) && aligned(values) && (!gate || aligned(gate))) {
-        status = ensure_order(pool);
+        split_scratch split {};
+        status = ensure_plan(pool);
+        if (!status)
+            status = ensure_split(pool, q_heads, split);
         if (status)
             return status;
         return run_kernel(ctx, "rope_append_decode", [&] {
             return launch_append_decode(ctx->stream, view, pool->meta, (uint32_t)layer, keys,
                                         values, queries, (uint32_t)q_heads, scale, output, gate,
-                                        ctx->cu_count, &freq, rotary);
+                                        ctx->cu_count, split, &freq, rotary);
         });
     }
     // unfused: queries rotated into a pool buffer, keys rotated into their

@@ -39,13 +39,28 @@ struct meta_view {
     const uint32_t* row_first; // first work item of each row
     const uint32_t* row_count; // work items (chunks) of each row
     const uint32_t* tiles;     // prefill query tiles: (first row, row count) pairs
-    const uint32_t* order;     // rows by decreasing position (longest work first)
+    // fast decode plan: (row, page chunk) pairs in dispatch order, longest
+    // work first; a row's chunk c covers pages [c*split_pages, (c+1)*split_pages)
+    const uint32_t* plan;
+    const uint32_t* split_first; // first partial record of each row cut into chunks
+    const uint32_t* cut;         // the rows cut into chunks (merged after the launch)
     uint32_t n_entries;
     uint32_t rows;
     uint32_t n_items;
     uint32_t chunk; // tokens per decode work item, a multiple of 16
     uint32_t n_tiles;
     uint32_t mean_pages; // pages attended per row, mean over the batch (host side)
+    uint32_t n_plan;      // entries of plan
+    uint32_t split_pages; // pages per chunk of the fast decode; 0: one chunk per row
+    uint32_t n_records;   // partial records of the rows cut into chunks
+    uint32_t n_cut;       // rows cut into chunks
+};
+
+// Device scratch of the fast decode's cut rows: a partial record
+// [max, denominator, 0, 0, acc[head_dim]] per (record, q head), written by the
+// chunks and read by the merge launch that follows them.
+struct split_scratch {
+    float* records;
 };
 
 // Largest query tile, in rows (positions): the prefill kernel covers a tile
@@ -147,10 +162,14 @@ struct ckv_pool {
     std::vector<uint32_t> positions;
     bool shared_tile = false;
     bool fusable = false; // slots are the rows' own positions, one row per table range
-    // derived when a decode launch first needs them: the longest-first row
-    // order (uploaded with the batch when the batch goes to the decode
-    // kernel anyway) and the split-KV work list
-    bool order_ready = false;
+    // while fusable: each row's own table index (offset + position / block_size)
+    // and its uploaded slot, so a table patch can tell whether the fused
+    // append still writes where ckv_append would
+    std::vector<uint32_t> own_index, own_slot;
+    // derived when a decode launch first needs them: the fast decode's plan
+    // (uploaded with the batch when the batch goes to the decode kernel
+    // anyway) and the generic path's split-KV work list
+    bool plan_ready = false;
     bool work_ready = false;
     bool work_multi = false; // some row has more than one chunk: partials are merged
     std::vector<uint32_t> scratch; // host staging of the derived arrays
@@ -161,8 +180,8 @@ struct ckv_pool {
     // device copies
     uint32_t* d_meta = nullptr;
     size_t d_meta_words = 0;
-    uint32_t* d_order = nullptr;
-    size_t d_order_words = 0;
+    uint32_t* d_plan = nullptr; // the plan of a batch uploaded without it
+    size_t d_plan_words = 0;
     uint32_t* d_work = nullptr;
     size_t d_work_words = 0;
     ckv::meta_view meta {};
@@ -213,15 +232,40 @@ hipError_t launch_expand_batch(hipStream_t s, const uint32_t* items, uint32_t n_
                                uint32_t block_size, bool with_slots, uint32_t* offsets,
                                uint32_t* lengths, uint32_t* positions, uint32_t* slots);
 
+// ---- decode plan (kernels_decode.hip) -------------------------------------------
+// The fast decode's plan of a batch, from its rows' positions: how many pages
+// each workgroup covers (0: a row per workgroup), the (row, chunk) items in
+// dispatch order (longest first) and each cut row's first partial record.
+// A row is cut into chunks when one workgroup per (row, kv head) would leave
+// the batch bound by its longest rows: when a row holds more than half of
+// one compute unit's share of the batch's pages. CKV_DECODE_SPLIT=<pages>
+// forces the chunk size (0: no cut).
+struct decode_plan_shape {
+    uint32_t split_pages;
+    uint32_t n_items;
+    uint32_t n_records;
+    uint32_t n_cut;
+};
+decode_plan_shape shape_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
+                                    uint32_t kv_heads, int cu_count);
+// Writes shape.n_items (row, chunk) pairs to plan, rows words to split_first
+// and the shape.n_cut cut rows to cut.
+void write_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
+                       const decode_plan_shape& shape, std::vector<uint64_t>& sort_keys,
+                       uint32_t* plan, uint32_t* split_first, uint32_t* cut);
+
 // ---- launchers (kernels_decode.hip) ------------------------------------------
 // Returns hipErrorInvalidValue when no kernel fits the geometry. The fast
-// path (decode_fast_applies) merges in the workgroup and needs no partials;
-// the generic path writes partials for rows with several chunks.
+// path (decode_fast_applies) merges a chunk's waves in the workgroup; when the
+// plan cuts rows into chunks it needs `split` (records of m.n_records x q_heads)
+// and launches a merge of the cut rows after the chunks; the generic path
+// writes partials for rows with several chunks and needs a merge launch.
 // gate (optional, same shape and dtype as out): out = attention * sigmoid(gate),
 // the sigmoid_mul of src/qwen/qwen_layer.cc:204 in the epilogue.
 hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                          const void* q, uint32_t q_heads, float scale, void* out,
-                         float* partials, int cu_count, const void* gate = nullptr);
+                         float* partials, int cu_count, const void* gate = nullptr,
+                         split_scratch split = {});
 bool decode_fast_applies(const pool_view& p, uint32_t q_heads, const void* q, const void* out);
 // store_kv + fast decode in one launch; the caller has checked
 // decode_fast_applies, 16-byte aligned inputs, and that every row's slot is
@@ -231,7 +275,7 @@ bool decode_fast_applies(const pool_view& p, uint32_t q_heads, const void* q, co
 hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_view& m,
                                 uint32_t layer, const void* k_in, const void* v_in, const void* q,
                                 uint32_t q_heads, float scale, void* out, const void* gate,
-                                int cu_count, const rope_table* rope = nullptr,
+                                int cu_count, split_scratch split, const rope_table* rope = nullptr,
                                 uint32_t rotary = 0);
 hipError_t launch_merge(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t q_heads,
                         void* out, const float* partials, const void* gate = nullptr);

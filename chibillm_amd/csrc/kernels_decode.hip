@@ -19,6 +19,7 @@
 // v_exp_f32.
 #include "ckv_internal.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 
@@ -141,19 +142,27 @@ __host__ __device__ constexpr uint32_t record_floats(uint32_t head_dim)
     return head_dim + 4;
 }
 
-// Fast path, one workgroup per (row, kv_head), W waves. With FUSED, the row's
-// new token (position = the row's last) is taken from k_in/v_in rows instead
-// of the cache and stored into its slot by the wave that owns the last page:
-// the append of store_kv and the attention in one pass. Wave w walks pages
-// w, w+W, w+2W, ... of the row (16-token pages, one scalar table read per
-// page); the next page's K/V loads are issued before the current page is
-// processed. Lane 16*group + part reads features 8*part..8*part+7 of token
+// Fast path, one workgroup per (plan item, kv_head), W waves. A plan item is
+// a row, or one chunk of split_pages pages of a row that the plan cuts (the
+// split-K of paged_attention_partial_f32 / paged_attention_reduce_f32,
+// src/metal/kernels/attention.metal:446-615, for any row). With FUSED, the
+// row's new token (position = the row's last) is taken from k_in/v_in rows
+// instead of the cache and stored into its slot by the wave that owns the
+// last page: the append of store_kv and the attention in one pass. Wave w
+// walks pages first+w, first+w+W, ... of its chunk (16-token pages, one scalar
+// table read per page); the next page's K/V loads are issued before the
+// current page is processed. Lane 16*group + part reads features 8*part..8*part+7 of token
 // 4j + group of the page (j = 0..3): four 1 KiB wave loads per page for K and
 // four for V. The wave's four row-group softmax states are merged with
 // shuffles, the W wave states through LDS, and the workgroup writes the
 // normalised output of the group's q heads. GATED multiplies it by
 // sigmoid(gate) first; the gate values are loaded when the workgroup starts,
-// so their latency hides behind the page loads. ROPE (with FUSED) rotates the
+// so their latency hides behind the page loads. A chunk of a cut row writes
+// its unnormalised state instead (a partial record per q head), which
+// merge_chunks_kernel combines after the launch. (Merging in the chunk that
+// finishes last needs an agent-scope release per workgroup, which on gfx950
+// writes back the XCD's L2: measured at about 1.9 us per workgroup per XCD,
+// far more than the second launch costs.) ROPE (with FUSED) rotates the
 // queries and the new token's key by the row's position first, as rope_f32
 // (src/metal/kernels/tensor_ops.metal:158-195) would: feature f < rotary/2
 // pairs with f + rotary/2, which sits in the lane part ^ (rotary/16) of the
@@ -163,7 +172,7 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
     pool_view p, meta_view m, uint32_t layer, const uint16_t* __restrict__ q, uint32_t q_heads,
     float scale_log2, uint16_t* __restrict__ out, const char* __restrict__ k_in,
     const char* __restrict__ v_in, const uint16_t* __restrict__ gate, rope_table64 freq,
-    uint32_t rotary)
+    uint32_t rotary, split_scratch split)
 {
     using ops = half2_ops<F16>;
     constexpr uint32_t D = 128;
@@ -175,11 +184,18 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
     const uint32_t group = lane >> 4;
     const uint32_t part = lane & 15;
     const uint32_t H = p.kv_heads;
-    const uint32_t row = m.order[blockIdx.x / H];
+    const uint32_t item = blockIdx.x / H;
+    const uint32_t row = m.plan[2 * item];
+    const uint32_t chunk = m.plan[2 * item + 1];
     const uint32_t kv_head = blockIdx.x % H;
     const uint32_t position = m.positions[row];
     const uint32_t n_pages = position / BS + 1;
     const uint32_t last_in_page = position % BS;
+    // this workgroup's pages [pg_first, pg_end) of the row's n_chunks chunks
+    const uint32_t span = m.split_pages ? m.split_pages : n_pages;
+    const uint32_t n_chunks = (n_pages + span - 1) / span;
+    const uint32_t pg_first = chunk * span;
+    const uint32_t pg_end = min(pg_first + span, n_pages);
     uint32_t gate_early = 0; // the first epilogue iteration's gate value (one register)
     if constexpr (GATED) {
         if (threadIdx.x < G * D)
@@ -344,8 +360,8 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
     };
 
     uint4 ka[4], va[4], kb[4], vb[4];
-    uint32_t pg = wave;
-    if (pg < n_pages)
+    uint32_t pg = pg_first + wave;
+    if (pg < pg_end)
         load_page(pg, ka, va);
     // ROPE: rotate the queries and the new key while the first page loads
     if constexpr (ROPE) {
@@ -356,16 +372,16 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
             qv[g] = rotate(qv[g], rc, rs);
         k_new = rotate(k_new, rc, rs);
     }
-    while (pg < n_pages) {
+    while (pg < pg_end) {
         uint32_t next = pg + W;
-        if (next < n_pages)
+        if (next < pg_end)
             load_page(next, kb, vb);
         process(ka, va, pg);
         pg = next;
-        if (pg >= n_pages)
+        if (pg >= pg_end)
             break;
         next = pg + W;
-        if (next < n_pages)
+        if (next < pg_end)
             load_page(next, ka, va);
         process(kb, vb, pg);
         pg = next;
@@ -406,28 +422,129 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
         }
     }
     __syncthreads();
-    uint32_t it = 0;
-    for (uint32_t t = threadIdx.x; t < G * D; t += blockDim.x, ++it) {
-        const uint32_t g = t / D;
-        const uint32_t f = t % D;
-        float M = -INFINITY;
+    // the workgroup's state of q head g, feature f: the W wave states merged
+    auto wg_state = [&](uint32_t g, uint32_t f, float& M, float& d, float& a) {
+        M = -INFINITY;
         for (uint32_t w = 0; w < W; ++w)
             M = fmaxf(M, lds_ml[(w * G + g) * 2]);
-        float d = 0.0f, a = 0.0f;
+        d = 0.0f;
+        a = 0.0f;
         for (uint32_t w = 0; w < W; ++w) {
             const float mw = lds_ml[(w * G + g) * 2];
             const float weight = mw == -INFINITY ? 0.0f : fast_exp2(mw - M);
             d += lds_ml[(w * G + g) * 2 + 1] * weight;
             a += lds_acc[(w * G + g) * D + f] * weight;
         }
+    };
+    auto emit = [&](uint32_t g, uint32_t f, uint32_t it, float o) {
         const uint64_t at = ((uint64_t)row * q_heads + kv_head * G + g) * D + f;
-        float o = a / d;
         if constexpr (GATED) {
             const uint16_t gb = it == 0 ? (uint16_t)gate_early : gate[at];
             o *= sigmoid(half_value<F16>(gb));
         }
         out[at] = static_cast<uint16_t>(F16 ? f16_bits(o) : bf16_bits(o));
+    };
+    if (n_chunks == 1) {
+        uint32_t it = 0;
+        for (uint32_t t = threadIdx.x; t < G * D; t += blockDim.x, ++it) {
+            float M, d, a;
+            wg_state(t / D, t % D, M, d, a);
+            emit(t / D, t % D, it, a / d);
+        }
+        return;
     }
+    // a chunk of a cut row: record [max, denominator, 0, 0, acc[D]] per q head
+    constexpr uint32_t RF = D + 4;
+    const uint64_t record_stride = (uint64_t)q_heads * RF; // between a row's chunks
+    float* const records = split.records
+        + ((uint64_t)m.split_first[row] * q_heads + kv_head * G) * RF;
+    for (uint32_t t = threadIdx.x; t < G * D; t += blockDim.x) {
+        const uint32_t g = t / D, f = t % D;
+        float M, d, a;
+        wg_state(g, f, M, d, a);
+        float* rec = records + chunk * record_stride + g * RF;
+        rec[4 + f] = a;
+        if (f == 0) {
+            rec[0] = M;
+            rec[1] = d;
+        }
+    }
+}
+
+// The rows the plan cut into chunks: one workgroup of 1024 threads per (cut
+// row, kv head). Thread (slice, g, f) folds chunks slice, slice + S, ... of q
+// head g (S = 8 / G slices) into a running (max, denominator, acc[f]) with
+// weights 2^(m_c - M), the reduction of paged_attention_reduce_f32
+// (src/metal/kernels/attention.metal:567-615) done online; the S slices are
+// then folded through LDS, and the result normalised, gated and rounded once,
+// as the single-chunk epilogue does. A row's records are read in parallel:
+// 128 consecutive floats per (chunk, q head), four chunks in flight per thread.
+template <int G, bool F16, bool GATED>
+__global__ __launch_bounds__(1024) void merge_chunks_kernel(
+    pool_view p, meta_view m, uint32_t q_heads, const float* __restrict__ records,
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ gate)
+{
+    constexpr uint32_t D = 128;
+    constexpr uint32_t RF = D + 4;
+    constexpr uint32_t S = 8 / G; // chunk slices per q head
+    __shared__ float fold_acc[S][G][D];
+    __shared__ float fold_ml[S][G][2];
+    const uint32_t H = p.kv_heads;
+    const uint32_t row = m.cut[blockIdx.x / H];
+    const uint32_t kv_head = blockIdx.x % H;
+    const uint32_t n_pages = m.positions[row] / p.block_size + 1;
+    const uint32_t n_chunks = (n_pages + m.split_pages - 1) / m.split_pages;
+    const uint32_t f = threadIdx.x % D;
+    const uint32_t g = (threadIdx.x / D) % G;
+    const uint32_t slice = threadIdx.x / (D * G);
+    const uint64_t stride = (uint64_t)q_heads * RF;
+    const float* rec = records + ((uint64_t)m.split_first[row] * q_heads + kv_head * G + g) * RF;
+    const uint64_t at = ((uint64_t)row * q_heads + kv_head * G + g) * D + f;
+    uint16_t gb = 0;
+    if constexpr (GATED)
+        gb = gate[at];
+    float M = -INFINITY, d = 0.0f, a = 0.0f;
+    auto fold = [&](float mc, float dc, float ac) {
+        const float nm = fmaxf(M, mc);
+        const float keep = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
+        const float take = fast_exp2(mc - nm);
+        d = d * keep + dc * take;
+        a = a * keep + ac * take;
+        M = nm;
+    };
+    uint32_t c = slice;
+    for (; c + 3 * S < n_chunks; c += 4 * S) {
+        float mc[4], dc[4], ac[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float* r = rec + (c + u * S) * stride;
+            mc[u] = r[0];
+            dc[u] = r[1];
+            ac[u] = r[4 + f];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            fold(mc[u], dc[u], ac[u]);
+    }
+    for (; c < n_chunks; c += S) {
+        const float* r = rec + c * stride;
+        fold(r[0], r[1], r[4 + f]);
+    }
+    fold_acc[slice][g][f] = a;
+    if (f == 0) {
+        fold_ml[slice][g][0] = M;
+        fold_ml[slice][g][1] = d;
+    }
+    __syncthreads();
+    if (slice != 0)
+        return;
+    for (uint32_t t = 1; t < S; ++t)
+        if (fold_ml[t][g][0] != -INFINITY) // a slice with no chunk holds nothing
+            fold(fold_ml[t][g][0], fold_ml[t][g][1], fold_acc[t][g][f]);
+    float o = a / d;
+    if constexpr (GATED)
+        o *= sigmoid(half_value<F16>(gb));
+    out[at] = static_cast<uint16_t>(F16 ? f16_bits(o) : bf16_bits(o));
 }
 
 // ---- generic path: any head_dim <= 1024, f32 / bf16 / fp16 ---------------------
@@ -463,6 +580,21 @@ __device__ __forceinline__ float wave_sum(float v)
 }
 
 constexpr int generic_max_features_per_lane = 16; // head_dim <= 1024
+
+// Cut rows (shape_decode_plan): a chunk is a quarter of a compute unit's
+// share of the batch's (page, kv head) units, at least split_min_pages, and
+// no row has more than split_max_chunks chunks (the merge of a row reads its
+// chunks' records: measured on MI355X, a 32K-token row cut into 128 chunks of
+// 16 pages decodes in 24 us and merges in 7.5 us, in 32 chunks of 64 pages
+// the pair takes 29 us in all); its workgroup has split_waves waves. On one
+// MI355X layer (bf16, 8 kv heads): batch 32 of U[256, 4096] tokens 54-55 us
+// for chunks of 16-48 pages (62.5 us uncut); one 5,000-token row 10.8 us at
+// 12 pages (49 us uncut); one 32K-token row 29-32 us at 16-64 pages (356 us
+// uncut).
+constexpr uint64_t split_per_share = 4;
+constexpr uint64_t split_min_pages = 12;
+constexpr uint64_t split_max_chunks = 32;
+constexpr uint32_t split_waves = 8;
 
 // One wave per (work item, kv_head); the group's q heads are processed one
 // after another, each with the per-token online softmax of
@@ -601,8 +733,10 @@ bool aligned16(const void* ptr)
 // of 50-160 pages, the two tie at 256 pages and 10 is 2.7 % faster at 288
 // (config 3); with 1-2 units per CU, 8 waves is 7-16 % slower. A smaller
 // batch takes the maximum (16, or 8 for larger groups) so each row streams
-// as fast as one CU allows. CKV_DECODE_WAVES overrides.
-uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count, uint32_t mean_pages)
+// as fast as one CU allows. Chunks of cut rows take split_waves (a chunk is
+// short, and several of them share a CU). CKV_DECODE_WAVES overrides.
+uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count, uint32_t mean_pages,
+                    uint32_t split_pages)
 {
     const uint32_t limit = group <= 2 ? 16u : 8u;
     if (const char* forced = std::getenv("CKV_DECODE_WAVES")) {
@@ -610,6 +744,8 @@ uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count, uint32_t mean_
         if (v >= 1 && v <= (long)limit)
             return (uint32_t)v;
     }
+    if (split_pages)
+        return std::min(limit, split_waves);
     if (group <= 2 && cu_count > 0 && units >= (uint32_t)cu_count)
         return units / (uint32_t)cu_count >= 6 && mean_pages < 256 ? 8 : 10;
     return limit;
@@ -619,10 +755,13 @@ template <int G>
 hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                        const void* q, uint32_t q_heads, float scale_log2, void* out, bool f16,
                        const void* k_in, const void* v_in, const void* gate, int cu_count,
-                       const rope_table* rope = nullptr, uint32_t rotary = 0)
+                       split_scratch split, const rope_table* rope = nullptr,
+                       uint32_t rotary = 0)
 {
-    const uint32_t units = m.rows * p.kv_heads;
-    const uint32_t waves = fast_waves(G, units, cu_count, m.mean_pages);
+    if (!m.plan || (m.n_cut && !split.records))
+        return hipErrorInvalidValue;
+    const uint32_t units = m.n_plan * p.kv_heads;
+    const uint32_t waves = fast_waves(G, units, cu_count, m.mean_pages, m.split_pages);
     const dim3 grid(units), block(64 * waves);
     // the merge's (acc, max, denominator) per wave, then the rope angle table
     const size_t lds = ((size_t)waves * G * (128 + 2) + (rope ? 2 * 64 : 0)) * sizeof(float);
@@ -637,11 +776,12 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
             f64.inv_freq[j] = rope->inv_freq[j];
     // one instantiation per (dtype, fused, gated, rope); rope only when fused
     const int variant = (rope ? 8 : 0) | (f16 ? 4 : 0) | (k_in ? 2 : 0) | (gate ? 1 : 0);
+    const float* records = split.records;
     switch (variant) {
 #define CKV_FAST_CASE(V, F16_, FUSED_, GATED_, ROPE_)                                          \
     case V:                                                                                    \
         decode_wg_kernel<G, F16_, FUSED_, GATED_, ROPE_><<<grid, block, lds, s>>>(            \
-            p, m, layer, qq, q_heads, scale_log2, oo, ki, vi, gg, f64, rotary);                \
+            p, m, layer, qq, q_heads, scale_log2, oo, ki, vi, gg, f64, rotary, split);         \
         break;
         CKV_FAST_CASE(0, false, false, false, false)
         CKV_FAST_CASE(1, false, false, true, false)
@@ -659,10 +799,117 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
     default:
         return hipErrorInvalidValue;
     }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !m.n_cut)
+        return e;
+    const dim3 merge_grid(m.n_cut * p.kv_heads), merge_block(1024);
+    switch ((f16 ? 2 : 0) | (gate ? 1 : 0)) {
+    case 0:
+        merge_chunks_kernel<G, false, false><<<merge_grid, merge_block, 0, s>>>(
+            p, m, q_heads, records, oo, gg);
+        break;
+    case 1:
+        merge_chunks_kernel<G, false, true><<<merge_grid, merge_block, 0, s>>>(
+            p, m, q_heads, records, oo, gg);
+        break;
+    case 2:
+        merge_chunks_kernel<G, true, false><<<merge_grid, merge_block, 0, s>>>(
+            p, m, q_heads, records, oo, gg);
+        break;
+    default:
+        merge_chunks_kernel<G, true, true><<<merge_grid, merge_block, 0, s>>>(
+            p, m, q_heads, records, oo, gg);
+        break;
+    }
     return hipGetLastError();
 }
 
 } // namespace
+
+decode_plan_shape shape_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
+                                    uint32_t kv_heads, int cu_count)
+{
+    decode_plan_shape shape { 0, (uint32_t)positions.size(), 0, 0 };
+    uint64_t total = 0, longest = 0;
+    for (const uint32_t p : positions) {
+        const uint64_t pages = p / block_size + 1;
+        total += pages;
+        longest = std::max(longest, pages);
+    }
+    uint64_t span = 0;
+    if (const char* forced = std::getenv("CKV_DECODE_SPLIT")) {
+        span = (uint64_t)std::max(0L, std::strtol(forced, nullptr, 10));
+    } else {
+        // a compute unit's share of the batch, in (page, kv head) units
+        const uint64_t share = total * kv_heads / (uint64_t)std::max(cu_count, 1);
+        if (2 * longest > share)
+            span = std::max({ split_min_pages, (share + split_per_share - 1) / split_per_share,
+                              (longest + split_max_chunks - 1) / split_max_chunks });
+    }
+    if (span == 0 || span >= longest)
+        return shape; // a row per workgroup
+    uint64_t items = 0, records = 0, cut = 0;
+    for (const uint32_t p : positions) {
+        const uint64_t n = (p / block_size + span) / span; // chunks of (p / bs + 1) pages
+        items += n;
+        records += n > 1 ? n : 0;
+        cut += n > 1 ? 1 : 0;
+    }
+    if (items > UINT32_MAX / kv_heads || records > UINT32_MAX || cut > UINT32_MAX / kv_heads)
+        return shape;
+    shape.split_pages = (uint32_t)span;
+    shape.n_items = (uint32_t)items;
+    shape.n_records = (uint32_t)records;
+    shape.n_cut = (uint32_t)cut;
+    return shape;
+}
+
+void write_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
+                       const decode_plan_shape& shape, std::vector<uint64_t>& sort_keys,
+                       uint32_t* plan, uint32_t* split_first, uint32_t* cut)
+{
+    const size_t rows = positions.size();
+    if (!shape.split_pages) {
+        // rows by decreasing position (ties in row order): the longest first
+        sort_keys.resize(rows);
+        for (size_t r = 0; r < rows; ++r)
+            sort_keys[r] = ((uint64_t)(UINT32_MAX - positions[r]) << 32) | r;
+        std::sort(sort_keys.begin(), sort_keys.end());
+        for (size_t r = 0; r < rows; ++r) {
+            plan[2 * r] = (uint32_t)sort_keys[r];
+            plan[2 * r + 1] = 0;
+            split_first[r] = 0;
+        }
+        return;
+    }
+    // chunks by decreasing page count: the full chunks of every row (row after
+    // row), then the short last chunks, longest first
+    const uint32_t span = shape.split_pages;
+    uint32_t record = 0;
+    size_t at = 0, n_cut = 0;
+    sort_keys.clear();
+    for (size_t r = 0; r < rows; ++r) {
+        const uint32_t pages = positions[r] / block_size + 1;
+        const uint32_t n = (pages + span - 1) / span, full = pages / span;
+        split_first[r] = n > 1 ? record : 0;
+        record += n > 1 ? n : 0;
+        if (n > 1)
+            cut[n_cut++] = (uint32_t)r;
+        for (uint32_t c = 0; c < full; ++c, ++at) {
+            plan[2 * at] = (uint32_t)r;
+            plan[2 * at + 1] = c;
+        }
+        if (full < n)
+            sort_keys.push_back(((uint64_t)(span - (pages - full * span)) << 32) | r);
+    }
+    std::sort(sort_keys.begin(), sort_keys.end());
+    for (const uint64_t key : sort_keys) {
+        const uint32_t r = (uint32_t)key;
+        plan[2 * at] = r;
+        plan[2 * at + 1] = (positions[r] / block_size + 1) / span; // the last chunk
+        ++at;
+    }
+}
 
 bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads)
 {
@@ -678,7 +925,7 @@ bool decode_fast_applies(const pool_view& p, uint32_t q_heads, const void* q, co
 
 hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                          const void* q, uint32_t q_heads, float scale, void* out,
-                         float* partials, int cu_count, const void* gate)
+                         float* partials, int cu_count, const void* gate, split_scratch split)
 {
     if (!m.rows)
         return hipSuccess;
@@ -688,16 +935,16 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
         switch (q_heads / p.kv_heads) {
         case 1:
             return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr, gate, cu_count);
+                                  nullptr, gate, cu_count, split);
         case 2:
             return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr, gate, cu_count);
+                                  nullptr, gate, cu_count, split);
         case 4:
             return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr, gate, cu_count);
+                                  nullptr, gate, cu_count, split);
         default:
             return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
-                                  nullptr, gate, cu_count);
+                                  nullptr, gate, cu_count, split);
         }
     }
     if (p.head_dim > 64u * generic_max_features_per_lane)
@@ -723,7 +970,8 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
 hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_view& m,
                                 uint32_t layer, const void* k_in, const void* v_in, const void* q,
                                 uint32_t q_heads, float scale, void* out, const void* gate,
-                                int cu_count, const rope_table* rope, uint32_t rotary)
+                                int cu_count, split_scratch split, const rope_table* rope,
+                                uint32_t rotary)
 {
     if (!m.rows)
         return hipSuccess;
@@ -734,16 +982,16 @@ hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_vi
     switch (q_heads / p.kv_heads) {
     case 1:
         return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
-                              cu_count, rope, rotary);
+                              cu_count, split, rope, rotary);
     case 2:
         return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
-                              cu_count, rope, rotary);
+                              cu_count, split, rope, rotary);
     case 4:
         return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
-                              cu_count, rope, rotary);
+                              cu_count, split, rope, rotary);
     default:
         return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
-                              cu_count, rope, rotary);
+                              cu_count, split, rope, rotary);
     }
 }
 

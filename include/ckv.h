@@ -187,9 +187,12 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
                       const uint32_t* positions, const uint32_t* slots, size_t rows);
 /* Device-side delta update of the uploaded block table: table[idx[i]] = val[i],
  * so a block_manager change is mirrored without re-sending the table. Rows'
- * offsets/lengths are unchanged; every idx must be < n_entries
- * (block_table_range_out_of_bounds) and every val < blocks
- * (cache_block_out_of_range). */
+ * offsets/lengths and the uploaded slots are unchanged; every idx must be
+ * < n_entries (block_table_range_out_of_bounds) and every val < blocks
+ * (cache_block_out_of_range). A patch that moves the page holding a row's own
+ * position away from that row's uploaded slot leaves ckv_append_decode on its
+ * unfused form (ckv_append to the uploaded slot, then the attention through
+ * the patched table), as store_kv followed by paged_attention would. */
 int ckv_tables_patch(ckv_pool* pool, const uint32_t* idx, const uint32_t* val, size_t n);
 
 /* ---- Device-resident sequence tables (prepare_paged_batch on the device) ----
@@ -238,6 +241,16 @@ int ckv_seq_tables_update(ckv_pool* pool, const uint32_t* seq, const uint32_t* i
 int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_position,
                      const uint32_t* token_count, size_t n_items, int with_slots);
 
+/* The fast decode's plan of the current batch (deriving it if a decode launch
+ * has not yet): pages per workgroup chunk (0 when every (row, kv head) is one
+ * workgroup), work items (rows or row chunks) and partial records. A row is
+ * cut into chunks when one workgroup per (row, kv head) would leave the batch
+ * bound by its longest rows; the chunks are merged as
+ * paged_attention_reduce_f32 merges (src/metal/kernels/attention.metal:567-615).
+ * A diagnostic with no counterpart in the reference, for tests and tuning. */
+int ckv_decode_plan(ckv_pool* pool, uint32_t* split_pages, uint32_t* work_items,
+                    uint32_t* records);
+
 /* ---- Ops -------------------------------------------------------------------------- */
 /* store_kv (src/tensor/tensor_ops.cc:412-463; kernel src/metal/kernels/attention.metal:3-33):
  * keys/values are device [rows, kv_heads*head_dim] of the pool dtype; row r is
@@ -255,10 +268,13 @@ int ckv_gather(ckv_pool* pool, size_t layer, size_t table_offset, size_t table_l
  * to logical positions 0..positions[r] through their table range:
  * out = softmax(q . k * scale) . v with fp32 accumulation. queries and
  * output are device [rows, q_heads*head_dim] of the pool dtype.
- * Decode form: split-KV over fixed token chunks of each (row, kv_head), the
- * q heads of a GQA group sharing every K/V read, then a merge
- * (paged_attention_partial_f32 / paged_attention_reduce_f32,
- * src/metal/kernels/attention.metal:446-615, generalised to every row).
+ * Decode form: the q heads of a GQA group share every K/V read. 16-bit pools
+ * with head_dim 128 and 16-token pages take one workgroup per (row, kv_head),
+ * or per page chunk of rows the batch plan cuts (ckv_decode_plan), the chunks
+ * merged by the last to finish; other geometries take split-KV over token
+ * chunks and a merge launch. Both are the split-K of
+ * paged_attention_partial_f32 / paged_attention_reduce_f32
+ * (src/metal/kernels/attention.metal:446-615), generalised to every row.
  * Checks: invalid_head_count, invalid_kv_head_mapping (q_heads % kv_heads),
  * cache_layer_out_of_range, position_count_mismatch (rows != uploaded rows). */
 int ckv_decode_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
@@ -315,8 +331,9 @@ int ckv_sigmoid_mul(ckv_context* ctx, int dtype, const void* gate, const void* i
  * j + rotary_dim/2 by position * theta^(-2j/rotary_dim); the rest is copied.
  * rotary_dim 0 means head_dim. input may equal output (in place). Checks, in
  * the reference's order: position_count_mismatch (rows != uploaded rows),
- * invalid_head_count, invalid_head_dimension (odd head_dim or rotary_dim, or
- * rotary_dim > head_dim), invalid_rope_theta (not positive and finite). */
+ * invalid_head_count, invalid_head_dimension (odd head_dim or rotary_dim,
+ * rotary_dim > head_dim, or rotary_dim > 1024), invalid_rope_theta (not
+ * positive and finite). */
 int ckv_rope(ckv_pool* pool, const void* input, void* output, size_t heads, float theta,
              size_t rotary_dim, size_t rows);
 /* rope of the key rows fused with ckv_append: the apply_rope + store_kv pair

@@ -165,9 +165,14 @@ def test_gated_prefill_tiles(ctx, group):
     pool.close()
 
 
-def test_append_decode_gated_equals_fused_pair(ctx):
+@pytest.mark.parametrize("split", [None, "3"])
+def test_append_decode_gated_equals_fused_pair(ctx, split, monkeypatch):
     """The decode step's fused append + attention with the gate: pages bit-exact
-    with ckv_append_decode, output within tolerance of the oracle."""
+    with ckv_append_decode, output within tolerance of the oracle; also with
+    every row cut into chunks of 3 pages (the gate applied by the chunk that
+    merges)."""
+    if split:
+        monkeypatch.setenv("CKV_DECODE_SPLIT", split)
     code = orc.BF16
     rng, lengths, tables, blocks = decode_case(5, batch=16)
     H, Hq = 8, 16

@@ -291,10 +291,14 @@ def fill_by_append(pool, lengths, tables, ks, vs, layer=0, code=orc.BF16):
         pool.append(layer, to_dev(k, code), to_dev(v, code))
 
 
-@pytest.mark.parametrize("chunk", [None, "32", "4096"])
-def test_config2_bf16_decode_over_permuted_pages(ctx, chunk, monkeypatch):
-    if chunk:
-        monkeypatch.setenv("CKV_DECODE_CHUNK", chunk)
+@pytest.mark.parametrize("split", [None, "0", "4", "17", "64"])
+def test_config2_bf16_decode_over_permuted_pages(ctx, split, monkeypatch):
+    """Config 2 through the fast decode kernel: the batch plan's default cut
+    (rows of up to 256 pages on 256 compute units are cut into chunks), no cut,
+    and forced chunks of 4, 17 and 64 pages; each checked against the oracle
+    and against the plan the library reports."""
+    if split is not None:
+        monkeypatch.setenv("CKV_DECODE_SPLIT", split)
     lengths, tables, ks, vs, q = config2_inputs()
     pool, _, _ = new_pool(ctx, (1, 65536, 16, 8, 128), orc.BF16)
     fill_by_append(pool, lengths, tables, ks, vs)
@@ -309,10 +313,56 @@ def test_config2_bf16_decode_over_permuted_pages(ctx, chunk, monkeypatch):
     flat = np.concatenate(tables)
     offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
     pool.upload(flat, offsets, [len(t) for t in tables], [n - 1 for n in lengths])
+    span, items, records = pool.decode_plan()
+    pages = [-(-n // 16) for n in lengths]
+    if split == "0":
+        assert (span, items, records) == (0, 32, 0)
+    else:
+        assert span == (int(split) if split else span) and span > 0
+        assert items == sum(-(-p // span) for p in pages)
+        assert records == sum(-(-p // span) for p in pages if p > span)
+        assert records > 0, "some row must be cut into several chunks"
     out = torch.empty(32, 16 * 128, dtype=torch.bfloat16, device="cuda")
     pool.decode(0, to_dev(q, orc.BF16), 16, float(np.float32(1 / math.sqrt(128))), out)
     expected = compact_oracle((8, 128), lengths, tables, ks, vs, q, 16)
-    assert_close(to_f32(out), expected, what=f"config 2 decode (chunk {chunk})")
+    assert_close(to_f32(out), expected, what=f"config 2 decode (split {split})")
+    ctx.sync()
+    pool.close()
+
+
+def misaligned(rows, width):
+    """A contiguous bf16 [rows, width] view 2 bytes past a 16-byte boundary:
+    the fast decode kernel needs 16-byte aligned queries and outputs, so such
+    views take the generic split-KV kernel."""
+    base = torch.empty(rows * width + 8, dtype=torch.bfloat16, device="cuda")
+    view = base[1:1 + rows * width].view(rows, width)
+    assert view.data_ptr() % 16 == 2
+    return view
+
+
+@pytest.mark.parametrize("chunk", ["32", "4096"])
+def test_config2_generic_split_kv_chunks(ctx, chunk, monkeypatch):
+    """Config 2 through the generic kernel (misaligned queries and output):
+    token chunks of 32 cut every row (256..4096 tokens) into 8..128 partials
+    merged by the merge launch; chunks of 4096 leave every row whole."""
+    monkeypatch.setenv("CKV_DECODE_CHUNK", chunk)
+    lengths, tables, ks, vs, q = config2_inputs(seed=11, batch=12)
+    pool, _, _ = new_pool(ctx, (1, 65536, 16, 8, 128), orc.BF16)
+    fill_by_append(pool, lengths, tables, ks, vs)
+    flat = np.concatenate(tables)
+    offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
+    pool.upload(flat, offsets, [len(t) for t in tables], [n - 1 for n in lengths])
+    qd = misaligned(len(lengths), 16 * 128)
+    qd.copy_(to_dev(q, orc.BF16))
+    out = misaligned(len(lengths), 16 * 128)
+    ctx.profile(True)
+    ctx.profile_reset()
+    pool.decode(0, qd, 16, float(np.float32(1 / math.sqrt(128))), out)
+    _, merges = ctx.profile_query("paged_attention_merge")
+    ctx.profile(False)
+    assert merges == (1 if chunk == "32" else 0), "chunks of 32 tokens need the merge launch"
+    expected = compact_oracle((8, 128), lengths, tables, ks, vs, q, 16)
+    assert_close(to_f32(out), expected, what=f"generic decode (chunk {chunk})")
     ctx.sync()
     pool.close()
 

@@ -200,11 +200,13 @@ def decode_rows(rng, code, batch, H, Hq, bs=16, D=128):
     return case
 
 
-@pytest.mark.parametrize("code,group,rotary,gated", [
-    (orc.BF16, 2, 0, False), (orc.F16, 2, 0, False), (orc.BF16, 1, 64, False),
-    (orc.BF16, 8, 32, False), (orc.BF16, 2, 0, True), (orc.F16, 4, 16, True),
-    (orc.BF16, 2, 48, False), (orc.F32, 2, 0, True)])
-def test_rope_append_decode_equals_unfused_sequence(ctx, code, group, rotary, gated):
+@pytest.mark.parametrize("code,group,rotary,gated,split", [
+    (orc.BF16, 2, 0, False, None), (orc.F16, 2, 0, False, None), (orc.BF16, 1, 64, False, None),
+    (orc.BF16, 8, 32, False, None), (orc.BF16, 2, 0, True, None), (orc.F16, 4, 16, True, None),
+    (orc.BF16, 2, 48, False, None), (orc.F32, 2, 0, True, None), (orc.BF16, 2, 0, True, "2"),
+    (orc.F16, 4, 32, False, "3")])
+def test_rope_append_decode_equals_unfused_sequence(ctx, code, group, rotary, gated, split,
+                                                   monkeypatch):
     """ckv_rope_append_decode (the fused decode kernel rotating queries and the
     new keys in registers; rotary 48 and f32 take the unfused form) against
     ckv_rope + ckv_rope_append + the attention, and against the oracle
@@ -213,8 +215,10 @@ def test_rope_append_decode_equals_unfused_sequence(ctx, code, group, rotary, ga
     two kernels that rotate it (each is within one of the oracle), so rotated
     keys are compared within one ulp and outputs within the attention tolerance
     (the unfused form's own outputs are compared bit for bit: same kernels)."""
-    print(f"rope_append_decode dtype {code} group {group} rotary {rotary} gated {gated}",
-          flush=True)
+    print(f"rope_append_decode dtype {code} group {group} rotary {rotary} gated {gated} "
+          f"split {split}", flush=True)
+    if split:  # rows cut into chunks of `split` pages (the chunk that merges applies the gate)
+        monkeypatch.setenv("CKV_DECODE_SPLIT", split)
     rng = orc.Mt64(60 + 7 * group + code + rotary + gated)
     H = 8 if group <= 2 else 2
     Hq = H * group

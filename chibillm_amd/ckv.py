@@ -62,6 +62,7 @@ _SIGNATURES = [
     ("ckv_gather", _i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp]),
     ("ckv_decode_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
     ("ckv_append_decode", _i, [_vp, _sz, _vp, _vp, _vp, _sz, C.c_float, _vp, _sz]),
+    ("ckv_append_decode_noalloc", _i, [_vp, _sz, _vp, _vp, _vp, _sz, C.c_float, _vp, _sz]),
     ("ckv_prefill_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
     ("ckv_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
     ("ckv_rope", _i, [_vp, _vp, _vp, _sz, C.c_float, _sz, _sz]),
@@ -320,6 +321,14 @@ class Pool:
         self.ctx.check(load().ckv_append_decode(self.handle, layer, _ptr(keys), _ptr(values),
                                                 _ptr(queries), q_heads, scale, _ptr(output),
                                                 rows))
+
+    def append_decode_noalloc(self, layer, keys, values, queries, q_heads, scale, output,
+                              rows=None) -> None:
+        """ckv_append_decode without allocating (ckv_append_decode_noalloc)."""
+        rows = queries.shape[0] if rows is None else rows
+        self.ctx.check(load().ckv_append_decode_noalloc(self.handle, layer, _ptr(keys),
+                                                        _ptr(values), _ptr(queries), q_heads,
+                                                        scale, _ptr(output), rows))
 
     def prefill(self, layer, queries, q_heads, scale, output, rows=None) -> None:
         self._attend(load().ckv_prefill_attention, layer, queries, q_heads, scale, output, rows)

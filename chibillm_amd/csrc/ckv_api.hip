@@ -9,15 +9,51 @@
 #include <cmath>
 
 #include <algorithm>
+#include <array>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <unordered_map>
 #include <unordered_set>
 
 using namespace ckv;
 
+// Scratch of ckv_append_decode_noalloc: the partial records of the rows its
+// batch plan cuts into chunks. Every GPU the library runs on holds its own copy
+// of this array until the process ends. In host code `noalloc_scratch` is a
+// host-side stand-in, not a device address: kernels are given the address
+// hipGetSymbolAddress returns for the current device (ckv_context::noalloc_scratch).
+constexpr size_t noalloc_scratch_bytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char noalloc_scratch[noalloc_scratch_bytes];
+
 namespace {
+
+// hipGetSymbolAddress once per device, under a lock (contexts of different
+// threads may be created at once); the result is kept per device ordinal.
+constexpr int max_scratch_devices = 64;
+std::mutex scratch_lock;
+std::array<void*, max_scratch_devices> scratch_address {};
+std::array<bool, max_scratch_devices> scratch_looked_up {};
+
+// With `device` current: this device's address of noalloc_scratch, or null.
+void* device_scratch(int device)
+{
+    if (device < 0 || device >= max_scratch_devices)
+        return nullptr;
+    std::lock_guard<std::mutex> hold(scratch_lock);
+    if (!scratch_looked_up[device]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(noalloc_scratch));
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            ptr = nullptr;
+        }
+        scratch_address[device] = ptr;
+        scratch_looked_up[device] = true;
+    }
+    return scratch_address[device];
+}
 
 int set_error(ckv_context* ctx, int code, const std::string& detail)
 {
@@ -690,6 +726,10 @@ int ckv_context_create(int device, ckv_context** out)
     }
     ctx->cu_count = props.multiProcessorCount;
     ctx->stream = ctx->own_stream;
+    // the device is current: its copy of the no-allocation scratch
+    ctx->noalloc_scratch = device_scratch(device);
+    // room for any detail text, so that storing one never allocates
+    ctx->last_error.reserve(512);
     *out = ctx;
     return CKV_OK;
 }
@@ -1709,6 +1749,82 @@ int ckv_rope_append_decode(ckv_pool* pool, size_t layer, const void* keys, const
     if (status)
         return status;
     return run_decode(pool, layer, pool->d_rope_q, q_heads, scale, output, gate);
+}
+
+namespace {
+
+// A status with a fixed detail text, stored in the context's reserved
+// string: no allocation.
+int fail_fixed(ckv_context* ctx, int code, const char* text)
+{
+    ctx->last_error.assign(text);
+    return code;
+}
+
+} // namespace
+
+int ckv_append_decode_noalloc(ckv_pool* pool, size_t layer, const void* keys, const void* values,
+                              const void* queries, size_t q_heads, float scale, void* output,
+                              size_t rows)
+{
+    if (!pool)
+        return CKV_E_INVALID_ARGUMENT;
+    ckv_context* ctx = pool->ctx;
+    // the checks of ckv_append_decode, in its order, with fixed texts
+    if (rows && (!keys || !values))
+        return fail_fixed(ctx, CKV_E_INVALID_ARGUMENT, "keys and values are required");
+    if (!pool->uploaded || !pool->has_slots)
+        return fail_fixed(ctx, CKV_E_NO_TABLES, "append before slots were uploaded");
+    if (rows != pool->slot_rows)
+        return fail_fixed(ctx, CKV_E_CACHE_SLOT_COUNT_MISMATCH, "rows != uploaded slots");
+    if (rows && (!queries || !output))
+        return fail_fixed(ctx, CKV_E_INVALID_ARGUMENT, "queries and output are required");
+    if (rows != pool->positions.size())
+        return fail_fixed(ctx, CKV_E_POSITION_COUNT_MISMATCH, "rows != uploaded positions");
+    if (q_heads == 0)
+        return fail_fixed(ctx, CKV_E_INVALID_HEAD_COUNT, "q_heads == 0");
+    if (q_heads % pool->kv_heads != 0)
+        return fail_fixed(ctx, CKV_E_INVALID_KV_HEAD_MAPPING, "q_heads % kv_heads != 0");
+    if (layer >= pool->layers)
+        return fail_fixed(ctx, CKV_E_CACHE_LAYER_OUT_OF_RANGE, "layer >= layers");
+    if (!rows)
+        return CKV_OK;
+    // what only this entry point requires
+    const pool_view view = view_of(pool);
+    if (!decode_fast_applies(view, (uint32_t)q_heads, queries, output))
+        return fail_fixed(ctx, CKV_E_INVALID_ARGUMENT,
+                          "no-allocation decode: needs a bf16/fp16 pool with head_dim 128, "
+                          "16-token pages, 1, 2, 4 or 8 q heads per kv head and 16-byte "
+                          "aligned pools, queries and output");
+    if (!pool->plan_ready)
+        return fail_fixed(ctx, CKV_E_INVALID_ARGUMENT,
+                          "no-allocation decode: the batch has multi-row query tiles, so its "
+                          "decode plan was not uploaded with it");
+    const meta_view& m = pool->meta;
+    const uint64_t need = (uint64_t)m.n_records * q_heads * partial_record_floats(128) * sizeof(float);
+    if (need > noalloc_scratch_bytes)
+        return fail_fixed(ctx, CKV_E_INVALID_ARGUMENT,
+                          "no-allocation decode: the batch's partial records exceed the "
+                          "16 MiB scratch (fewer or shorter rows cut into chunks fit)");
+    if (m.n_cut && !ctx->noalloc_scratch)
+        return fail_fixed(ctx, CKV_E_HIP_FAILURE,
+                          "no-allocation decode: the scratch array has no device address");
+    const split_scratch split { static_cast<float*>(ctx->noalloc_scratch) };
+    const bool fused = pool->fusable && reinterpret_cast<uintptr_t>(keys) % 16 == 0
+        && reinterpret_cast<uintptr_t>(values) % 16 == 0;
+    hipError_t e = hipSuccess;
+    if (fused) {
+        e = launch_append_decode(ctx->stream, view, m, (uint32_t)layer, keys, values, queries,
+                                 (uint32_t)q_heads, scale, output, nullptr, ctx->cu_count, split);
+    } else {
+        e = launch_store_kv(ctx->stream, view, m, (uint32_t)layer, keys, values, (uint32_t)rows);
+        if (e == hipSuccess)
+            e = launch_decode(ctx->stream, view, m, (uint32_t)layer, queries, (uint32_t)q_heads,
+                              scale, output, nullptr, ctx->cu_count, nullptr, split);
+    }
+    if (e != hipSuccess)
+        return fail_fixed(ctx, CKV_E_HIP_FAILURE, hipGetErrorString(e));
+    return CKV_OK;
 }
 
 int ckv_sigmoid_mul(ckv_context* ctx, int dtype, const void* gate, const void* input,

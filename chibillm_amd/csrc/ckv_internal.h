@@ -138,6 +138,11 @@ struct ckv_context {
     staging_slot staging[staging_slots];
     int staging_next = 0; // the slot stage() hands out
 
+    // this device's copy of the no-allocation entry point's scratch array
+    // (its device address, from hipGetSymbolAddress at context creation; null
+    // if that failed)
+    void* noalloc_scratch = nullptr;
+
     bool profile = false;
     std::vector<ckv::pending_timing> pending;
     std::vector<hipEvent_t> spare_events;

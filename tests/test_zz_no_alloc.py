@@ -1,0 +1,119 @@
+"""ckv_append_decode_noalloc (the decode step for callers that cannot allocate:
+its partial records go to the library's fixed per-GPU scratch array) against
+ckv_append_decode through the C ABI: the same pages and outputs bit for bit,
+on two calls in a row, the second with a smaller batch, and the oracle within
+2e-2 abs + 1e-2 rel. Also what it refuses instead of allocating."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from chibillm_amd import ckv
+from oracle import oracle as orc
+from tests.gpu_util import assert_close, new_context, new_pool, to_dev, to_f32
+from tests.test_gpu_parity import compact_oracle, fill_by_append
+
+pytestmark = pytest.mark.gpu
+
+SCALE = float(np.float32(1 / math.sqrt(128)))
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = new_context()
+    yield c
+    c.sync()
+    c.close()
+
+
+def batch(seed, lengths, B):
+    rng = orc.Mt64(seed)
+    perm = rng.permutation(B)
+    tables, at = [], 0
+    for n in lengths:
+        tables.append(perm[at:at + -(-n // 16)])
+        at += len(tables[-1])
+    F = 8 * 128
+    ks = [rng.normal(n * F, orc.BF16).reshape(n, F) for n in lengths]
+    vs = [rng.normal(n * F, orc.BF16).reshape(n, F) for n in lengths]
+    q = rng.normal(len(lengths) * 2048, orc.BF16).reshape(len(lengths), -1)
+    return tables, ks, vs, q
+
+
+def test_noalloc_equals_append_decode_on_two_calls(ctx):
+    """Call 1: six rows of 1 to 20,000 tokens (the plan cuts the long ones into
+    chunks, so the scratch records are used); call 2: three shorter rows on
+    another layer. Each call's pages and output equal ckv_append_decode's bit
+    for bit; the outputs are within tolerance of the oracle."""
+    calls = [([20000, 9000, 300, 17, 1, 4100], 0, 101), ([6000, 2500, 33], 1, 202)]
+    B = sum(-(-n // 16) for n in calls[0][0]) + sum(-(-n // 16) for n in calls[1][0]) + 8
+    pools = [new_pool(ctx, (2, B, 16, 8, 128), orc.BF16, fill=float("nan")) for _ in range(2)]
+    for lengths, layer, seed in calls:
+        print(f"noalloc call: rows {lengths}, layer {layer}", flush=True)
+        tables, ks, vs, q = batch(seed, lengths, B)
+        flat = np.concatenate(tables)
+        offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
+        positions = [n - 1 for n in lengths]
+        slots = [orc.slot(t, p, 16) for t, p in zip(tables, positions)]
+        outs = []
+        for which, (pool, _, _) in enumerate(pools):
+            fill_by_append(pool, [n - 1 for n in lengths], tables, [k[:-1] for k in ks],
+                           [v[:-1] for v in vs], layer=layer)
+            pool.upload(flat, offsets, [len(t) for t in tables], positions, slots)
+            span, _, records = pool.decode_plan()
+            assert span > 0 and records > 0, "the batch must use the scratch records"
+            k_new = to_dev(np.stack([k[-1] for k in ks]), orc.BF16)
+            v_new = to_dev(np.stack([v[-1] for v in vs]), orc.BF16)
+            out = torch.full((len(lengths), 2048), float("nan"), dtype=torch.bfloat16,
+                             device="cuda")
+            args = (layer, k_new, v_new, to_dev(q, orc.BF16), 16, SCALE, out)
+            if which == 0:
+                pool.append_decode(*args)
+            else:
+                pool.append_decode_noalloc(*args)
+            ctx.sync()
+            outs.append(out)
+        assert torch.equal(outs[0], outs[1]), "noalloc output differs from ckv_append_decode"
+        for a, b in zip(pools[0][1:], pools[1][1:]):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16)), "pages differ"
+        expected = compact_oracle((8, 128), lengths, tables, ks, vs, q, 16)
+        assert_close(to_f32(outs[1]), expected, what=f"noalloc rows {lengths}")
+    for pool, _, _ in pools:
+        pool.close()
+
+
+def test_noalloc_refuses_instead_of_allocating(ctx, monkeypatch):
+    """A batch of multi-row query tiles (no decode plan uploaded), an f32 pool
+    and a plan whose records exceed the 16 MiB array are refused with
+    invalid_argument; nothing is launched."""
+    q = torch.zeros(4, 2048, dtype=torch.bfloat16, device="cuda")
+    kv = torch.zeros(4, 1024, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty_like(q)
+    pool, _, _ = new_pool(ctx, (1, 2100, 16, 8, 128), orc.BF16)
+    # four rows of one sequence at consecutive positions: a prefill tile
+    pool.upload([0, 1], [0] * 4, [2] * 4, [3, 4, 5, 6], slots=[3, 4, 5, 6])
+    with pytest.raises(ckv.CkvError) as e:
+        pool.append_decode_noalloc(0, kv, kv, q, 16, SCALE, out)
+    assert e.value.name == "ckv.invalid_argument" and "query tiles" in str(e.value)
+    # four rows of 8,000 tokens cut into 1-page chunks: 2,000 records x 16 q
+    # heads x 528 bytes > 16 MiB
+    monkeypatch.setenv("CKV_DECODE_SPLIT", "1")
+    flat = np.arange(2000, dtype=np.uint32)
+    pool.upload(flat, [0, 500, 1000, 1500], [500] * 4, [7999] * 4,
+                slots=[(500 * r + 499) * 16 + 15 for r in range(4)])
+    assert pool.decode_plan()[2] == 2000
+    with pytest.raises(ckv.CkvError) as e:
+        pool.append_decode_noalloc(0, kv, kv, q, 16, SCALE, out)
+    assert e.value.name == "ckv.invalid_argument" and "16 MiB" in str(e.value)
+    monkeypatch.delenv("CKV_DECODE_SPLIT")
+    pool.close()
+    f32, _, _ = new_pool(ctx, (1, 4, 16, 8, 128), orc.F32)
+    f32.upload([0, 1, 2, 3], [0, 1, 2, 3], [1] * 4, [0] * 4, slots=[0, 16, 32, 48])
+    qf = torch.zeros(4, 2048, device="cuda")
+    kf = torch.zeros(4, 1024, device="cuda")
+    with pytest.raises(ckv.CkvError) as e:
+        f32.append_decode_noalloc(0, kf, kf, qf, 16, SCALE, torch.empty_like(qf))
+    assert e.value.name == "ckv.invalid_argument"
+    ctx.sync()
+    f32.close()

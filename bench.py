@@ -16,6 +16,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -26,8 +27,12 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
 # HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE /
-# WRITE_SIZE passes scaled by a known-size copy (written by those passes)
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "append_decode_config3_traffic.json")
+# WRITE_SIZE passes scaled by a known-size copy (chibillm_amd/rocprof_summary.py
+# traffic writes these files from those passes)
+TRAFFIC_FILES = {
+    "config3": os.path.join(ROOT, "profiles", "append_decode_config3_traffic.json"),
+    "config2": os.path.join(ROOT, "profiles", "decode_config2_traffic.json"),
+}
 LAYERS, BATCH, KV_HEADS, Q_HEADS, HEAD_DIM, BLOCK = 28, 128, 8, 16, 128, 16
 CTX_LO, CTX_HI = 1024, 8192
 
@@ -36,29 +41,62 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def traffic_bytes(kernel):
+def traffic_bytes(workload, kernel):
     """Measured HBM bytes per launch of `kernel` if a counter summary exists."""
     try:
-        with open(TRAFFIC_FILE) as fh:
+        with open(TRAFFIC_FILES[workload]) as fh:
             data = json.load(fh)
-    except OSError:
+    except (OSError, KeyError):
         return None
     entry = data.get("kernels", {}).get(kernel)
     return None if entry is None else int(entry["hbm_bytes_per_launch"])
 
 
-def cpu_baseline(threads, budget_s=10.0):
-    """Oracle decode attention (the CPU restatement of the reference kernel,
-    fp32 accumulation) on a bounded sample of the workload: the full batch of
-    128 sequences at the same length distribution, bf16 K/V of one layer,
-    attended layer after layer until about `budget_s` seconds have passed (at
-    most 28 layers). The K/V pages hold a tiled block of N(0,1) values: the
-    timing does not depend on the values."""
+# ---- CPU baseline (the oracle: a C restatement of the reference path) ----------------
+
+BOX_CPU_SHARE = 16  # host threads one GPU's box gives a job, whatever os.cpu_count() shows
+
+
+def baseline_threads(args):
+    return args.cpu_threads or min(os.cpu_count() or 1, BOX_CPU_SHARE)
+
+
+def cpu_model():
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def median_seconds(fn, runs):
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def host_decode_batch(lengths, seed):
+    """One layer of bf16 K/V on the host for rows of `lengths` tokens on permuted
+    pages, and bf16 queries: the oracle's attention over them. The pages hold a
+    tiled block of N(0,1) values (the timing does not depend on the values)."""
     from oracle import oracle as orc
 
-    gen = np.random.default_rng(1)
-    rows = BATCH
-    lengths = [int(x) for x in gen.integers(CTX_LO, CTX_HI + 1, rows)]
+    gen = np.random.default_rng(seed)
     F = KV_HEADS * HEAD_DIM
     pages = [math.ceil(n / BLOCK) for n in lengths]
     n_pages = sum(pages)
@@ -66,53 +104,206 @@ def cpu_baseline(threads, budget_s=10.0):
     reps = -(-(n_pages * BLOCK * F) // block.size)
     kc = np.tile(block, reps)[:n_pages * BLOCK * F]
     vc = np.roll(kc, 12345)
-    q = orc.from_f32(gen.standard_normal((rows, Q_HEADS * HEAD_DIM), np.float32), orc.BF16)
+    q = orc.from_f32(gen.standard_normal((len(lengths), Q_HEADS * HEAD_DIM), np.float32),
+                     orc.BF16)
     perm = gen.permutation(n_pages).astype(np.uint32)
     offsets = np.cumsum([0] + pages[:-1])
-    att = orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, orc.BF16, q, orc.BF16,
-                        [n - 1 for n in lengths], perm, offsets, pages, Q_HEADS, 0,
-                        1 / math.sqrt(HEAD_DIM))
+    return orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, orc.BF16, q, orc.BF16,
+                         [n - 1 for n in lengths], perm, offsets, pages, Q_HEADS, 0,
+                         1 / math.sqrt(HEAD_DIM))
+
+
+def cpu_decode_baseline(lengths, threads, runs, with_step=False):
+    """The CPU path of one decode step at these lengths, timed on this host
+    (median of `runs` each): decode attention over one layer on `threads`
+    threads and on one thread (oracle/oracle.c, the restated
+    paged_attention_f32 with fp32 accumulation), and with_step: the append of
+    one K/V row per sequence into a layer (store_kv) and the host work of the
+    step, block_manager reservations plus prepare_paged_batch."""
+    from oracle import oracle as orc
+
+    F = KV_HEADS * HEAD_DIM
     layer_bytes = sum(lengths) * F * 2 * 2
-    layers = 0
-    t0 = time.perf_counter()
-    while layers < LAYERS and (layers == 0 or time.perf_counter() - t0 < budget_s):
-        att.online_threads(threads)
-        layers += 1
-    dt = time.perf_counter() - t0
-    one = orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, orc.BF16, q[:4],
-                        orc.BF16, [n - 1 for n in lengths[:4]], perm, offsets[:4], pages[:4],
-                        Q_HEADS, 0, 1 / math.sqrt(HEAD_DIM))
-    t1 = time.perf_counter()
-    one.online_threads(1)
-    dt1 = time.perf_counter() - t1
-    single_gbs = sum(lengths[:4]) * F * 4 / dt1 / 1e9
-    return {
-        "value": round(layers * layer_bytes / dt / 1e9, 3),
+    att = host_decode_batch(lengths, 1)
+    all_s = median_seconds(lambda: att.online_threads(threads), runs)
+    single_s = median_seconds(lambda: att.online_threads(1), runs)
+    out = {
+        "value": round(layer_bytes / all_s / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle/oracle.c decode attention (restated paged_attention_f32, fp32 "
-                   f"accumulate) over {rows} sequences ({sum(lengths)} tokens, "
-                   f"{layer_bytes / 1e9:.2f} GB of bf16 K/V per layer) x {layers} layers in "
-                   f"{dt:.1f} s on {threads} threads; single-thread {single_gbs:.3f} GB/s on 4 "
-                   f"of them"),
+        "threads": threads,
+        "cores_total": os.cpu_count(),
+        "cpu_model": cpu_model(),
+        "median_of": runs,
+        "single_thread": {"value": round(layer_bytes / single_s / 1e9, 3), "unit": "GB/s"},
+        "legs_ms": {"decode_attention_per_layer": round(all_s * 1e3, 3),
+                    "decode_attention_per_layer_single_thread": round(single_s * 1e3, 3)},
     }
+    del att
+    if with_step:
+        rows = len(lengths)
+        gen = np.random.default_rng(2)
+        k = orc.from_f32(gen.standard_normal((rows, F), np.float32), orc.BF16)
+        pages = sum(math.ceil((n + 1) / BLOCK) for n in lengths) + 1
+        kc = np.zeros(pages * BLOCK * F, np.uint16)
+        vc = np.zeros_like(kc)
+        slots = gen.permutation(pages * BLOCK)[:rows].astype(np.uint32)
+        reps = 100
+        append_s = median_seconds(
+            lambda: [orc.store_kv(kc, vc, k, k, slots, 0, pages * BLOCK) for _ in range(reps)],
+            runs) / reps
 
+        def host_steps():
+            step = orc.DecodeStepHost(lengths, pages + rows, BLOCK,
+                                      math.ceil(max(lengths) / BLOCK) + 2)
+            t0 = time.perf_counter()
+            step.step()
+            return time.perf_counter() - t0
+
+        host_s = statistics.median(host_steps() for _ in range(runs))
+        out["legs_ms"]["append_store_kv_per_layer"] = round(append_s * 1e3, 4)
+        out["legs_ms"]["block_manager_and_prepare_paged_batch_per_step"] = round(host_s * 1e3, 4)
+    return out
+
+
+def calibration_copy(ctx):
+    """A copy of known size for scaling the HBM counters: ckv_copy_blocks of 1024
+    pages of 32 KiB, keys and values (64 MiB read, 64 MiB written)."""
+    from chibillm_amd import ckv
+
+    calib = ckv.Pool(ctx, 1, 2048, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16)
+    calib.copy_blocks(np.arange(1024), np.arange(1024, 2048))
+    ctx.sync()
+    calib.close()
+    log("calibration copy: 1024 pages x 32 KiB, keys + values = 64 MiB read, 64 MiB written")
+
+
+# ---- config 2: single-layer decode attention -----------------------------------------
+
+CONFIG2_BATCH, CONFIG2_POOL = 32, 65536
+CONFIG2_LO, CONFIG2_HI = 256, 4096
+
+
+def bench_config2(args):
+    """one layer, batch 32, contexts U[256, 4096], 16-token
+    pages from a seeded permutation of a 65,536-page pool. A step is one
+    ckv_decode_attention call (its decode launch, and its merge launch when the
+    plan cuts rows) over the uploaded batch; one event pair on the launch
+    stream brackets the timed steps (an event pair per 55 us step would add
+    its own gaps)."""
+    import torch
+
+    from chibillm_amd import ckv
+
+    steps = 2000 if args.steps == 20 else args.steps
+    device = torch.device("cuda:0")
+    gen = np.random.default_rng(args.seed)
+    lengths = [int(x) for x in gen.integers(CONFIG2_LO, CONFIG2_HI + 1, CONFIG2_BATCH)]
+    perm = gen.permutation(CONFIG2_POOL).astype(np.uint32)
+    pages = [math.ceil(n / BLOCK) for n in lengths]
+    flat = perm[:sum(pages)]
+    offsets = np.cumsum([0] + pages[:-1])
+    F = KV_HEADS * HEAD_DIM
+    ctx = ckv.Context(0, stream=torch.cuda.current_stream())
+    if args.calibrate_copy:
+        calibration_copy(ctx)
+    tgen = torch.Generator(device=device)
+    tgen.manual_seed(args.seed)
+    elems = CONFIG2_POOL * BLOCK * F
+    keys = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=tgen)
+    values = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=tgen)
+    pool = ckv.Pool(ctx, 1, CONFIG2_POOL, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16, keys, values)
+    q = torch.randn(CONFIG2_BATCH, Q_HEADS * HEAD_DIM, generator=tgen, device=device).to(
+        torch.bfloat16)
+    out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(HEAD_DIM)
+    pool.upload(flat, offsets, pages, [n - 1 for n in lengths])
+    split_pages, items, records = pool.decode_plan()
+    log(f"config2: {sum(lengths)} tokens, plan: chunks of {split_pages} pages, {items} items, "
+        f"{records} records")
+    for _ in range(args.warmup * 10):
+        pool.decode(0, q, Q_HEADS, scale, out)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        pool.decode(0, q, Q_HEADS, scale, out)
+    end.record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    launch_ms = start.elapsed_time(end) / steps
+    kv_bytes = sum(lengths) * F * 2 * 2
+    per_launch = kv_bytes + 2 * CONFIG2_BATCH * Q_HEADS * HEAD_DIM * 2 + 4 * sum(pages)
+    achieved = per_launch / (launch_ms / 1e3) / 1e9
+    result = {
+        "metric": "paged decode KV-read GB/s (% HBM peak), Qwen3-0.6B KV, one layer, batch 32",
+        "value": round(kv_bytes / (launch_ms / 1e3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup * 10,
+        "ms_per_step": round(launch_ms, 5),
+        "wall_ms_per_step": round(elapsed * 1e3 / steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) K/V/Q, seeded lengths and page permutation",
+        "config": {
+            "workload": "config2: single-layer paged GQA decode attention, batch 32, context "
+                        "U[256,4096], pages from a seeded permutation of a 65,536-page pool",
+            "batch": CONFIG2_BATCH, "kv_heads": KV_HEADS, "q_heads": Q_HEADS,
+            "head_dim": HEAD_DIM, "block_size": BLOCK, "pool_pages": CONFIG2_POOL,
+            "tokens": sum(lengths), "plan": {"split_pages": split_pages, "items": items,
+                                             "records": records},
+        },
+        "hbm_frac": round(kv_bytes / (launch_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "kernel": "paged_attention_decode (decode_wg_kernel + merge_chunks_kernel)",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_bytes("config2", "decode"),
+            "avg_launch_us": round(launch_ms * 1e3, 3),
+            "algorithmic_bytes_per_launch": int(per_launch),
+        },
+        "cpu_baseline": None,
+    }
+    pool.close()
+    del keys, values
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        threads = baseline_threads(args)
+        log(f"CPU baseline on {threads} threads")
+        base = cpu_decode_baseline(lengths, threads, runs=5)
+        base["sample"] = (f"the whole workload: oracle/oracle.c decode attention (restated "
+                          f"paged_attention_f32, fp32 accumulate) over the same {CONFIG2_BATCH} "
+                          f"rows ({sum(lengths)} tokens, {kv_bytes / 1e9:.3f} GB of bf16 K/V), "
+                          f"median of 5 runs on {threads} threads and 5 on one")
+        result["cpu_baseline"] = base
+    return result
+
+
+# ---- config 3: the 28-layer decode step (headline) -----------------------------------
 
 def bench_config3(args):
     import torch
 
     from chibillm_amd import ckv
-    from oracle import oracle as orc  # seeded lengths / page order only
 
     device = torch.device("cuda:0")
-    rng = orc.Mt64(args.seed)
-    lengths = np.array([rng.uniform_int(CTX_LO, CTX_HI) for _ in range(BATCH)], np.int64)
-    total_steps = args.warmup + args.steps
+    gen = np.random.default_rng(args.seed)
+    lengths = gen.integers(CTX_LO, CTX_HI + 1, BATCH).astype(np.int64)
+    profile_steps = min(args.steps, 5)
+    total_steps = args.warmup + args.steps + profile_steps
     max_len = lengths + total_steps
     pages_needed = [math.ceil(n / BLOCK) for n in max_len]
     n_pool = sum(pages_needed) + 64
-    perm = rng.permutation(n_pool)
+    perm = gen.permutation(n_pool).astype(np.uint32)
     F = KV_HEADS * HEAD_DIM
     max_pages = max(pages_needed)
 
@@ -137,41 +328,39 @@ def bench_config3(args):
         f"context tokens {int(lengths.sum())}")
     ctx = ckv.Context(0, stream=torch.cuda.current_stream())
     if args.calibrate_copy:
-        calib = ckv.Pool(ctx, 1, 2048, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16)
-        calib.copy_blocks(np.arange(1024), np.arange(1024, 2048))
-        ctx.sync()
-        calib.close()
-        log("calibration copy: 1024 pages x 32 KiB, keys + values = 64 MiB read, 64 MiB written")
+        calibration_copy(ctx)
     elems = LAYERS * n_pool * BLOCK * F
     keys = torch.empty(elems, dtype=torch.bfloat16, device=device)
     values = torch.empty(elems, dtype=torch.bfloat16, device=device)
-    gen = torch.Generator(device=device)
-    gen.manual_seed(args.seed)
+    tgen = torch.Generator(device=device)
+    tgen.manual_seed(args.seed)
     t0 = time.perf_counter()
     step = 1 << 30
     for buf in (keys, values):
         for i in range(0, elems, step):
-            buf[i:i + step].normal_(generator=gen)
+            buf[i:i + step].normal_(generator=tgen)
     torch.cuda.synchronize()
     log(f"filled K/V with N(0,1) in {time.perf_counter() - t0:.1f} s")
     pool = ckv.Pool(ctx, LAYERS, n_pool, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16, keys, values)
 
-    q = torch.randn(LAYERS, BATCH, Q_HEADS * HEAD_DIM, generator=gen, device=device).to(torch.bfloat16)
-    k_new = torch.randn(LAYERS, BATCH, F, generator=gen, device=device).to(torch.bfloat16)
-    v_new = torch.randn(LAYERS, BATCH, F, generator=gen, device=device).to(torch.bfloat16)
+    q = torch.randn(LAYERS, BATCH, Q_HEADS * HEAD_DIM, generator=tgen, device=device).to(torch.bfloat16)
+    k_new = torch.randn(LAYERS, BATCH, F, generator=tgen, device=device).to(torch.bfloat16)
+    v_new = torch.randn(LAYERS, BATCH, F, generator=tgen, device=device).to(torch.bfloat16)
     out = torch.empty(LAYERS, BATCH, Q_HEADS * HEAD_DIM, dtype=torch.bfloat16, device=device)
-    gate = (torch.randn(LAYERS, BATCH, Q_HEADS * HEAD_DIM, generator=gen, device=device)
+    gate = (torch.randn(LAYERS, BATCH, Q_HEADS * HEAD_DIM, generator=tgen, device=device)
             .to(torch.bfloat16) if args.gate else None)
     scale = 1.0 / math.sqrt(HEAD_DIM)
     offsets = np.arange(BATCH, dtype=np.uint32) * max_pages
 
-    def one_step():
+    def one_step(start=None, end=None):
         positions = lengths.copy()  # the new token's position
         for s in range(BATCH):
             ensure_pages(s, int(positions[s]) + 1)
         slots = [int(flat[s * max_pages + p // BLOCK]) * BLOCK + p % BLOCK
                  for s, p in enumerate(positions)]
         pool.upload(flat, offsets, owned, positions, slots)
+        if start is not None:
+            start.record()
         for layer in range(LAYERS):
             if args.no_fuse:
                 pool.append(layer, k_new[layer], v_new[layer])
@@ -186,6 +375,8 @@ def bench_config3(args):
             else:
                 pool.append_decode(layer, k_new[layer], v_new[layer], q[layer], Q_HEADS, scale,
                                    out[layer])
+        if end is not None:
+            end.record()
         attended = positions + 1
         lengths[:] = attended
         return int(attended.sum()), int(sum(math.ceil(a / BLOCK) for a in attended))
@@ -195,24 +386,32 @@ def bench_config3(args):
     torch.cuda.synchronize()
     log(f"warmup {args.warmup} steps done")
 
-    ctx.profile(True)
-    ctx.profile_reset()
+    # the timed region: whole steps, no per-launch timing; one event pair per
+    # step on the launch stream brackets its 28 launches (after the upload)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     tokens_attended = pages_read = 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        toks, pages = one_step()
+    for i in range(args.steps):
+        toks, pages = one_step(starts[i], ends[i])
         tokens_attended += toks
         pages_read += pages
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    launches_ms = sum(a.elapsed_time(b) for a, b in zip(starts, ends))
+    log(f"timed {args.steps} steps in {elapsed:.3f} s")
+
+    # a separate, profiled pass: per-kernel times from events around every launch
     dominant = ("paged_attention_decode" if args.no_fuse
                 else "rope_append_decode" if args.rope else "append_decode")
-    decode_ms, decode_n = ctx.profile_query(dominant)
-    merge_ms, merge_n = ctx.profile_query("paged_attention_merge")
-    store_ms, store_n = ctx.profile_query("store_kv")
+    ctx.profile(True)
+    ctx.profile_reset()
+    for _ in range(profile_steps):
+        one_step()
+    kernels = {name: ctx.profile_query(name)
+               for name in (dominant, "paged_attention_merge", "store_kv")}
     ctx.profile(False)
-    log(f"timed {args.steps} steps in {elapsed:.3f} s")
 
     kv_row_bytes = F * 2 * 2  # K + V, bf16, all KV heads
     kv_bytes = LAYERS * tokens_attended * kv_row_bytes
@@ -224,8 +423,9 @@ def bench_config3(args):
     qo_rows = 3 if args.gate else 2  # Q and O, and the gate when it is read
     per_launch = (tokens_attended * kv_row_bytes + pages_read * 4
                   + args.steps * (qo_rows * BATCH * Q_HEADS * HEAD_DIM * 2 + appended)) / args.steps
-    decode_avg_s = decode_ms / decode_n / 1e3
-    achieved = per_launch / decode_avg_s / 1e9
+    launches = LAYERS * args.steps * (2 if args.no_fuse else 1)
+    avg_launch_s = launches_ms / launches / 1e3
+    achieved = per_launch / (launches_ms / (LAYERS * args.steps) / 1e3) / 1e9
     result = {
         "metric": "paged decode KV-read GB/s (% HBM peak) + tokens/s, Qwen3-0.6B KV, batch 128",
         "value": round(value, 2),
@@ -255,11 +455,9 @@ def bench_config3(args):
         },
         "tokens_per_s": round(BATCH * args.steps / elapsed, 1),
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
-        "kernels_ms_per_step": {
-            dominant: round(decode_ms / args.steps, 4),
-            "paged_attention_merge": round(merge_ms / args.steps, 4),
-            "store_kv": round(store_ms / args.steps, 4),
-        },
+        "launch_ms_per_step": round(launches_ms / args.steps, 4),
+        "kernels_ms_per_step_profiled_pass": {
+            name: round(ms / max(profile_steps, 1), 4) for name, (ms, _) in kernels.items()},
         "roofline": {
             "kernel": dominant,
             "bound": "hbm",
@@ -267,9 +465,10 @@ def bench_config3(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_bytes(dominant),
-            "avg_launch_us": round(decode_avg_s * 1e6, 2),
+            "traffic": traffic_bytes("config3", dominant),
+            "avg_launch_us": round(avg_launch_s * 1e6, 2),
             "algorithmic_bytes_per_launch": int(per_launch),
+            "timing": "one event pair per step around its 28 launches, launch gaps included",
         },
         "cpu_baseline": None,
     }
@@ -277,9 +476,25 @@ def bench_config3(args):
     del keys, values
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
+        threads = baseline_threads(args)
         log(f"CPU baseline on {threads} threads")
-        result["cpu_baseline"] = cpu_baseline(threads)
+        base_lengths = [int(x) for x in np.random.default_rng(args.seed).integers(
+            CTX_LO, CTX_HI + 1, BATCH)]
+        base = cpu_decode_baseline(base_lengths, threads, runs=5, with_step=True)
+        legs = base["legs_ms"]
+        step_ms = (LAYERS * (legs["decode_attention_per_layer"]
+                             + legs["append_store_kv_per_layer"])
+                   + legs["block_manager_and_prepare_paged_batch_per_step"])
+        base["step_ms"] = round(step_ms, 2)
+        base["tokens_per_s"] = round(BATCH / (step_ms / 1e3), 1)
+        base["sample"] = (f"one layer of the workload, scaled by {LAYERS}: oracle/oracle.c decode "
+                          f"attention (restated paged_attention_f32, fp32 accumulate) over the "
+                          f"{BATCH} rows ({sum(base_lengths)} tokens, "
+                          f"{sum(base_lengths) * F * 4 / 1e9:.2f} GB of bf16 K/V per layer), "
+                          f"store_kv of the {BATCH} new rows, and the step's block_manager + "
+                          f"prepare_paged_batch; median of 5 runs each, on {threads} threads "
+                          f"and on one")
+        result["cpu_baseline"] = base
     return result
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
@@ -294,39 +509,47 @@ def prefill_flops(prefix, chunk, seqs):
     return 4 * HEAD_DIM * Q_HEADS * seqs * keys
 
 
-def prefill_cpu_baseline(threads, prefix):
-    """Oracle causal attention (restated paged_flash_attention_prefill_f32 maths,
-    fp32) on a bounded sample: 4 sequences x 256 chunk rows of one layer."""
+def prefill_cpu_baseline(threads, prefix, runs=5):
+    """Oracle causal attention (restated paged_flash_attention_prefill_f32
+    maths, fp32) on bounded samples of one layer: 4 sequences x 256 chunk rows
+    on `threads` threads and 1 sequence x 128 rows on one thread, median of
+    `runs` each."""
     from oracle import oracle as orc
 
-    gen = np.random.default_rng(2)
-    seqs, rows = 4, 256
-    F = KV_HEADS * HEAD_DIM
-    pages = math.ceil((prefix + rows) / BLOCK)
-    n_pages = pages * seqs
-    kc = orc.from_f32(gen.standard_normal(n_pages * BLOCK * F, np.float32), orc.BF16)
-    vc = orc.from_f32(gen.standard_normal(n_pages * BLOCK * F, np.float32), orc.BF16)
-    q = orc.from_f32(gen.standard_normal((seqs * rows, Q_HEADS * HEAD_DIM), np.float32),
-                     orc.BF16)
-    table = gen.permutation(n_pages).astype(np.uint32)
-    positions = [prefix + i for _ in range(seqs) for i in range(rows)]
-    offsets = [s * pages for s in range(seqs) for _ in range(rows)]
-    att = orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, orc.BF16, q, orc.BF16,
-                        positions, table, offsets, [pages] * len(positions), Q_HEADS, 0,
-                        1 / math.sqrt(HEAD_DIM))
-    t0 = time.perf_counter()
-    att.online_threads(threads)
-    dt = time.perf_counter() - t0
-    flops = prefill_flops(prefix, rows, seqs)
+    def sample(seqs, rows, seed):
+        gen = np.random.default_rng(seed)
+        F = KV_HEADS * HEAD_DIM
+        pages = math.ceil((prefix + rows) / BLOCK)
+        n_pages = pages * seqs
+        kc = orc.from_f32(gen.standard_normal(n_pages * BLOCK * F, np.float32), orc.BF16)
+        vc = orc.from_f32(gen.standard_normal(n_pages * BLOCK * F, np.float32), orc.BF16)
+        q = orc.from_f32(gen.standard_normal((seqs * rows, Q_HEADS * HEAD_DIM), np.float32),
+                         orc.BF16)
+        table = gen.permutation(n_pages).astype(np.uint32)
+        positions = [prefix + i for _ in range(seqs) for i in range(rows)]
+        offsets = [s * pages for s in range(seqs) for _ in range(rows)]
+        return orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, orc.BF16, q,
+                             orc.BF16, positions, table, offsets, [pages] * len(positions),
+                             Q_HEADS, 0, 1 / math.sqrt(HEAD_DIM))
+
+    big, small = sample(4, 256, 2), sample(1, 128, 3)
+    all_s = median_seconds(lambda: big.online_threads(threads), runs)
+    single_s = median_seconds(lambda: small.online_threads(1), runs)
+    flops, flops1 = prefill_flops(prefix, 256, 4), prefill_flops(prefix, 128, 1)
     return {
-        "value": round(flops / dt / 1e9, 3),
+        "value": round(flops / all_s / 1e9, 3),
         "unit": "GFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle/oracle.c causal attention over paged bf16 K/V, fp32 accumulate: "
-                   f"1 layer x {seqs} sequences x {rows} rows at positions {prefix}.."
-                   f"{prefix + rows - 1} ({flops / 1e9:.1f} GFLOP) in {dt:.2f} s on "
-                   f"{threads} threads"),
+        "threads": threads,
+        "cores_total": os.cpu_count(),
+        "cpu_model": cpu_model(),
+        "median_of": runs,
+        "single_thread": {"value": round(flops1 / single_s / 1e9, 3), "unit": "GFLOP/s"},
+        "sample": (f"oracle/oracle.c causal attention over paged bf16 K/V, fp32 accumulate, one "
+                   f"layer: 4 sequences x 256 rows at positions {prefix}..{prefix + 255} "
+                   f"({flops / 1e9:.1f} GFLOP) on {threads} threads, and 1 x 128 rows "
+                   f"({flops1 / 1e9:.1f} GFLOP) on one; median of {runs} runs each"),
     }
 
 
@@ -338,7 +561,6 @@ def bench_config4(args):
     import torch
 
     from chibillm_amd import ckv
-    from oracle import oracle as orc  # seeded page order only
 
     device = torch.device("cuda:0")
     prefix, S, C = args.prefix, PREFILL_SEQS, PREFILL_CHUNK
@@ -348,7 +570,7 @@ def bench_config4(args):
     prefix_pages = math.ceil(prefix / BLOCK)
     own = math.ceil((prefix + C) / BLOCK) - full
     n_pool = prefix_pages + S * own + 16
-    perm = orc.Mt64(args.seed).permutation(n_pool)
+    perm = np.random.default_rng(args.seed).permutation(n_pool).astype(np.uint32)
     prefix_table = perm[:prefix_pages]
     tables = [np.concatenate([prefix_table[:full],
                               perm[prefix_pages + s * own:prefix_pages + (s + 1) * own]])
@@ -461,7 +683,7 @@ def bench_config4(args):
     del keys, values, q, k_new, v_new, out
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
+        threads = baseline_threads(args)
         log(f"CPU baseline on {threads} threads")
         result["cpu_baseline"] = prefill_cpu_baseline(threads, prefix)
     return result
@@ -479,14 +701,13 @@ def bench_spill(args):
     import torch
 
     from chibillm_amd import ckv
-    from oracle import oracle as orc  # seeded page order only
 
     device = torch.device("cuda:0")
     tokens = args.prefix
     F = KV_HEADS * HEAD_DIM
     pages = math.ceil(tokens / BLOCK)
     n_pool = 2 * pages + 16
-    perm = orc.Mt64(args.seed).permutation(n_pool)
+    perm = np.random.default_rng(args.seed).permutation(n_pool).astype(np.uint32)
     src, dst = perm[:pages], perm[pages:2 * pages]
     ctx = ckv.Context(0, stream=torch.cuda.current_stream())
     elems = LAYERS * n_pool * BLOCK * F
@@ -624,10 +845,23 @@ def bench_config5(args):
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
+        threads = baseline_threads(args)
         log(f"CPU baseline on {threads} threads")
-        base = cpu_baseline(threads)
-        base["sample"] = "decode attention, the dominant work of the trace: " + base["sample"]
+        base_lengths = [int(x) for x in np.random.default_rng(args.seed).integers(
+            CTX_LO, CTX_HI + 1, BATCH)]
+        base = cpu_decode_baseline(base_lengths, threads, runs=5, with_step=True)
+        legs = base["legs_ms"]
+        step_ms = (LAYERS * (legs["decode_attention_per_layer"]
+                             + legs["append_store_kv_per_layer"])
+                   + legs["block_manager_and_prepare_paged_batch_per_step"])
+        base["kv_read_gbs"] = base["value"]
+        base["value"] = round(BATCH / (step_ms / 1e3), 1)
+        base["unit"] = "tokens/s"
+        base["sample"] = (f"a decode step of {BATCH} rows at U[{CTX_LO},{CTX_HI}] tokens, the "
+                          f"dominant work of the trace, one layer scaled by {LAYERS}: "
+                          f"oracle/oracle.c decode attention, store_kv and the step's "
+                          f"block_manager + prepare_paged_batch; median of 5 runs each on "
+                          f"{threads} threads (attention also on one)")
         result["cpu_baseline"] = base
     return result
 
@@ -645,9 +879,11 @@ def main():
                          "written), the known-size copy the HBM counters are scaled by")
     ap.add_argument("--no-fuse", action="store_true",
                     help="append and decode as two launches instead of ckv_append_decode")
-    ap.add_argument("--workload", choices=["config3", "config4", "config5", "spill"],
+    ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5", "spill"],
                     default="config3",
-                    help="config3 (default): the headline decode step; config4: chunked "
+                    help="config3 (default): the headline decode step; config2: one layer of "
+                         "decode attention, batch 32 (a step is one launch, default 2000 "
+                         "steps); config4: chunked "
                          "prefill of 64 sequences over a shared prefix (MFMA tiles); config5: "
                          "the continuous-batching churn trace (C++ scheduler driver); spill: "
                          "a cached prefix exported to host memory and imported back")
@@ -669,7 +905,9 @@ def main():
               "(run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
-    if args.workload == "config4":
+    if args.workload == "config2":
+        result = bench_config2(args)
+    elif args.workload == "config4":
         result = bench_config4(args)
     elif args.workload == "config5":
         result = bench_config5(args)

@@ -316,6 +316,74 @@ size_t orc_bm_free_count(const orc_block_manager* bm)
     return bm->size;
 }
 
+int orc_prepare_paged_batch(size_t n_items, const uint32_t* token_count,
+                            const uint32_t* tables, const size_t* table_start,
+                            const uint32_t* table_len, const uint32_t* positions,
+                            size_t max_positions, size_t block_count, size_t block_size,
+                            uint32_t* flat_table, uint32_t* slots, uint32_t* offsets,
+                            uint32_t* lengths)
+{
+    /* src/model_batch.cc:132-139: empty batch, zero geometry */
+    if (!n_items || !block_size || !block_count)
+        return 1;
+    size_t flat = 0, row = 0;
+    for (size_t i = 0; i < n_items; ++i) {
+        /* :151-160: the item's rows and its table */
+        if (!token_count[i] || !table_len[i] || flat > UINT32_MAX
+            || table_len[i] > UINT32_MAX - flat)
+            return 1;
+        const uint32_t* table = tables + table_start[i];
+        const uint32_t offset = (uint32_t)flat;
+        /* :162-169: append the table, every entry < block_count */
+        for (size_t b = 0; b < table_len[i]; ++b) {
+            if (table[b] >= block_count)
+                return 1;
+            flat_table[flat++] = table[b];
+        }
+        /* :171-192: one slot, offset and length per row */
+        for (size_t t = 0; t < token_count[i]; ++t, ++row) {
+            const uint32_t position = positions[row];
+            if (position >= max_positions)
+                return 1;
+            const size_t logical = position / block_size;
+            if (logical >= table_len[i])
+                return 1;
+            const size_t slot = (size_t)table[logical] * block_size + position % block_size;
+            if (slot > UINT32_MAX)
+                return 1;
+            slots[row] = (uint32_t)slot;
+            offsets[row] = offset;
+            lengths[row] = table_len[i];
+        }
+    }
+    return 0;
+}
+
+int orc_decode_step_host(orc_block_manager* bm, size_t n, uint32_t* lengths,
+                         uint32_t* scratch_tables, size_t* scratch_start, uint32_t* scratch_len,
+                         uint32_t* token_count, uint32_t* flat_table, uint32_t* slots,
+                         uint32_t* offsets, uint32_t* row_lengths, size_t block_count,
+                         size_t block_size)
+{
+    size_t at = 0;
+    for (size_t s = 0; s < n; ++s) {
+        if (orc_bm_reserve(bm, s, (size_t)lengths[s] + 1))
+            return 1;
+        scratch_start[s] = at;
+        scratch_len[s] = (uint32_t)orc_bm_table(bm, s, scratch_tables + at, (size_t)-1);
+        at += scratch_len[s];
+        token_count[s] = 1;
+    }
+    /* the new token of sequence s sits at position lengths[s] */
+    if (orc_prepare_paged_batch(n, token_count, scratch_tables, scratch_start, scratch_len,
+                                lengths, (size_t)UINT32_MAX, block_count, block_size, flat_table,
+                                slots, offsets, row_lengths))
+        return 1;
+    for (size_t s = 0; s < n; ++s)
+        lengths[s] += 1;
+    return 0;
+}
+
 size_t orc_bm_table(const orc_block_manager* bm, size_t seq, uint32_t* out, size_t cap)
 {
     const size_t n = bm->lengths[seq];

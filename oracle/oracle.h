@@ -79,6 +79,34 @@ size_t orc_bm_table(const orc_block_manager* bm, size_t seq, uint32_t* out, size
 int orc_slot(const uint32_t* table, size_t table_length, uint32_t position, uint32_t block_size,
              uint32_t* slot);
 
+/* ---- prepare_paged_batch (src/model_batch.cc:127-204) ------------------ */
+/* Items are runs of token rows: item i has token_count[i] rows starting at
+ * row sum(token_count[0..i)), and its block table is
+ * tables[table_start[i] .. table_start[i] + table_len[i]). For every row:
+ * slot = table[pos / bs] * bs + pos % bs, table offset = the item's start in
+ * the flat table, table length = the item's table length; the flat table is
+ * the items' tables concatenated. Returns 0, or 1 (inconsistent_batch) for the
+ * reference's checks: no items or rows, block_size or block_count 0, an item
+ * with no tokens or an empty table, a table entry >= block_count, a position
+ * >= max_positions or past its table, or a slot beyond u32. flat_table needs
+ * sum(table_len) entries; slots, offsets and lengths one per row. */
+int orc_prepare_paged_batch(size_t n_items, const uint32_t* token_count,
+                            const uint32_t* tables, const size_t* table_start,
+                            const uint32_t* table_len, const uint32_t* positions,
+                            size_t max_positions, size_t block_count, size_t block_size,
+                            uint32_t* flat_table, uint32_t* slots, uint32_t* offsets,
+                            uint32_t* lengths);
+/* One decode step's host work for n sequences (ids 0..n-1) that each append
+ * one token: block_manager reserve(seq, lengths[seq] + 1), then
+ * prepare_paged_batch over one row per sequence at position lengths[seq];
+ * lengths[] is advanced by one. scratch_tables needs the sum of the table
+ * lengths after the step. Returns 0, 1 (capacity exhausted or inconsistent). */
+int orc_decode_step_host(orc_block_manager* bm, size_t n, uint32_t* lengths,
+                         uint32_t* scratch_tables, size_t* scratch_start, uint32_t* scratch_len,
+                         uint32_t* token_count, uint32_t* flat_table, uint32_t* slots,
+                         uint32_t* offsets, uint32_t* row_lengths, size_t block_count,
+                         size_t block_size);
+
 /* ---- Cache addressing (src/metal/metal_kv_cache.cc:150-179) ------------- */
 /* Layout [layer, block, token_in_block, kv_head, feature]. Returns 0, or the
  * kv_cache_errc value (7 layer, 8 block, 9 token, 10 head, 11 feature). */

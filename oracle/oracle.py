@@ -78,6 +78,12 @@ def lib() -> C.CDLL:
         L.orc_bm_table.restype = _size_t
         L.orc_bm_table.argtypes = [_vp, _size_t, _u32p, _size_t]
         L.orc_slot.argtypes = [_u32p, _size_t, C.c_uint32, C.c_uint32, _u32p]
+        _szp = C.POINTER(_size_t)
+        L.orc_prepare_paged_batch.argtypes = [_size_t, _u32p, _u32p, _szp, _u32p, _u32p,
+                                              _size_t, _size_t, _size_t, _u32p, _u32p, _u32p,
+                                              _u32p]
+        L.orc_decode_step_host.argtypes = [_vp, _size_t, _u32p, _u32p, _szp, _u32p, _u32p,
+                                           _u32p, _u32p, _u32p, _u32p, _size_t, _size_t]
         L.orc_element_offset.argtypes = [C.POINTER(Geometry), _size_t, _size_t, _size_t,
                                          _size_t, _size_t, C.POINTER(_size_t)]
         L.orc_store_kv.argtypes = [_vp, _vp, _vp, _vp, _u32p, _size_t, _size_t, _size_t,
@@ -204,6 +210,60 @@ def slot(table, position: int, block_size: int) -> int | None:
     if lib().orc_slot(_p32(t), t.size, position, block_size, C.byref(out)):
         return None
     return out.value
+
+
+def prepare_paged_batch(token_counts, tables, positions, max_positions: int,
+                        block_count: int, block_size: int):
+    """src/model_batch.cc:127-204: (flat table, slots, offsets, lengths), or None
+    for inconsistent_batch. tables: one block table per item."""
+    counts = _u32(token_counts)
+    lens = _u32([len(t) for t in tables])
+    flat_in = _u32(np.concatenate([np.asarray(t, np.uint32) for t in tables])
+                   if len(tables) and lens.sum() else [])
+    starts = np.ascontiguousarray(np.cumsum([0] + [len(t) for t in tables[:-1]]),
+                                  dtype=np.uintp) if len(tables) else np.zeros(0, np.uintp)
+    pos = _u32(positions)
+    rows = int(counts.sum()) if counts.size else 0
+    flat = np.zeros(max(int(lens.sum()), 1), np.uint32)
+    slots, offsets, lengths = (np.zeros(max(rows, 1), np.uint32) for _ in range(3))
+    status = lib().orc_prepare_paged_batch(
+        counts.size, _p32(counts), _p32(flat_in), starts.ctypes.data_as(C.POINTER(_size_t)),
+        _p32(lens), _p32(pos), max_positions, block_count, block_size, _p32(flat),
+        _p32(slots), _p32(offsets), _p32(lengths))
+    if status:
+        return None
+    return flat[:int(lens.sum())], slots[:rows], offsets[:rows], lengths[:rows]
+
+
+class DecodeStepHost:
+    """One decode step's host work for n sequences (orc_decode_step_host): the
+    block_manager reservation of one more token per sequence, then
+    prepare_paged_batch over one row per sequence. Buffers sized for
+    max_pages pages per sequence."""
+
+    def __init__(self, lengths, block_count: int, block_size: int, max_pages: int):
+        n = len(lengths)
+        self.bm = BlockManager(block_count, block_size, n)
+        self.n, self.block_count, self.block_size = n, block_count, block_size
+        self.lengths = _u32(lengths).copy()
+        for s in range(n):  # the sequences' current tokens
+            if self.bm.reserve(s, int(self.lengths[s])):
+                raise ValueError("pool too small")
+        cap = n * max_pages
+        self.tables = np.zeros(cap, np.uint32)
+        self.start = np.zeros(n, np.uintp)
+        self.table_len, self.counts = np.zeros(n, np.uint32), np.zeros(n, np.uint32)
+        self.flat = np.zeros(cap, np.uint32)
+        self.slots, self.offsets, self.row_lengths = (np.zeros(n, np.uint32) for _ in range(3))
+
+    def step(self) -> None:
+        status = lib().orc_decode_step_host(
+            self.bm._h, self.n, _p32(self.lengths), _p32(self.tables),
+            self.start.ctypes.data_as(C.POINTER(_size_t)), _p32(self.table_len),
+            _p32(self.counts), _p32(self.flat), _p32(self.slots), _p32(self.offsets),
+            _p32(self.row_lengths), self.block_count, self.block_size)
+        if status:
+            raise RuntimeError("decode step host work failed")
 
 
 def element_offset(geom: tuple, layer, block, token, head, feature):

@@ -197,6 +197,64 @@ def test_slots_cover_each_page_once_in_logical_order():
 
 # ---- cache addressing ---------------------------------------------------------------
 
+def test_prepare_paged_batch_rows_follow_the_closed_form():
+    """src/model_batch.cc:127-204 restated: per row, slot = table[p / bs] * bs +
+    p % bs (brute force over every position of a fragmented table), the item's
+    offset in the flat table and its table length; the flat table is the
+    items' tables concatenated."""
+    rng = np.random.default_rng(4)
+    for block_size in (1, 2, 16):
+        tables = [rng.permutation(64)[:n].astype(np.uint32) for n in (3, 1, 7)]
+        counts = [3 * block_size, block_size, 7 * block_size]
+        positions = np.concatenate([np.arange(c) for c in counts]).astype(np.uint32)
+        got = orc.prepare_paged_batch(counts, tables, positions, 10**6, 64, block_size)
+        assert got is not None
+        flat, slots, offsets, lengths = got
+        assert flat.tolist() == np.concatenate(tables).tolist()
+        row = 0
+        for i, (t, c) in enumerate(zip(tables, counts)):
+            for p in range(c):
+                assert slots[row] == int(t[p // block_size]) * block_size + p % block_size
+                assert offsets[row] == sum(len(x) for x in tables[:i])
+                assert lengths[row] == len(t)
+                row += 1
+
+
+def test_prepare_paged_batch_rejects_inconsistent_batches():
+    """The checks of src/model_batch.cc:132-192, each on its own."""
+    ok = dict(token_counts=[2], tables=[[3, 4]], positions=[16, 17], max_positions=64,
+              block_count=8, block_size=16)
+    assert orc.prepare_paged_batch(**ok) is not None
+    for change in (dict(token_counts=[]), dict(block_size=0), dict(block_count=0),
+                   dict(token_counts=[0], positions=[]), dict(tables=[[]]),
+                   dict(tables=[[3, 8]]),            # entry >= block_count
+                   dict(positions=[16, 64]),         # position >= max_positions
+                   dict(positions=[16, 32])):        # logical block past the table
+        args = dict(ok)
+        args.update(change)
+        if change.get("token_counts") == []:
+            args["tables"], args["positions"] = [], []
+        assert orc.prepare_paged_batch(**args) is None, change
+
+
+def test_decode_step_host_matches_block_manager_and_slots():
+    """One decode step's host work equals block_manager reserve(len + 1) per
+    sequence (FIFO pages) followed by the slot closed form at position len."""
+    lengths = [1, 15, 16, 17, 40, 300]
+    step = orc.DecodeStepHost(lengths, 200, 16, 32)
+    step.step()
+    bm = orc.BlockManager(200, 16, len(lengths))
+    for s, n in enumerate(lengths):
+        assert bm.reserve(s, n) is None
+    for s, n in enumerate(lengths):
+        assert bm.reserve(s, n + 1) is None
+    tables = [bm.table(s) for s in range(len(lengths))]
+    assert step.flat[:sum(len(t) for t in tables)].tolist() == np.concatenate(tables).tolist()
+    assert step.slots.tolist() == [orc.slot(t, n, 16) for t, n in zip(tables, lengths)]
+    assert step.row_lengths.tolist() == [len(t) for t in tables]
+    assert step.lengths.tolist() == [n + 1 for n in lengths]
+
+
 def test_element_offsets_follow_layout_order():
     # tests/metal_kv_cache_test.cc:82-101, geometry (L2, B3, bs4, H2, D8)
     g = (2, 3, 4, 2, 8)

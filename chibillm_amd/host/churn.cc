@@ -9,14 +9,27 @@
 //
 // Prints one JSON line: steps/s, tokens/s (prefill + decode rows), and the
 // algorithmic HBM bytes of the path per second against the 8 TB/s peak.
+//
+// --check <dir> checks the trace as it runs and stops at the first failure
+// (exit status 3): every --check-every steps, the page accounting (each live
+// sequence's pages are held once, reference counts sum to the pages in tables,
+// free + used = pool) and the K/V of sampled sequences, packed back from the
+// pool for all layers, against the rows the trace appended for them; and at
+// the first decode step after --dump-after, the last layer's K/V, queries and
+// outputs of up to eight rows are written to <dir> for a CPU check of the
+// attention (decode_rows.json and raw bf16 .bin files).
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <deque>
+#include <fstream>
 #include <random>
 #include <string>
+#include <unordered_map>
+#include <unordered_set>
 
 #include "hip_model_state.h"
 #include "inference_engine.h"
@@ -39,7 +52,16 @@ struct options {
     bool profile = false;
     bool device_tables = false; // sequence tables kept on the device (device_tables)
     bool host_timing = false;   // drain the GPU before each step's metadata work and time it
+    std::string check_dir;      // --check: verify the trace and dump one decode step here
+    std::size_t check_every = 250;
+    std::size_t dump_after = 1000;
 };
+
+// Sequences whose K/V the check follows: every 50th id.
+bool sampled(seq_id id)
+{
+    return id % 50 == 7;
+}
 
 // Seeded draws: std::mt19937_64 (fully specified) with explicit transforms.
 struct draws {
@@ -197,11 +219,201 @@ public:
             }
         }
         account(batch, h2d);
+        if (checking_) {
+            auto recorded = record(batch);
+            if (recorded && dump_wanted_ && decode) {
+                recorded = dump(batch);
+                dump_wanted_ = false;
+                dumped_ = recorded.has_value();
+            }
+            if (!recorded) {
+                check_error_ = recorded.error();
+                return fail(model_runner_errc::backend_failure, "check: " + check_error_);
+            }
+        }
         return std::vector<token_id>(batch.sample_count(), 7);
     }
 
     const totals& stats() const noexcept { return totals_; }
     hip_model_state* state() const noexcept { return state_; }
+
+    // ---- --check ------------------------------------------------------------
+    // Host copies of the row buffers (the same seeded draws as allocate()).
+    void keep_host_rows()
+    {
+        const std::size_t rows = opt_.max_batch_tokens;
+        const std::size_t F = opt_.kv_heads * opt_.head_dim, QF = opt_.q_heads * opt_.head_dim;
+        k_host_ = random_bf16(rows * F, 11);
+        v_host_ = random_bf16(rows * F, 12);
+        q_host_ = random_bf16(rows * QF, 13);
+        checking_ = true;
+    }
+    void forget(seq_id id) { appended_.erase(id); }
+    void request_dump() { dump_wanted_ = true; }
+    bool dumped() const noexcept { return dumped_; }
+    std::size_t kv_tokens_checked() const noexcept { return kv_tokens_checked_; }
+
+    // Page accounting over the live sequences: no page in two tables or twice
+    // in one, each table page held exactly once (no prefix sharing in this
+    // trace), the reference counts summing to the pages in tables, and free +
+    // used = the pool.
+    result<void, std::string> check_pages(const std::unordered_set<seq_id>& live) const
+    {
+        const block_manager& pages = state_->pages();
+        std::vector<std::uint8_t> seen(pages.block_count(), 0);
+        std::size_t in_tables = 0;
+        for (const seq_id id : live) {
+            for (const block_id b : pages.resources(id).blocks) {
+                if (b >= pages.block_count() || seen[b])
+                    return fail("page " + std::to_string(b) + " held twice (sequence "
+                                + std::to_string(id) + ")");
+                seen[b] = 1;
+                if (pages.refcount(b) != 1)
+                    return fail("page " + std::to_string(b) + " has "
+                                + std::to_string(pages.refcount(b)) + " references");
+                ++in_tables;
+            }
+        }
+        std::uint64_t refs = 0;
+        for (std::size_t b = 0; b < pages.block_count(); ++b)
+            refs += pages.refcount(static_cast<block_id>(b));
+        if (refs != in_tables)
+            return fail("reference counts sum to " + std::to_string(refs) + ", tables hold "
+                        + std::to_string(in_tables));
+        if (pages.free_block_count() + in_tables != pages.block_count())
+            return fail("free " + std::to_string(pages.free_block_count()) + " + used "
+                        + std::to_string(in_tables) + " != pool "
+                        + std::to_string(pages.block_count()));
+        return {};
+    }
+
+    // Every appended token of up to `limit` followed sequences, all layers,
+    // packed back from their pages and compared bit for bit with the row the
+    // trace appended at that position.
+    result<void, std::string> check_kv(std::size_t limit)
+    {
+        const std::size_t F = opt_.kv_heads * opt_.head_dim;
+        std::vector<seq_id> ids;
+        for (const auto& [id, rows] : appended_)
+            if (!rows.empty())
+                ids.push_back(id);
+        std::sort(ids.begin(), ids.end());
+        // `limit` of them per check, rotating through the followed sequences
+        const std::size_t count = std::min(limit, ids.size());
+        for (std::size_t i = 0; i < count; ++i) {
+            const seq_id id = ids[(check_round_ * limit + i) % ids.size()];
+            const auto& rows = appended_.at(id);
+            const std::size_t n = rows.size();
+            std::vector<std::uint16_t> pk, pv;
+            if (auto packed = pack(id, n, pk, pv); !packed)
+                return packed;
+            for (std::size_t layer = 0; layer < opt_.layers; ++layer)
+                for (std::size_t t = 0; t < n; ++t) {
+                    const std::size_t at = (layer * n + t) * F;
+                    const std::size_t src = static_cast<std::size_t>(rows[t]) * F;
+                    if (std::memcmp(&pk[at], &k_host_[src], F * 2) != 0
+                        || std::memcmp(&pv[at], &v_host_[src], F * 2) != 0)
+                        return fail("sequence " + std::to_string(id) + " layer "
+                                    + std::to_string(layer) + " token " + std::to_string(t)
+                                    + " differs from the row appended");
+                }
+            kv_tokens_checked_ += n * opt_.layers;
+        }
+        ++check_round_;
+        return {};
+    }
+
+private:
+    // The sequence's first n tokens of every layer, [layer][token][feature].
+    result<void, std::string> pack(seq_id id, std::size_t n, std::vector<std::uint16_t>& k,
+                                   std::vector<std::uint16_t>& v) const
+    {
+        const std::size_t F = opt_.kv_heads * opt_.head_dim;
+        const std::size_t bytes = opt_.layers * n * F * 2;
+        auto dk = device_buffer::make(ctx_, bytes);
+        auto dv = device_buffer::make(ctx_, bytes);
+        if (!dk || !dv)
+            return fail(std::string("check buffers"));
+        const auto blocks = state_->pages().resources(id).blocks;
+        const int rc = ckv_checkpoint_pack(state_->cache().pool(), blocks.data(), blocks.size(), n,
+                                           dk->data(), dv->data());
+        if (rc)
+            return fail(std::string("pack: ") + ckv_error_name(rc));
+        k.resize(bytes / 2);
+        v.resize(bytes / 2);
+        if (!dk->download(k.data(), bytes) || !dv->download(v.data(), bytes))
+            return fail(std::string("check download"));
+        return {};
+    }
+
+    // Rows of the batch that append a followed sequence's tokens: position ->
+    // row of the K/V buffers. A position appended again (a sequence computed
+    // anew after losing its pages) replaces what followed it.
+    result<void, std::string> record(const model_batch& batch)
+    {
+        for (const auto& item : batch.items) {
+            if (!sampled(item.id))
+                continue;
+            auto& rows = appended_[item.id];
+            for (std::size_t t = 0; t < item.token_count; ++t) {
+                const std::size_t r = item.token_offset + t;
+                const std::size_t position = batch.positions[r];
+                if (position > rows.size())
+                    return fail("sequence " + std::to_string(item.id) + " appends position "
+                                + std::to_string(position) + " after "
+                                + std::to_string(rows.size()) + " tokens");
+                rows.resize(position);
+                rows.push_back(static_cast<std::uint32_t>(r));
+            }
+        }
+        return {};
+    }
+
+    // The last layer's K/V, queries and outputs of up to eight rows of this
+    // decode batch, for a CPU check of the attention.
+    result<void, std::string> dump(const model_batch& batch)
+    {
+        const std::size_t F = opt_.kv_heads * opt_.head_dim, QF = opt_.q_heads * opt_.head_dim;
+        const std::size_t rows = batch.tokens.size();
+        const std::size_t n_dump = std::min<std::size_t>(rows, 8);
+        std::vector<std::uint16_t> out(rows * QF);
+        if (!o_.download(out.data(), rows * QF * 2))
+            return fail(std::string("output download"));
+        const std::string dir = opt_.check_dir + "/";
+        auto write = [&](const std::string& name, const std::uint16_t* p, std::size_t n) {
+            std::ofstream f(dir + name, std::ios::binary);
+            f.write(reinterpret_cast<const char*>(p), static_cast<std::streamsize>(n * 2));
+            return static_cast<bool>(f);
+        };
+        std::string json = "{\"layer\": " + std::to_string(opt_.layers - 1)
+            + ", \"kv_heads\": " + std::to_string(opt_.kv_heads)
+            + ", \"q_heads\": " + std::to_string(opt_.q_heads)
+            + ", \"head_dim\": " + std::to_string(opt_.head_dim) + ", \"rows\": [";
+        std::vector<std::uint16_t> q, o;
+        for (std::size_t i = 0; i < n_dump; ++i) {
+            // spread over the batch: rows 0, rows/8, 2 rows/8, ...
+            const std::size_t r = i * rows / n_dump;
+            const auto& item = batch.items[r];
+            const std::size_t n = batch.positions[r] + 1;
+            std::vector<std::uint16_t> pk, pv;
+            if (auto packed = pack(item.id, n, pk, pv); !packed)
+                return packed;
+            const std::size_t last = (opt_.layers - 1) * n * F;
+            if (!write("k_" + std::to_string(i) + ".bin", &pk[last], n * F)
+                || !write("v_" + std::to_string(i) + ".bin", &pv[last], n * F))
+                return fail(std::string("dump write"));
+            q.insert(q.end(), q_host_.begin() + r * QF, q_host_.begin() + (r + 1) * QF);
+            o.insert(o.end(), out.begin() + r * QF, out.begin() + (r + 1) * QF);
+            json += (i ? ", " : "") + std::string("{\"seq\": ") + std::to_string(item.id)
+                + ", \"position\": " + std::to_string(n - 1) + ", \"row\": " + std::to_string(r)
+                + "}";
+        }
+        json += "]}\n";
+        if (!write("q.bin", q.data(), q.size()) || !write("out.bin", o.data(), o.size()))
+            return fail(std::string("dump write"));
+        std::ofstream(dir + "decode_rows.json") << json;
+        return {};
+    }
 
 private:
     // Algorithmic bytes of one step, all layers: K+V of every attended token
@@ -245,6 +457,15 @@ private:
     device_buffer k_, v_, q_, o_;
     std::vector<std::uint32_t> positions_;
     totals totals_;
+    // --check
+    bool checking_ = false, dump_wanted_ = false, dumped_ = false;
+    std::vector<std::uint16_t> k_host_, v_host_, q_host_;
+    std::unordered_map<seq_id, std::vector<std::uint32_t>> appended_;
+    std::size_t check_round_ = 0, kv_tokens_checked_ = 0;
+    std::string check_error_;
+
+public:
+    const std::string& check_error() const noexcept { return check_error_; }
 };
 
 bool
@@ -268,7 +489,13 @@ parse(int argc, char** argv, options& o)
         }
         if (!(v = next()))
             return false;
-        if (a == "--steps")
+        if (a == "--check")
+            o.check_dir = v;
+        else if (a == "--check-every")
+            o.check_every = std::strtoull(v, nullptr, 10);
+        else if (a == "--dump-after")
+            o.dump_after = std::strtoull(v, nullptr, 10);
+        else if (a == "--steps")
             o.steps = std::strtoull(v, nullptr, 10);
         else if (a == "--seed")
             o.seed = std::strtoull(v, nullptr, 10);
@@ -303,7 +530,7 @@ main(int argc, char** argv)
                      "usage: churn [--steps N] [--seed S] [--pool-gb G] [--max-live N] "
                      "[--arrival-mean M] [--layers L] [--max-batch-tokens T] "
                      "[--prefill-chunk C] [--sigma S] [--profile] [--device-tables] "
-                     "[--host-timing]\n");
+                     "[--host-timing] [--check DIR [--check-every N] [--dump-after STEP]]\n");
         return 2;
     }
     auto ctx = hip_context::make(0);
@@ -330,6 +557,26 @@ main(int argc, char** argv)
         std::fprintf(stderr, "allocation failed: %s\n", a.error().c_str());
         return 1;
     }
+    const bool check = !opt.check_dir.empty();
+    if (check)
+        runner.keep_host_rows();
+    std::unordered_set<seq_id> live;
+    std::size_t checks = 0;
+    // the trace's checks; a failure ends the run with status 3
+    auto run_checks = [&](std::size_t step) -> bool {
+        auto pages = runner.check_pages(live);
+        if (pages)
+            pages = runner.check_kv(4);
+        if (!pages) {
+            std::fprintf(stderr, "[churn] check failed at step %zu: %s\n", step,
+                         pages.error().c_str());
+            return false;
+        }
+        ++checks;
+        std::fprintf(stderr, "[churn] step %zu: checks passed (%zu live, %zu K/V tokens so far)\n",
+                     step, live.size(), runner.kv_tokens_checked());
+        return true;
+    };
     if (opt.profile)
         ckv_profile_enable(ctx->get(), 1);
     std::fprintf(stderr, "[churn] pool %zu pages (%.1f GB), %zu layers, live cap %zu, %zu steps\n",
@@ -362,6 +609,7 @@ main(int argc, char** argv)
             ++arrived;
         }
         while (!pending.empty()) {
+            const seq_id id = pending.front().id(); // try_add may move the sequence
             auto r = engine->try_add(pending.front());
             if (!r) {
                 std::fprintf(stderr, "admission: %s\n", describe_error(r.error()).c_str());
@@ -369,20 +617,24 @@ main(int argc, char** argv)
             }
             if (*r == admission_result::deferred)
                 break;
-            if (*r == admission_result::too_large)
+            if (*r == admission_result::too_large) {
                 ++rejected;
-            else
+            } else {
                 ++admitted;
+                live.insert(id);
+            }
             pending.pop_front();
         }
         const auto& sched = engine->engine_scheduler();
         peak_live = std::max(peak_live, sched.running_count() + sched.waiting_count());
         if (sched.running_count() + sched.waiting_count() == 0)
             continue;
+        if (check && step >= opt.dump_after && !runner.dumped())
+            runner.request_dump();
         auto updates = engine->step();
         if (!updates) {
             std::fprintf(stderr, "step %zu: %s\n", step, describe_error(updates.error()).c_str());
-            return 1;
+            return runner.check_error().empty() ? 1 : 3;
         }
         for (const auto& u : *updates)
             if (u.reason != finish_reason::none) {
@@ -390,8 +642,12 @@ main(int argc, char** argv)
                     std::fprintf(stderr, "remove: %s\n", describe_error(removed.error()).c_str());
                     return 1;
                 }
+                live.erase(u.id);
+                runner.forget(u.id);
                 ++finished;
             }
+        if (check && (step + 1) % opt.check_every == 0 && !run_checks(step))
+            return 3;
         const auto now = std::chrono::steady_clock::now();
         if (now - last_report > std::chrono::seconds(10)) {
             last_report = now;
@@ -403,6 +659,8 @@ main(int argc, char** argv)
         std::fprintf(stderr, "sync: %s\n", describe_error(synced.error()).c_str());
         return 1;
     }
+    if (check && !run_checks(opt.steps))
+        return 3;
     const double seconds =
         std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     const auto& t = runner.stats();
@@ -423,6 +681,9 @@ main(int argc, char** argv)
                 finished, rejected, pending.size(), peak_live, config.kv_block_count,
                 opt.device_tables ? "true" : "false",
                 t.h2d_bytes / std::max<std::size_t>(1, t.prefill_steps + t.decode_steps));
+    if (check)
+        std::printf(", \"check\": {\"checks\": %zu, \"kv_tokens_checked\": %zu, \"dumped\": %s}",
+                    checks, runner.kv_tokens_checked(), runner.dumped() ? "true" : "false");
     if (opt.host_timing)
         std::printf(", \"metadata_host_us_per_step\": %.2f",
                     1e6 * t.metadata_host_s / std::max<std::size_t>(1, t.timed_steps));

@@ -49,3 +49,53 @@ def test_churn_driver_runs_a_short_trace():
     assert trace["finished"] > 0 and trace["rejected"] == 0
     assert trace["peak_live"] <= 64
     assert trace["prefill_tokens"] + trace["decode_tokens"] > 0
+
+
+@pytest.mark.gpu
+def test_churn_full_size_checked_trace(tmp_path):
+    """BASELINE config 5 at its real size (160 GB pool, 28 layers, live batch
+    512), a bounded 800-step trace under --check: every 200 steps the page
+    accounting holds (each live sequence's pages held once, reference counts
+    summing to the pages in tables, free + used = pool) and sampled sequences'
+    K/V, packed back from every layer, equal the rows the trace appended for
+    them (the driver stops at the first failure with status 3). One decode
+    step's last-layer rows are dumped and checked here against the oracle,
+    within 2e-2 abs + 1e-2 rel."""
+    import json
+    import math
+
+    import numpy as np
+
+    from oracle import oracle as orc
+    from tests.gpu_util import assert_close
+    from tests.test_gpu_parity import compact_oracle
+
+    path = os.path.join(BIN, "churn")
+    if not os.path.exists(path):
+        pytest.fail(f"{path} is not built: run __graft_entry__.build()")
+    print("churn --check: 800 steps, 160 GB, 28 layers", flush=True)
+    proc = subprocess.run([path, "--steps", "800", "--check", str(tmp_path), "--check-every",
+                           "200", "--dump-after", "500"], capture_output=True, text=True,
+                          timeout=240)
+    print(proc.stderr[-3000:])
+    assert proc.returncode == 0, proc.stderr[-3000:]
+    trace = json.loads(proc.stdout.strip().splitlines()[-1])
+    assert trace["pool_pages"] == 87193
+    assert trace["check"]["checks"] == 5 and trace["check"]["dumped"]
+    assert trace["check"]["kv_tokens_checked"] > 0
+    assert trace["decode_steps"] > 0 and trace["finished"] > 0 and trace["rejected"] == 0
+
+    meta = json.loads((tmp_path / "decode_rows.json").read_text())
+    H, D, HQ = meta["kv_heads"], meta["head_dim"], meta["q_heads"]
+    rows = meta["rows"]
+    q = np.fromfile(tmp_path / "q.bin", np.uint16).reshape(len(rows), HQ * D)
+    out = np.fromfile(tmp_path / "out.bin", np.uint16).reshape(len(rows), HQ * D)
+    lengths = [r["position"] + 1 for r in rows]
+    ks = [np.fromfile(tmp_path / f"k_{i}.bin", np.uint16).reshape(n, H * D)
+          for i, n in enumerate(lengths)]
+    vs = [np.fromfile(tmp_path / f"v_{i}.bin", np.uint16).reshape(n, H * D)
+          for i, n in enumerate(lengths)]
+    tables = [np.zeros(math.ceil(n / 16), np.uint32) for n in lengths]
+    expected = compact_oracle((H, D), lengths, tables, ks, vs, q, HQ)
+    assert_close(orc.to_f32(out, orc.BF16), expected,
+                 what=f"decode rows of sequences {[r['seq'] for r in rows]}")

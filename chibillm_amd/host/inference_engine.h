@@ -70,16 +70,28 @@ public:
     [[nodiscard]] result<void, inference_engine_error> cancel(seq_id id);
     [[nodiscard]] result<void, inference_engine_error> remove(seq_id id);
 
+    // Host time spent in each stage of the steps so far (no reference
+    // counterpart): scheduling, building the model batch, the runner's
+    // execute (which includes enqueueing the device work), and completion.
+    struct stage_times {
+        std::uint64_t steps = 0;
+        double schedule_s = 0, build_s = 0, execute_s = 0, complete_s = 0;
+    };
+    [[nodiscard]] const stage_times& times() const noexcept { return times_; }
+
 private:
     inference_engine(scheduler s, model_runner& runner) noexcept
         : scheduler_(std::move(s))
         , runner_(&runner)
     {}
-    failure<inference_engine_error> fail_after_abort(const scheduled_batch& batch,
-                                                     inference_engine_error e);
+    result<std::vector<sequence_update>, inference_engine_error>
+    run(const scheduled_batch& scheduled);
+    failure<inference_engine_error> abandon(const scheduled_batch& batch,
+                                            inference_engine_error cause);
 
     scheduler scheduler_;
     model_runner* runner_;
+    stage_times times_;
 };
 
 } // namespace chibillm

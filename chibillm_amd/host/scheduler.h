@@ -11,7 +11,6 @@
 #include <optional>
 #include <span>
 #include <unordered_map>
-#include <variant>
 #include <vector>
 
 #include "block_manager.h"
@@ -118,7 +117,7 @@ public:
     scheduler& operator=(scheduler&&) noexcept = default;
 
     [[nodiscard]] const scheduler_config& config() const noexcept { return config_; }
-    [[nodiscard]] std::size_t sequence_count() const noexcept { return sequences_.size(); }
+    [[nodiscard]] std::size_t sequence_count() const noexcept { return members_.size(); }
     [[nodiscard]] std::size_t waiting_count() const noexcept { return waiting_.size(); }
     [[nodiscard]] std::size_t running_count() const noexcept { return running_.size(); }
     [[nodiscard]] bool has_in_flight_batch() const noexcept { return active_.has_value(); }
@@ -149,29 +148,46 @@ public:
     [[nodiscard]] result<void, scheduler_error> remove(seq_id id);
 
 private:
-    scheduler(scheduler_config config, token_id eos, std::unique_ptr<model_state> state);
-    seq* mutable_sequence(seq_id id) noexcept;
-    result<void, scheduler_error> select(scheduled_batch& batch, std::deque<seq_id>& queue,
-                                         std::size_t item_limit);
-    void rollback_reservations(const scheduled_batch& batch) noexcept;
-    bool cacheable_prefix(std::size_t count) const noexcept;
-    void cache_prefix(const seq& sequence) noexcept;
-    void check_invariants() const noexcept;
-
-    struct prefill_turn {};
-    // the unvisited members of a decode round are the first `remaining` of running_
-    struct decode_round {
-        std::size_t remaining;
+    // A sequence the scheduler holds (live or finished) and the pages it was
+    // admitted against; they are committed while it is waiting or running.
+    struct member {
+        seq sequence;
+        std::size_t budget;
     };
+    // One item of a batch before any reservation: how many tokens, and
+    // whether they end the sequence's unprocessed tokens (it then samples).
+    struct planned {
+        seq_id id;
+        std::size_t tokens;
+        bool samples;
+    };
+
+    scheduler(scheduler_config config, token_id eos, std::unique_ptr<model_state> state);
+    member* find_member(seq_id id) noexcept;
+    std::optional<std::size_t> page_budget(const seq& sequence) const noexcept;
+    result<void, scheduler_error> open_state(seq& sequence);
+    bool restore_checkpoint(seq_id id, const model_checkpoint& saved) noexcept;
+    result<std::vector<planned>, scheduler_error> plan(bool prefill, std::size_t limit) const;
+    std::size_t checkpoint_cut(const seq& sequence, std::size_t tokens) const noexcept;
+    result<void, scheduler_error> reserve(const std::vector<planned>& items, scheduled_batch& batch);
+    result<void, scheduler_error> settle(seq_id id, member& m, token_id sample, bool prefill);
+    void leave(seq_id id, member& m) noexcept;
+    void unschedule(const scheduled_batch& batch) noexcept;
+    bool worth_caching(std::size_t count) const noexcept;
+    void publish_prefix(const seq& sequence) noexcept;
+    void check_invariants() const noexcept;
 
     scheduler_config config_;
     token_id eos_;
     std::unique_ptr<model_state> state_;
     prefix_cache prefixes_; // declared after state_: destroyed first
-    std::variant<prefill_turn, decode_round> turn_ { prefill_turn {} };
-    std::unordered_map<seq_id, seq> sequences_;
+    std::unordered_map<seq_id, member> members_;
     std::deque<seq_id> waiting_;
     std::deque<seq_id> running_;
+    std::size_t committed_pages_ = 0; // the budgets of the waiting and running members
+    // running members still to serve in the current decode round (they are the
+    // first decode_left_ of running_); 0 outside a round, the prefill turn
+    std::size_t decode_left_ = 0;
     std::optional<scheduled_batch> active_;
     bool transaction_open_ = false;
     batch_id next_batch_ = 1;

@@ -19,12 +19,16 @@
 
 using namespace ckv;
 
-// Scratch of ckv_append_decode_noalloc: the partial records of the rows its
-// batch plan cuts into chunks. Every GPU the library runs on holds its own copy
-// of this array until the process ends. In host code `noalloc_scratch` is a
-// host-side stand-in, not a device address: kernels are given the address
-// hipGetSymbolAddress returns for the current device (ckv_context::noalloc_scratch).
+// Scratch of ckv_append_decode_noalloc: the arrival counters (the first
+// noalloc_counter_bytes; zero when the library loads, and every call leaves
+// them zero) and then the partial records of the rows its batch plan cuts into
+// chunks. Every GPU the library runs on holds its own copy of this array until
+// the process ends. In host code `noalloc_scratch` is a host-side stand-in, not
+// a device address: kernels are given the address hipGetSymbolAddress returns
+// for the current device (ckv_context::noalloc_scratch).
 constexpr size_t noalloc_scratch_bytes = (size_t)16 << 20;
+constexpr size_t noalloc_counter_bytes = (size_t)256 << 10;
+constexpr size_t noalloc_record_bytes = noalloc_scratch_bytes - noalloc_counter_bytes;
 static __device__ __align__(256) unsigned char noalloc_scratch[noalloc_scratch_bytes];
 
 namespace {
@@ -297,22 +301,45 @@ int ensure_plan(ckv_pool* pool)
 }
 
 // Scratch of the fast decode when its plan cuts rows into chunks: a partial
-// record for every (record, q head).
+// record for every (record, q head) and an arrival counter for every
+// (record, kv head). The counters have a buffer of their own (the generic
+// decode writes its partials over d_partials) and are zeroed by a fill
+// kernel whenever it is allocated; launches leave them zero.
 int ensure_split(ckv_pool* pool, size_t q_heads, split_scratch& split)
 {
     split = {};
     const meta_view& m = pool->meta;
     if (!m.n_cut)
         return CKV_OK;
+    ckv_context* ctx = pool->ctx;
     size_t capacity_floats = pool->d_partials_bytes / sizeof(float);
     const size_t floats = (size_t)m.n_records * q_heads
         * partial_record_floats((uint32_t)pool->head_dim);
-    const int status = ensure_device(pool->ctx, &pool->d_partials, &capacity_floats, floats,
-                                     "decode partials");
+    int status = ensure_device(ctx, &pool->d_partials, &capacity_floats, floats,
+                               "decode partials");
     pool->d_partials_bytes = capacity_floats * sizeof(float);
     if (status)
         return status;
+    const size_t counters = (size_t)m.n_records * pool->kv_heads;
+    if (counters > pool->d_arrivals_words) {
+        status = ensure_device(ctx, &pool->d_arrivals, &pool->d_arrivals_words, counters,
+                               "decode arrival counters");
+        if (status)
+            return status;
+        status = run_kernel(ctx, "fill", [&] {
+            return launch_fill(ctx->stream, pool->d_arrivals, 0,
+                               (uint32_t)pool->d_arrivals_words);
+        });
+        if (status) {
+            // not known to be zero: allocate and clear again next time
+            (void)hipFree(pool->d_arrivals);
+            pool->d_arrivals = nullptr;
+            pool->d_arrivals_words = 0;
+            return status;
+        }
+    }
     split.records = pool->d_partials;
+    split.arrivals = pool->d_arrivals;
     return CKV_OK;
 }
 
@@ -941,6 +968,8 @@ int ckv_pool_destroy(ckv_pool* pool)
         (void)hipFree(pool->d_meta);
     if (pool->d_partials)
         (void)hipFree(pool->d_partials);
+    if (pool->d_arrivals)
+        (void)hipFree(pool->d_arrivals);
     if (pool->d_pairs)
         (void)hipFree(pool->d_pairs);
     if (pool->d_seq)
@@ -1802,14 +1831,18 @@ int ckv_append_decode_noalloc(ckv_pool* pool, size_t layer, const void* keys, co
                           "decode plan was not uploaded with it");
     const meta_view& m = pool->meta;
     const uint64_t need = (uint64_t)m.n_records * q_heads * partial_record_floats(128) * sizeof(float);
-    if (need > noalloc_scratch_bytes)
+    const uint64_t counters = (uint64_t)m.n_records * pool->kv_heads * sizeof(uint32_t);
+    if (need > noalloc_record_bytes || counters > noalloc_counter_bytes)
         return fail_fixed(ctx, CKV_E_INVALID_ARGUMENT,
                           "no-allocation decode: the batch's partial records exceed the "
-                          "16 MiB scratch (fewer or shorter rows cut into chunks fit)");
+                          "scratch (16 MiB less 256 KiB of counters; fewer or shorter rows "
+                          "cut into chunks fit)");
     if (m.n_cut && !ctx->noalloc_scratch)
         return fail_fixed(ctx, CKV_E_HIP_FAILURE,
                           "no-allocation decode: the scratch array has no device address");
-    const split_scratch split { static_cast<float*>(ctx->noalloc_scratch) };
+    unsigned char* const scratch = static_cast<unsigned char*>(ctx->noalloc_scratch);
+    const split_scratch split { reinterpret_cast<float*>(scratch + noalloc_counter_bytes),
+                                reinterpret_cast<uint32_t*>(scratch) };
     const bool fused = pool->fusable && reinterpret_cast<uintptr_t>(keys) % 16 == 0
         && reinterpret_cast<uintptr_t>(values) % 16 == 0;
     hipError_t e = hipSuccess;

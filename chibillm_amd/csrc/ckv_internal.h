@@ -58,9 +58,13 @@ struct meta_view {
 
 // Device scratch of the fast decode's cut rows: a partial record
 // [max, denominator, 0, 0, acc[head_dim]] per (record, q head), written by the
-// chunks and read by the merge launch that follows them.
+// chunks, and an arrival counter per (record, kv head), of which a cut row
+// uses the one at (its first record, kv head). The counters must be zero
+// before a launch and every launch leaves them zero (the row's last chunk
+// resets its counter), so they are cleared once, when allocated.
 struct split_scratch {
     float* records;
+    uint32_t* arrivals;
 };
 
 // Largest query tile, in rows (positions): the prefill kernel covers a tile
@@ -205,6 +209,8 @@ struct ckv_pool {
     // device scratch
     float* d_partials = nullptr;
     size_t d_partials_bytes = 0;
+    uint32_t* d_arrivals = nullptr; // the fast decode's arrival counters (zero between launches)
+    size_t d_arrivals_words = 0;
     uint32_t* d_pairs = nullptr; // block-id pairs / patch pairs
     size_t d_pairs_words = 0;
     char* d_spill = nullptr; // staging of checkpoint export/import

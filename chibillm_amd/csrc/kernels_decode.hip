@@ -47,6 +47,27 @@ __device__ __forceinline__ float fast_exp2(float x)
     return __builtin_amdgcn_exp2f(x);
 }
 
+// Relaxed agent-scope accesses: coherent across the XCDs on their own (the
+// store writes through, the load misses any cache line that could be stale),
+// so data passed this way between workgroups needs no L2 writeback, only
+// the writer's wait for its stores to complete before it signals.
+__device__ __forceinline__ void agent_store(float* p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float agent_load(const float* p)
+{
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until every vector memory access this wave issued (stores included)
+// has completed; a compiler barrier too.
+__device__ __forceinline__ void wait_vector_memory()
+{
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 // f32 -> bf16 round to nearest even, NaN quieted (src/tensor/types.h:60-75).
 __device__ __forceinline__ uint32_t bf16_bits(float x)
 {
@@ -158,11 +179,12 @@ __host__ __device__ constexpr uint32_t record_floats(uint32_t head_dim)
 // normalised output of the group's q heads. GATED multiplies it by
 // sigmoid(gate) first; the gate values are loaded when the workgroup starts,
 // so their latency hides behind the page loads. A chunk of a cut row writes
-// its unnormalised state instead (a partial record per q head), which
-// merge_chunks_kernel combines after the launch. (Merging in the chunk that
-// finishes last needs an agent-scope release per workgroup, which on gfx950
-// writes back the XCD's L2: measured at about 1.9 us per workgroup per XCD,
-// far more than the second launch costs.) ROPE (with FUSED) rotates the
+// its unnormalised state instead (a partial record per q head) with
+// agent-scope stores and counts itself in; the chunk that arrives last merges
+// the row's records in the same launch. (An agent-scope release fence per
+// workgroup would write back the XCD's whole L2, measured at about 1.9 us per
+// workgroup per XCD; stores that are coherent on their own need only a wait
+// for completion before the count.) ROPE (with FUSED) rotates the
 // queries and the new token's key by the row's position first, as rope_f32
 // (src/metal/kernels/tensor_ops.metal:158-195) would: feature f < rotary/2
 // pairs with f + rotary/2, which sits in the lane part ^ (rotary/16) of the
@@ -453,7 +475,8 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
         }
         return;
     }
-    // a chunk of a cut row: record [max, denominator, 0, 0, acc[D]] per q head
+    // a chunk of a cut row: record [max, denominator, 0, 0, acc[D]] per q head,
+    // stored at agent scope (through to where every XCD reads it)
     constexpr uint32_t RF = D + 4;
     const uint64_t record_stride = (uint64_t)q_heads * RF; // between a row's chunks
     float* const records = split.records
@@ -463,88 +486,93 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
         float M, d, a;
         wg_state(g, f, M, d, a);
         float* rec = records + chunk * record_stride + g * RF;
-        rec[4 + f] = a;
+        agent_store(rec + 4 + f, a);
         if (f == 0) {
-            rec[0] = M;
-            rec[1] = d;
+            agent_store(rec, M);
+            agent_store(rec + 1, d);
         }
     }
-}
-
-// The rows the plan cut into chunks: one workgroup of 1024 threads per (cut
-// row, kv head). Thread (slice, g, f) folds chunks slice, slice + S, ... of q
-// head g (S = 8 / G slices) into a running (max, denominator, acc[f]) with
-// weights 2^(m_c - M), the reduction of paged_attention_reduce_f32
-// (src/metal/kernels/attention.metal:567-615) done online; the S slices are
-// then folded through LDS, and the result normalised, gated and rounded once,
-// as the single-chunk epilogue does. A row's records are read in parallel:
-// 128 consecutive floats per (chunk, q head), four chunks in flight per thread.
-template <int G, bool F16, bool GATED>
-__global__ __launch_bounds__(1024) void merge_chunks_kernel(
-    pool_view p, meta_view m, uint32_t q_heads, const float* __restrict__ records,
-    uint16_t* __restrict__ out, const uint16_t* __restrict__ gate)
-{
-    constexpr uint32_t D = 128;
-    constexpr uint32_t RF = D + 4;
-    constexpr uint32_t S = 8 / G; // chunk slices per q head
-    __shared__ float fold_acc[S][G][D];
-    __shared__ float fold_ml[S][G][2];
-    const uint32_t H = p.kv_heads;
-    const uint32_t row = m.cut[blockIdx.x / H];
-    const uint32_t kv_head = blockIdx.x % H;
-    const uint32_t n_pages = m.positions[row] / p.block_size + 1;
-    const uint32_t n_chunks = (n_pages + m.split_pages - 1) / m.split_pages;
-    const uint32_t f = threadIdx.x % D;
-    const uint32_t g = (threadIdx.x / D) % G;
-    const uint32_t slice = threadIdx.x / (D * G);
-    const uint64_t stride = (uint64_t)q_heads * RF;
-    const float* rec = records + ((uint64_t)m.split_first[row] * q_heads + kv_head * G + g) * RF;
-    const uint64_t at = ((uint64_t)row * q_heads + kv_head * G + g) * D + f;
-    uint16_t gb = 0;
-    if constexpr (GATED)
-        gb = gate[at];
-    float M = -INFINITY, d = 0.0f, a = 0.0f;
-    auto fold = [&](float mc, float dc, float ac) {
-        const float nm = fmaxf(M, mc);
-        const float keep = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
-        const float take = fast_exp2(mc - nm);
-        d = d * keep + dc * take;
-        a = a * keep + ac * take;
-        M = nm;
-    };
-    uint32_t c = slice;
-    for (; c + 3 * S < n_chunks; c += 4 * S) {
-        float mc[4], dc[4], ac[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float* r = rec + (c + u * S) * stride;
-            mc[u] = r[0];
-            dc[u] = r[1];
-            ac[u] = r[4 + f];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            fold(mc[u], dc[u], ac[u]);
-    }
-    for (; c < n_chunks; c += S) {
-        const float* r = rec + c * stride;
-        fold(r[0], r[1], r[4 + f]);
-    }
-    fold_acc[slice][g][f] = a;
-    if (f == 0) {
-        fold_ml[slice][g][0] = M;
-        fold_ml[slice][g][1] = d;
+    // Arrival: every wave waits until its record stores are complete, then
+    // one thread counts the chunk in. The chunk that arrives last resets the
+    // counter and merges the row's records (agent-scope loads, so none comes
+    // from a stale cache line); the others are done.
+    wait_vector_memory();
+    __syncthreads();
+    uint32_t* const arrivals = split.arrivals + (uint64_t)m.split_first[row] * H + kv_head;
+    uint32_t* const last_flag = reinterpret_cast<uint32_t*>(lds_ml); // lds_ml is read out
+    if (threadIdx.x == 0) {
+        const uint32_t before =
+            __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t last = before == n_chunks - 1;
+        if (last)
+            __hip_atomic_store(arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last_flag = last;
     }
     __syncthreads();
-    if (slice != 0)
+    if (!*last_flag)
         return;
-    for (uint32_t t = 1; t < S; ++t)
-        if (fold_ml[t][g][0] != -INFINITY) // a slice with no chunk holds nothing
-            fold(fold_ml[t][g][0], fold_ml[t][g][1], fold_acc[t][g][f]);
-    float o = a / d;
-    if constexpr (GATED)
-        o *= sigmoid(half_value<F16>(gb));
-    out[at] = static_cast<uint16_t>(F16 ? f16_bits(o) : bf16_bits(o));
+    // Thread (slice, g, f) folds chunks slice, slice + S, ... of q head g with
+    // weights 2^(m_c - M) (paged_attention_reduce_f32,
+    // src/metal/kernels/attention.metal:567-615, done online); the S slices are
+    // folded through LDS and the result normalised, gated and rounded once.
+    const uint32_t S = blockDim.x >= G * D ? blockDim.x / (G * D) : 1;
+    for (uint32_t t = threadIdx.x; t < S * G * D; t += blockDim.x) {
+        const uint32_t slice = t / (G * D), g = (t / D) % G, f = t % D;
+        const float* rec = records + g * RF;
+        float M = -INFINITY, d = 0.0f, a = 0.0f;
+        auto fold = [&](float mc, float dc, float ac) {
+            const float nm = fmaxf(M, mc);
+            const float keep = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
+            const float take = fast_exp2(mc - nm);
+            d = d * keep + dc * take;
+            a = a * keep + ac * take;
+            M = nm;
+        };
+        uint32_t c = slice;
+        for (; c + 3 * S < n_chunks; c += 4 * S) {
+            float mc[4], dc[4], ac[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float* r = rec + (c + u * S) * record_stride;
+                mc[u] = agent_load(r);
+                dc[u] = agent_load(r + 1);
+                ac[u] = agent_load(r + 4 + f);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                fold(mc[u], dc[u], ac[u]);
+        }
+        for (; c < n_chunks; c += S) {
+            const float* r = rec + c * record_stride;
+            fold(agent_load(r), agent_load(r + 1), agent_load(r + 4 + f));
+        }
+        if (S == 1) {
+            emit(g, f, 1, a / d);
+            continue;
+        }
+        lds_acc[(slice * G + g) * D + f] = a;
+        if (f == 0) {
+            lds_ml[2 + (slice * G + g) * 2] = M;
+            lds_ml[2 + (slice * G + g) * 2 + 1] = d;
+        }
+    }
+    if (S == 1)
+        return;
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t < G * D; t += blockDim.x) {
+        const uint32_t g = t / D, f = t % D;
+        float M = -INFINITY;
+        for (uint32_t sl = 0; sl < S; ++sl)
+            M = fmaxf(M, lds_ml[2 + (sl * G + g) * 2]);
+        float d = 0.0f, a = 0.0f;
+        for (uint32_t sl = 0; sl < S; ++sl) {
+            const float ms = lds_ml[2 + (sl * G + g) * 2];
+            const float w = ms == -INFINITY ? 0.0f : fast_exp2(ms - M); // a slice may hold no chunk
+            d += lds_ml[2 + (sl * G + g) * 2 + 1] * w;
+            a += lds_acc[(sl * G + g) * D + f] * w;
+        }
+        emit(g, f, 1, a / d);
+    }
 }
 
 // ---- generic path: any head_dim <= 1024, f32 / bf16 / fp16 ---------------------
@@ -758,7 +786,7 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
                        split_scratch split, const rope_table* rope = nullptr,
                        uint32_t rotary = 0)
 {
-    if (!m.plan || (m.n_cut && !split.records))
+    if (!m.plan || (m.n_cut && (!split.records || !split.arrivals)))
         return hipErrorInvalidValue;
     const uint32_t units = m.n_plan * p.kv_heads;
     const uint32_t waves = fast_waves(G, units, cu_count, m.mean_pages, m.split_pages);
@@ -776,7 +804,6 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
             f64.inv_freq[j] = rope->inv_freq[j];
     // one instantiation per (dtype, fused, gated, rope); rope only when fused
     const int variant = (rope ? 8 : 0) | (f16 ? 4 : 0) | (k_in ? 2 : 0) | (gate ? 1 : 0);
-    const float* records = split.records;
     switch (variant) {
 #define CKV_FAST_CASE(V, F16_, FUSED_, GATED_, ROPE_)                                          \
     case V:                                                                                    \
@@ -798,28 +825,6 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
 #undef CKV_FAST_CASE
     default:
         return hipErrorInvalidValue;
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !m.n_cut)
-        return e;
-    const dim3 merge_grid(m.n_cut * p.kv_heads), merge_block(1024);
-    switch ((f16 ? 2 : 0) | (gate ? 1 : 0)) {
-    case 0:
-        merge_chunks_kernel<G, false, false><<<merge_grid, merge_block, 0, s>>>(
-            p, m, q_heads, records, oo, gg);
-        break;
-    case 1:
-        merge_chunks_kernel<G, false, true><<<merge_grid, merge_block, 0, s>>>(
-            p, m, q_heads, records, oo, gg);
-        break;
-    case 2:
-        merge_chunks_kernel<G, true, false><<<merge_grid, merge_block, 0, s>>>(
-            p, m, q_heads, records, oo, gg);
-        break;
-    default:
-        merge_chunks_kernel<G, true, true><<<merge_grid, merge_block, 0, s>>>(
-            p, m, q_heads, records, oo, gg);
-        break;
     }
     return hipGetLastError();
 }

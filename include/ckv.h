@@ -305,19 +305,23 @@ int ckv_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_he
  * capture, tight serving loops, harnesses that forbid hipMalloc): no
  * counterpart in the reference. Same arguments, checks and results as
  * ckv_append_decode, bit for bit, but it calls no hipMalloc, hipFree or other
- * allocating routine: the partial records of rows the batch plan cuts into
- * chunks go to a fixed 16 MiB device array of the library (one per GPU, held
- * until the process ends) instead of pool buffers, and its launches are not
- * timed by ckv_profile_*. It needs what the allocating calls already set up:
+ * allocating routine: the partial records and arrival counters of rows the
+ * batch plan cuts into chunks go to a fixed 16 MiB device array of the
+ * library (one per GPU, held until the process ends) instead of pool buffers,
+ * and its launches are not timed by ckv_profile_*. The array's first 256 KiB
+ * are the counters (zero when the library loads; every call leaves them zero),
+ * the rest the records. It needs what the allocating calls already set up:
  * a batch of single-row query tiles uploaded with ckv_tables_upload or
  * ckv_batch_upload (its plan goes up with it), and the fast decode's geometry
  * (bf16/fp16, head_dim 128, 16-token pages, 1, 2, 4 or 8 q heads per kv head,
  * 16-byte aligned pools, queries and output). Otherwise, and when the batch's
- * records exceed the array (n_records * q_heads * 528 bytes > 16 MiB, see
- * ckv_decode_plan), it returns invalid_argument with a reason in
- * ckv_last_error. Every call on one GPU shares that GPU's array: calls that
- * may overlap on one GPU (other threads, other streams) race, so a caller
- * serialises them, as one stream does. */
+ * records exceed the array (n_records * q_heads * 528 bytes > 16 MiB - 256 KiB
+ * or n_records * kv_heads * 4 bytes > 256 KiB, see ckv_decode_plan), it
+ * returns invalid_argument with a reason in ckv_last_error. Every call on one
+ * GPU shares that GPU's array: calls that may overlap on one GPU (other
+ * threads, other streams) race, on the outputs and on the counters, which can
+ * then stay wrong for later calls; a caller serialises them, as one stream
+ * does. */
 int ckv_append_decode_noalloc(ckv_pool* pool, size_t layer, const void* keys, const void* values,
                               const void* queries, size_t q_heads, float scale, void* output,
                               size_t rows);

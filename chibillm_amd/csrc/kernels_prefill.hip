@@ -32,12 +32,15 @@
 // involved. Eight LDS stages; block kb + 4 is loaded while block kb is
 // scored, and one barrier every two blocks publishes the next two, so each
 // load has two to three iterations in flight. The block table entries are
-// scalar loads, issued a block before their use.
+// scalar loads, issued a block before their use; a page's address is a 32-bit
+// offset from the layer's base (64-bit only for layers beyond 4 GiB).
 //
 // Keys past the tile's last position are read from a zero row (never from
 // the pool), so no page outside a row's table is touched and masked keys
 // carry finite zeros into P.V.
 #include "ckv_internal.h"
+
+#include <type_traits>
 
 namespace ckv {
 namespace {
@@ -107,6 +110,24 @@ __device__ __forceinline__ void dma16_s(const void* base, uint32_t voff, uint32_
                  "s_mov_b32 m0, %0"
                  : "=&s"(saved)
                  : "v"(voff), "s"(base), "s"(lds));
+}
+
+// The K and V DMAs of one block, each with a scalar 64-bit base and a per-lane
+// 32-bit byte offset, under one save and restore of M0.
+__device__ __forceinline__ void dma16_pair(const void* kb, uint32_t koff, uint32_t klds,
+                                           const void* vb, uint32_t voff, uint32_t vlds)
+{
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %3\n\t"
+                 "s_nop 0\n\t"
+                 "global_load_lds_dwordx4 %1, %2\n\t"
+                 "s_mov_b32 m0, %6\n\t"
+                 "s_nop 0\n\t"
+                 "global_load_lds_dwordx4 %4, %5\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(koff), "s"(kb), "s"(klds), "v"(voff), "s"(vb), "s"(vlds));
 }
 
 // vmcnt wait (the other counters left alone) that lets `outstanding` of this
@@ -206,7 +227,7 @@ __device__ __forceinline__ void exponentiate(f32x16_t& s, float m, float& l, flo
     l += sum;
 }
 
-template <int G, bool F16>
+template <int G, bool F16, bool WIDE>
 __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
     pool_view p, meta_view md, uint32_t layer, const uint16_t* __restrict__ q,
     uint16_t* __restrict__ out, uint32_t q_heads, float c, const uint16_t* __restrict__ gate)
@@ -269,6 +290,7 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
     const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
     const size_t page_bytes = (size_t)page_tokens * F * 2;
+    const uint32_t page_bytes32 = __builtin_amdgcn_readfirstlane((uint32_t)page_bytes);
     const uint8_t* kbytes = uniform_ptr(reinterpret_cast<const uint8_t*>(kbase));
     const uint8_t* vbytes = uniform_ptr(reinterpret_cast<const uint8_t*>(vbase));
     const uint8_t* zbytes = reinterpret_cast<const uint8_t*>(zero_row);
@@ -277,29 +299,57 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
     // Block table entries through the constant address space (scalar loads),
     // read one block before that block's loads are issued.
     uint32_t page_a = 0, page_b = 0;
+    const uint32_t last_entry = pos_last / page_tokens; // the tile's last table entry
+    auto fetch_pages_unchecked = [&](uint32_t kb) {
+        using c32 = const __attribute__((address_space(4))) uint32_t;
+        const auto* cb = (const __attribute__((address_space(4))) uint8_t*)(uintptr_t)table;
+        page_a = *(c32*)(cb + 8 * kb);
+        // the block's second page, or its first when the tile ends in the first
+        page_b = *(c32*)(cb + 4 * min(2 * kb + 1, last_entry));
+    };
     auto fetch_pages = [&](uint32_t kb) {
-        if (kb < n_blocks) {
-            const auto* ct = (const __attribute__((address_space(4))) uint32_t*)(uintptr_t)table;
-            const uint32_t key0 = kb * block_keys;
-            page_a = ct[2 * kb];
-            // the block's second page, or its first when the tile ends in the first
-            page_b = ct[2 * kb + (key0 + page_tokens <= pos_last ? 1 : 0)];
-        }
+        if (kb < n_blocks)
+            fetch_pages_unchecked(kb);
     };
     // K region `wave` and V group `wave` of block kb, into its stage
+    // The K region `wave` and V group `wave` of a block whose 32 keys are all
+    // in the tile, from pages pg0 and pg1, into LDS stage address st. A layer
+    // spanning at most 4 GiB takes 32-bit page offsets from its base (two
+    // scalar multiplies); a WIDE one 64-bit page addresses.
+    auto load_full = [&](uint32_t pg0, uint32_t pg1, uint32_t st) {
+        if constexpr (WIDE) {
+            const uint8_t* k0 = kbytes + pg0 * page_bytes;
+            const uint8_t* k1 = kbytes + pg1 * page_bytes;
+            const uint8_t* vp = vbytes + (wave_u >= 4 ? pg1 : pg0) * page_bytes;
+            dma16((k_hi ? k1 : k0) + k_off, st + wave_u * 1024);
+            dma16_s(vp, v_off, st + k_stage_bytes + wave_u * vg_bytes);
+        } else {
+            const uint32_t off0 = pg0 * page_bytes32, off1 = pg1 * page_bytes32;
+            dma16_pair(kbytes, (k_hi ? off1 : off0) + k_off, st + wave_u * 1024, vbytes,
+                       (wave_u >= 4 ? off1 : off0) + v_off,
+                       st + k_stage_bytes + wave_u * vg_bytes);
+        }
+    };
+    // load_block for a block whose keys are all in the tile and whose
+    // successor exists (the page fetch needs no check)
+    auto load_block_steady = [&](uint32_t kb) {
+        const uint32_t pg0 = __builtin_amdgcn_readfirstlane(page_a);
+        const uint32_t pg1 = __builtin_amdgcn_readfirstlane(page_b);
+        fetch_pages_unchecked(kb + 1);
+        load_full(pg0, pg1, lds_base + (kb % n_stages) * stage_bytes);
+    };
     auto load_block = [&](uint32_t kb) {
         const uint32_t key0 = kb * block_keys;
         const uint32_t pg0 = __builtin_amdgcn_readfirstlane(page_a);
         const uint32_t pg1 = __builtin_amdgcn_readfirstlane(page_b);
         fetch_pages(kb + 1);
         const uint32_t st = lds_base + (kb % n_stages) * stage_bytes;
-        const uint8_t* k0 = kbytes + pg0 * page_bytes;
-        const uint8_t* k1 = kbytes + pg1 * page_bytes;
-        const uint8_t* vp = vbytes + (wave_u >= 4 ? pg1 : pg0) * page_bytes;
         if (key0 + block_keys - 1 <= pos_last) { // every key of the block is in the tile
-            dma16((k_hi ? k1 : k0) + k_off, st + wave_u * 1024);
-            dma16_s(vp, v_off, st + k_stage_bytes + wave_u * vg_bytes);
+            load_full(pg0, pg1, st);
         } else {
+            const uint8_t* k0 = kbytes + pg0 * page_bytes;
+            const uint8_t* k1 = kbytes + pg1 * page_bytes;
+            const uint8_t* vp = vbytes + (wave_u >= 4 ? pg1 : pg0) * page_bytes;
             const uint8_t* ksrc = key0 + k_key <= pos_last ? (k_hi ? k1 : k0) + k_off : zbytes + k_feat * 2;
             dma16(ksrc, st + wave_u * 1024);
             const uint8_t* vsrc = key0 + vd_key <= pos_last ? vp + v_off : zbytes + (lane & 15) * 16;
@@ -423,9 +473,18 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
         stats(0);
         rescale();
     }
-    // steady state: iteration kb finishes block kb - 1 and scores block kb
-    for (uint32_t kb = 1; kb < n_blocks; ++kb) {
-        if (kb + 4 < n_blocks)
+    // Iteration kb finishes block kb - 1 and scores block kb. The steady
+    // state runs iterations in pairs (kb odd, kb + 1) while kb + 6 < n_blocks:
+    // the blocks such a pair loads (kb + 4, kb + 5) hold only keys inside the
+    // tile and the pages it fetches (blocks kb + 5, kb + 6) exist, so its loads,
+    // fetches and waits take no checks, and the barrier's place is fixed (ODD).
+    // Cutting the per-block scalar work this way (with the 32-bit page
+    // offsets) made config 4's prefill 4.6 % faster.
+    auto iteration = [&](uint32_t kb, auto steady, auto odd) {
+        constexpr bool STEADY = decltype(steady)::value;
+        if constexpr (STEADY)
+            load_block_steady(kb + 4);
+        else if (kb + 4 < n_blocks)
             load_block(kb + 4);
         uint4 ka[8], va[4][2];
         uint4 pt[2];
@@ -437,13 +496,24 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
         read_v(kb - 1, va);
         pv(va, pt);                  // matrix: block kb - 1
         const bool grew = stats(kb); // vector: block kb
-        if (kb & 1) {
-            wait_dma(newer(kb + 2, kb + 4)); // this wave's loads of blocks kb + 1, kb + 2
+        if (STEADY ? decltype(odd)::value : (kb & 1) != 0) {
+            // this wave's loads of blocks kb + 1, kb + 2 (in the steady state
+            // those of kb + 3 and kb + 4 stay in flight)
+            wait_dma(STEADY ? 4u : newer(kb + 2, kb + 4));
             __syncthreads();
         }
         if (grew)
             rescale(); // before block kb's probabilities are formed
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
+    uint32_t kb = 1;
+    for (; kb + 6 < n_blocks; kb += 2) { // kb odd: a barrier follows it
+        iteration(kb, yes {}, yes {});
+        iteration(kb + 1, yes {}, no {});
     }
+    for (; kb < n_blocks; ++kb)
+        iteration(kb, no {}, no {});
     // the last block's probabilities and product
     {
         uint4 va[4][2];
@@ -485,12 +555,22 @@ hipError_t launch_g(hipStream_t s, const pool_view& p, const meta_view& m, uint3
     const auto* qq = static_cast<const uint16_t*>(q);
     auto* oo = static_cast<uint16_t*>(out);
     const auto* gg = static_cast<const uint16_t*>(gate);
-    if (p.dtype == CKV_F16)
-        hipLaunchKernelGGL((prefill_kernel<G, true>), dim3(grid), dim3(64 * waves), 0, s, p, m,
-                           layer, qq, oo, q_heads, c, gg);
+    // a layer's K (or V) span beyond 4 GiB needs 64-bit page addresses
+    const bool wide = p.layer_elems * 2 > 0xFFFFFFFFull;
+    const bool f16 = p.dtype == CKV_F16;
+    const dim3 g(grid), b(64 * waves);
+    if (f16 && wide)
+        hipLaunchKernelGGL((prefill_kernel<G, true, true>), g, b, 0, s, p, m, layer, qq, oo,
+                           q_heads, c, gg);
+    else if (f16)
+        hipLaunchKernelGGL((prefill_kernel<G, true, false>), g, b, 0, s, p, m, layer, qq, oo,
+                           q_heads, c, gg);
+    else if (wide)
+        hipLaunchKernelGGL((prefill_kernel<G, false, true>), g, b, 0, s, p, m, layer, qq, oo,
+                           q_heads, c, gg);
     else
-        hipLaunchKernelGGL((prefill_kernel<G, false>), dim3(grid), dim3(64 * waves), 0, s, p, m,
-                           layer, qq, oo, q_heads, c, gg);
+        hipLaunchKernelGGL((prefill_kernel<G, false, false>), g, b, 0, s, p, m, layer, qq, oo,
+                           q_heads, c, gg);
     return hipGetLastError();
 }
 

@@ -1652,7 +1652,10 @@ int prefill_impl(ckv_pool* pool, size_t layer, const void* queries, size_t q_hea
         return status;
     const pool_view view = view_of(pool);
     const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-    if (!prefill_supported(view, (uint32_t)q_heads, queries, output) || (gate && !aligned(gate)))
+    // the MFMA kernel tracks maxima of the unscaled scores, which needs scale > 0;
+    // the decode kernels scale first and take any scale, one row at a time
+    if (!prefill_supported(view, (uint32_t)q_heads, queries, output) || (gate && !aligned(gate))
+        || !(scale > 0.0f))
         return run_decode(pool, layer, queries, q_heads, scale, output, gate);
     ckv_context* ctx = pool->ctx;
     return run_kernel(ctx, "paged_attention_prefill", [&] {

@@ -218,9 +218,10 @@ __device__ __forceinline__ float block_max(const f32x16_t& s)
 __device__ __forceinline__ void exponentiate(f32x16_t& s, float m, float& l, float c)
 {
     const float mc = m * c;
-    float sum = 0.0f;
+    s[0] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[0], c, -mc));
+    float sum = s[0]; // an exponential is never -0, so this is 0 + s[0] exactly
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+    for (int r = 1; r < 16; ++r) {
         s[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -mc));
         sum += s[r];
     }
@@ -265,7 +266,8 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
     const bool active = rb * 32 < nrows;
     const uint32_t qpos = pos0 + min(row, nrows - 1);
     const size_t qoff = (size_t)(row0 + min(row, nrows - 1)) * q_stride + (size_t)head * dim;
-    const uint32_t pos_lo = pos0 + rb * 32;
+    // the q-block's first position, wave-uniform: the diagonal test is a scalar branch
+    const uint32_t pos_lo = __builtin_amdgcn_readfirstlane(pos0 + rb * 32);
 
     // Q^T operands: lane (n, g) holds features 16*ks + 8*g .. +7 of its query
     uint4 qr[8];
@@ -362,6 +364,9 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
     for (int mt = 0; mt < 4; ++mt)
         o[mt] = f32x16_t {};
     float m = -__builtin_inff(), l = 0.0f;
+    // the running maximum past which a block's maxima force a rescale
+    float m_limit = -__builtin_inff();
+    const float rescale_raw = rescale_log2 / c;
 
     // Software pipeline over key blocks. Iteration kb issues S(kb) = K(kb) Q^T
     // on the matrix core while the vector ALU turns S(kb-1) into
@@ -435,13 +440,14 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
         }
         sp = sc;
         mx = block_max(sp);
-        return __any((mx - m) * c > rescale_log2);
+        return __any(mx > m_limit);
     };
     auto rescale = [&]() {
         const float m_new = fmaxf(m, mx);
         const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c); // 0 at the start
         l *= alpha;
         m = m_new;
+        m_limit = m_new + rescale_raw;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
             o[mt] *= alpha;

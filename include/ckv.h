@@ -292,7 +292,9 @@ int ckv_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void
 /* Prefill form (paged_flash_attention_prefill_f32,
  * src/metal/kernels/attention.metal:246-444): query tiles of consecutive
  * positions of one sequence share every K/V tile; QK^T and PV run on MFMA
- * for 16-bit pools. Same arguments and checks as ckv_decode_attention. */
+ * for 16-bit pools and scale > 0 (other scales take the decode form row by
+ * row, with the same results). Same arguments and checks as
+ * ckv_decode_attention. */
 int ckv_prefill_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
                           float scale, void* output, size_t rows);
 /* Kernel selection of dispatch_paged_attention_f32 / paged_attention

@@ -208,3 +208,38 @@ def test_layer_beyond_4_gib_takes_64_bit_page_addresses(ctx):
     pool.close()
     del pool
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("scale_value", [-0.125, 0.0])
+def test_non_positive_scale_matches_the_oracle(ctx, scale_value):
+    """softmax(q.k * scale) for scale <= 0 (the reference takes any scale): the
+    prefill route hands such batches to the decode form, which scales every
+    score before taking maxima; a 40-row chunk of one sequence against the
+    oracle."""
+    H, Hq, n, chunk = 2, 4, 300, 40
+    F = H * D
+    rng = orc.Mt64(91)
+    table = rng.permutation(pages_for(n) + 3)[:pages_for(n)].astype(np.uint32)
+    blocks = pages_for(n) + 3
+    k = rng.normal(n * F, orc.BF16).reshape(n, F)
+    v = rng.normal(n * F, orc.BF16).reshape(n, F)
+    pool, _, _ = new_pool(ctx, (1, blocks, 16, H, D), orc.BF16)
+    pool.upload(table, [0] * n, [len(table)] * n, list(range(n)),
+                [orc.slot(table, p, 16) for p in range(n)])
+    pool.append(0, to_dev(k, orc.BF16), to_dev(v, orc.BF16))
+    positions = list(range(n - chunk, n))
+    pool.upload(table, [0] * chunk, [len(table)] * chunk, positions)
+    q = rng.normal(chunk * Hq * D, orc.BF16).reshape(chunk, Hq * D)
+    kc = np.zeros(blocks * 16 * F, np.uint16)
+    vc = np.zeros_like(kc)
+    orc.store_kv(kc, vc, k, v, [orc.slot(table, p, 16) for p in range(n)], 0, blocks * 16)
+    expected = orc.Attention((1, blocks, 16, H, D), kc, vc, orc.BF16, q, orc.BF16, positions,
+                             table, [0] * chunk, [len(table)] * chunk, Hq, 0,
+                             scale_value).online_threads(8)
+    qd = to_dev(q, orc.BF16)
+    for name in ("prefill", "attention"):
+        out = torch.full_like(qd, float("nan"))
+        getattr(pool, name)(0, qd, Hq, scale_value, out)
+        ctx.sync()
+        assert_close(to_f32(out), expected, what=f"{name}, scale {scale_value}")
+    pool.close()

@@ -249,11 +249,11 @@ bool all_distinct(ckv_pool* pool, const uint32_t* keys, size_t n, size_t bound)
     return true;
 }
 
-// Words of the fast decode plan in the metadata block: (row, chunk) pairs,
-// each row's first partial record, then the cut rows.
+// Words of the fast decode plan in the metadata block: the work items'
+// entries, each row's first partial record, then the cut rows.
 size_t plan_words(const decode_plan_shape& shape, size_t rows)
 {
-    return round4(2 * (size_t)shape.n_items) + round4(rows) + shape.n_cut;
+    return round4(plan_entry_words * shape.n_items) + round4(rows) + shape.n_cut;
 }
 
 // Writes the plan at `words` (plan_words long) and points the batch's
@@ -261,10 +261,10 @@ size_t plan_words(const decode_plan_shape& shape, size_t rows)
 void put_plan(ckv_pool* pool, const decode_plan_shape& shape, uint32_t* words,
               const uint32_t* device)
 {
-    const size_t s_first = round4(2 * (size_t)shape.n_items);
+    const size_t s_first = round4(plan_entry_words * shape.n_items);
     const size_t s_cut = s_first + round4(pool->positions.size());
-    write_decode_plan(pool->positions, (uint32_t)pool->block_size, shape, pool->sort_keys, words,
-                      words + s_first, words + s_cut);
+    write_decode_plan(pool->positions, pool->row_offsets, (uint32_t)pool->block_size, shape,
+                      pool->sort_keys, words, words + s_first, words + s_cut);
     meta_view& m = pool->meta;
     m.plan = device;
     m.split_first = device + s_first;
@@ -1117,6 +1117,7 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     // (never the previous batch's pointers with this batch's positions)
     pool->uploaded = false;
     pool->positions.assign(positions, positions + rows);
+    pool->row_offsets.assign(offsets, offsets + rows);
     if (fusable) {
         pool->own_index.resize(rows);
         for (size_t r = 0; r < rows; ++r)
@@ -1348,9 +1349,12 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
     pool->uploaded = false;
     std::vector<uint32_t>& positions = pool->positions;
     positions.resize(rows);
+    pool->row_offsets.resize(rows);
     for (size_t i = 0, r = 0; i < n_items; ++i)
-        for (uint32_t j = 0; j < token_count[i]; ++j)
-            positions[r++] = first_position[i] + j;
+        for (uint32_t j = 0; j < token_count[i]; ++j, ++r) {
+            positions[r] = first_position[i] + j;
+            pool->row_offsets[r] = seq[i] * (uint32_t)pool->seq_cap; // the sequence's arena slot
+        }
     const bool with_plan = !shared;
     const decode_plan_shape plan_shape = with_plan
         ? shape_decode_plan(positions, (uint32_t)bs, (uint32_t)pool->kv_heads, ctx->cu_count)

@@ -39,11 +39,14 @@ struct meta_view {
     const uint32_t* row_first; // first work item of each row
     const uint32_t* row_count; // work items (chunks) of each row
     const uint32_t* tiles;     // prefill query tiles: (first row, row count) pairs
-    // fast decode plan: (row, page chunk) pairs in dispatch order, longest
-    // work first; a row's chunk c covers pages [c*split_pages, (c+1)*split_pages)
+    // fast decode plan: one entry of plan_entry_words per work item in dispatch
+    // order, longest work first: (row, page chunk, the row's position, the flat
+    // table index of the chunk's first page); a row's chunk c covers pages
+    // [c*split_pages, (c+1)*split_pages). A workgroup needs nothing else from
+    // the batch to issue its first page loads.
     const uint32_t* plan;
     const uint32_t* split_first; // first partial record of each row cut into chunks
-    const uint32_t* cut;         // the rows cut into chunks (merged after the launch)
+    const uint32_t* cut;         // the rows cut into chunks
     uint32_t n_entries;
     uint32_t rows;
     uint32_t n_items;
@@ -169,6 +172,7 @@ struct ckv_pool {
     size_t n_entries = 0; // entries of the table the rows index
     size_t slot_rows = 0; // rows with an uploaded slot (0 without slots)
     std::vector<uint32_t> positions;
+    std::vector<uint32_t> row_offsets; // each row's table offset (the decode plan's entries)
     bool shared_tile = false;
     bool fusable = false; // slots are the rows' own positions, one row per table range
     // while fusable: each row's own table index (offset + position / block_size)
@@ -259,9 +263,11 @@ struct decode_plan_shape {
 };
 decode_plan_shape shape_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
                                     uint32_t kv_heads, int cu_count);
-// Writes shape.n_items (row, chunk) pairs to plan, rows words to split_first
-// and the shape.n_cut cut rows to cut.
-void write_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
+constexpr size_t plan_entry_words = 4;
+// Writes shape.n_items plan entries to plan, rows words to split_first and the
+// shape.n_cut cut rows to cut; offsets are the rows' table offsets.
+void write_decode_plan(const std::vector<uint32_t>& positions,
+                       const std::vector<uint32_t>& offsets, uint32_t block_size,
                        const decode_plan_shape& shape, std::vector<uint64_t>& sort_keys,
                        uint32_t* plan, uint32_t* split_first, uint32_t* cut);
 

@@ -207,10 +207,11 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
     const uint32_t part = lane & 15;
     const uint32_t H = p.kv_heads;
     const uint32_t item = blockIdx.x / H;
-    const uint32_t row = m.plan[2 * item];
-    const uint32_t chunk = m.plan[2 * item + 1];
+    const uint4 entry = *reinterpret_cast<const uint4*>(m.plan + plan_entry_words * item);
+    const uint32_t row = entry.x;
+    const uint32_t chunk = entry.y;
     const uint32_t kv_head = blockIdx.x % H;
-    const uint32_t position = m.positions[row];
+    const uint32_t position = entry.z;
     const uint32_t n_pages = position / BS + 1;
     const uint32_t last_in_page = position % BS;
     // this workgroup's pages [pg_first, pg_end) of the row's n_chunks chunks
@@ -227,8 +228,11 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
     const uint64_t page_bytes = (uint64_t)BS * row_bytes;
     const char* kl = static_cast<const char*>(p.keys) + (uint64_t)layer * p.layer_elems * 2u;
     const char* vl = static_cast<const char*>(p.values) + (uint64_t)layer * p.layer_elems * 2u;
-    const uint32_t* tbl = m.table + m.offsets[row];
+    const uint32_t* tbl = m.table + (entry.w - pg_first); // the row's table
     const uint32_t head_off = kv_head * (D * 2u) + part * 16u;
+    // the layer's bases and the table are known from the arguments alone: load
+    // them now, beside the plan entry, not after it
+    asm volatile("" ::"s"(kl), "s"(vl), "s"(m.table), "s"(row_bytes), "s"(q));
 
     uint4 qv[G];
 #pragma unroll
@@ -869,27 +873,34 @@ decode_plan_shape shape_decode_plan(const std::vector<uint32_t>& positions, uint
     return shape;
 }
 
-void write_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
+void write_decode_plan(const std::vector<uint32_t>& positions,
+                       const std::vector<uint32_t>& offsets, uint32_t block_size,
                        const decode_plan_shape& shape, std::vector<uint64_t>& sort_keys,
                        uint32_t* plan, uint32_t* split_first, uint32_t* cut)
 {
     const size_t rows = positions.size();
-    if (!shape.split_pages) {
+    const uint32_t span = shape.split_pages;
+    auto entry = [&](size_t at, uint32_t r, uint32_t chunk) {
+        uint32_t* e = plan + plan_entry_words * at;
+        e[0] = r;
+        e[1] = chunk;
+        e[2] = positions[r];
+        e[3] = offsets[r] + chunk * span;
+    };
+    if (!span) {
         // rows by decreasing position (ties in row order): the longest first
         sort_keys.resize(rows);
         for (size_t r = 0; r < rows; ++r)
             sort_keys[r] = ((uint64_t)(UINT32_MAX - positions[r]) << 32) | r;
         std::sort(sort_keys.begin(), sort_keys.end());
         for (size_t r = 0; r < rows; ++r) {
-            plan[2 * r] = (uint32_t)sort_keys[r];
-            plan[2 * r + 1] = 0;
+            entry(r, (uint32_t)sort_keys[r], 0);
             split_first[r] = 0;
         }
         return;
     }
     // chunks by decreasing page count: the full chunks of every row (row after
     // row), then the short last chunks, longest first
-    const uint32_t span = shape.split_pages;
     uint32_t record = 0;
     size_t at = 0, n_cut = 0;
     sort_keys.clear();
@@ -900,19 +911,15 @@ void write_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_si
         record += n > 1 ? n : 0;
         if (n > 1)
             cut[n_cut++] = (uint32_t)r;
-        for (uint32_t c = 0; c < full; ++c, ++at) {
-            plan[2 * at] = (uint32_t)r;
-            plan[2 * at + 1] = c;
-        }
+        for (uint32_t c = 0; c < full; ++c, ++at)
+            entry(at, (uint32_t)r, c);
         if (full < n)
             sort_keys.push_back(((uint64_t)(span - (pages - full * span)) << 32) | r);
     }
     std::sort(sort_keys.begin(), sort_keys.end());
     for (const uint64_t key : sort_keys) {
         const uint32_t r = (uint32_t)key;
-        plan[2 * at] = r;
-        plan[2 * at + 1] = (positions[r] / block_size + 1) / span; // the last chunk
-        ++at;
+        entry(at++, r, (positions[r] / block_size + 1) / span); // the last chunk
     }
 }
 

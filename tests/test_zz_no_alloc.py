@@ -83,6 +83,41 @@ def test_noalloc_equals_append_decode_on_two_calls(ctx):
         pool.close()
 
 
+def test_noalloc_back_to_back_calls_are_bit_identical(ctx):
+    """100 queued ckv_append_decode_noalloc calls over one cut batch (the same
+    new token appended to the same slot each time, which leaves the pages as
+    they were): the merge of every cut row reuses the array's records and
+    arrival counters call after call, and every output equals the first bit
+    for bit."""
+    lengths = [12000, 5000, 700, 64]
+    B = sum(-(-n // 16) for n in lengths) + 4
+    tables, ks, vs, q = batch(303, lengths, B)
+    pool, _, _ = new_pool(ctx, (1, B, 16, 8, 128), orc.BF16)
+    fill_by_append(pool, [n - 1 for n in lengths], tables, [k[:-1] for k in ks],
+                   [v[:-1] for v in vs])
+    flat = np.concatenate(tables)
+    offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
+    positions = [n - 1 for n in lengths]
+    pool.upload(flat, offsets, [len(t) for t in tables], positions,
+                [orc.slot(t, p, 16) for t, p in zip(tables, positions)])
+    span, _, records = pool.decode_plan()
+    assert span > 0 and records > 0
+    k_new = to_dev(np.stack([k[-1] for k in ks]), orc.BF16)
+    v_new = to_dev(np.stack([v[-1] for v in vs]), orc.BF16)
+    qd = to_dev(q, orc.BF16)
+    outs = [torch.empty(len(lengths), 2048, dtype=torch.bfloat16, device="cuda")
+            for _ in range(100)]
+    for out in outs:
+        pool.append_decode_noalloc(0, k_new, v_new, qd, 16, SCALE, out)
+    ctx.sync()
+    first = outs[0].view(torch.int16)
+    for i, out in enumerate(outs[1:], 1):
+        assert torch.equal(out.view(torch.int16), first), f"call {i} differs from the first"
+    expected = compact_oracle((8, 128), lengths, tables, ks, vs, q, 16)
+    assert_close(to_f32(outs[0]), expected, what="first noalloc call")
+    pool.close()
+
+
 def test_noalloc_refuses_instead_of_allocating(ctx, monkeypatch):
     """A batch of multi-row query tiles (no decode plan uploaded), an f32 pool
     and a plan whose records exceed the 16 MiB array are refused with

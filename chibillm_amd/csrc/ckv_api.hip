@@ -1097,8 +1097,7 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
         while (n < prefill_tile_rows && r + n < rows && offsets[r + n] == offsets[r]
                && lengths[r + n] == lengths[r] && positions[r + n] == positions[r + n - 1] + 1)
             ++n;
-        tiles.push_back((uint32_t)r);
-        tiles.push_back((uint32_t)n);
+        tiles.insert(tiles.end(), { (uint32_t)r, (uint32_t)n, positions[r], offsets[r] });
         shared = shared || n > 1;
         r += n;
     }
@@ -1172,7 +1171,7 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     m.positions = pool->d_meta + s_positions;
     m.slots = pool->d_meta + s_slots;
     m.tiles = pool->d_meta + s_tiles;
-    m.n_tiles = (uint32_t)(tiles.size() / 2);
+    m.n_tiles = (uint32_t)(tiles.size() / tile_entry_words);
     adopt_batch(pool, rows, n_entries, slots != nullptr, shared, fusable, with_plan, false);
     return CKV_OK;
 }
@@ -1334,8 +1333,9 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
             span += token_count[end++];
         for (size_t at = 0; at < span; at += prefill_tile_rows) {
             const size_t n = std::min<size_t>(prefill_tile_rows, span - at);
-            tiles.push_back((uint32_t)(first_row + at));
-            tiles.push_back((uint32_t)n);
+            tiles.insert(tiles.end(), { (uint32_t)(first_row + at), (uint32_t)n,
+                                        (uint32_t)(first_position[i] + at),
+                                        seq[i] * (uint32_t)pool->seq_cap });
             shared = shared || n > 1;
         }
         first_row += span;
@@ -1435,7 +1435,7 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
     m.positions = d + s_positions;
     m.slots = d + s_slots;
     m.tiles = d + s_tiles;
-    m.n_tiles = (uint32_t)(tiles.size() / 2);
+    m.n_tiles = (uint32_t)(tiles.size() / tile_entry_words);
     adopt_batch(pool, rows, pool->seq_max * pool->seq_cap, with_slots != 0, shared, fusable,
                 with_plan, true);
     return CKV_OK;

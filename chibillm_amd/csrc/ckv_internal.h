@@ -38,7 +38,9 @@ struct meta_view {
     const uint32_t* items; // decode work list: (row, chunk) pairs
     const uint32_t* row_first; // first work item of each row
     const uint32_t* row_count; // work items (chunks) of each row
-    const uint32_t* tiles;     // prefill query tiles: (first row, row count) pairs
+    // prefill query tiles, tile_entry_words each: (first row, row count, the
+    // first row's position, the rows' table offset)
+    const uint32_t* tiles;
     // fast decode plan: one entry of plan_entry_words per work item in dispatch
     // order, longest work first: (row, page chunk, the row's position, the flat
     // table index of the chunk's first page); a row's chunk c covers pages
@@ -69,6 +71,8 @@ struct split_scratch {
     float* records;
     uint32_t* arrivals;
 };
+
+constexpr size_t tile_entry_words = 4;
 
 // Largest query tile, in rows (positions): the prefill kernel covers a tile
 // with G workgroups of 256/G rows for GQA group size G.

@@ -241,15 +241,17 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
     const uint32_t rest = blockIdx.x / kv_heads;
     const uint32_t sub = rest % G;
     const uint32_t tile = rest / G;
-    const uint32_t count = md.tiles[2 * tile + 1];
+    // one scalar load gives the tile: first row, rows, first position, table offset
+    const uint4 te = *reinterpret_cast<const uint4*>(md.tiles + tile_entry_words * tile);
+    const uint32_t count = te.y;
     const uint32_t r0 = sub * tile_rows;
     if (r0 >= count)
         return;
     const uint32_t nrows = min(tile_rows, count - r0);
-    const uint32_t row0 = md.tiles[2 * tile] + r0;
-    const uint32_t pos0 = md.positions[row0];
-    const uint32_t pos_last = pos0 + nrows - 1; // positions are consecutive inside a tile
-    const uint32_t* table = md.table + md.offsets[row0];
+    const uint32_t row0 = te.x + r0;
+    const uint32_t pos0 = te.z + r0; // positions are consecutive inside a tile
+    const uint32_t pos_last = pos0 + nrows - 1;
+    const uint32_t* table = md.table + te.w;
     const uint32_t n_blocks = pos_last / block_keys + 1;
 
     const uint32_t tid = threadIdx.x;

@@ -182,16 +182,18 @@ def calibration_copy(ctx):
 # ---- config 2: single-layer decode attention -----------------------------------------
 
 CONFIG2_BATCH, CONFIG2_POOL = 32, 65536
+LONG_ROW_TOKENS = 32768
 CONFIG2_LO, CONFIG2_HI = 256, 4096
 
 
-def bench_config2(args):
+def bench_config2(args, long_row=False):
     """one layer, batch 32, contexts U[256, 4096], 16-token
     pages from a seeded permutation of a 65,536-page pool. A step is one
     ckv_decode_attention call (one decode launch; the rows the plan cuts into
-    chunks are merged by their last chunk) over the uploaded batch; one event pair on the launch
-    stream brackets the timed steps (an event pair per 55 us step would add
-    its own gaps)."""
+    chunks are merged by their last chunk) over the uploaded batch; one event
+    pair on the launch stream brackets the timed steps (an event pair per 55 us
+    step would add its own gaps). long_row (--workload longrow): the same over
+    one row of 32,768 tokens, the single long row split-K exists for."""
     import torch
 
     from chibillm_amd import ckv
@@ -200,6 +202,9 @@ def bench_config2(args):
     device = torch.device("cuda:0")
     gen = np.random.default_rng(args.seed)
     lengths = [int(x) for x in gen.integers(CONFIG2_LO, CONFIG2_HI + 1, CONFIG2_BATCH)]
+    if long_row:
+        lengths = [LONG_ROW_TOKENS]
+    batch = len(lengths)
     perm = gen.permutation(CONFIG2_POOL).astype(np.uint32)
     pages = [math.ceil(n / BLOCK) for n in lengths]
     flat = perm[:sum(pages)]
@@ -214,13 +219,14 @@ def bench_config2(args):
     keys = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=tgen)
     values = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=tgen)
     pool = ckv.Pool(ctx, 1, CONFIG2_POOL, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16, keys, values)
-    q = torch.randn(CONFIG2_BATCH, Q_HEADS * HEAD_DIM, generator=tgen, device=device).to(
+    q = torch.randn(batch, Q_HEADS * HEAD_DIM, generator=tgen, device=device).to(
         torch.bfloat16)
     out = torch.empty_like(q)
     scale = 1.0 / math.sqrt(HEAD_DIM)
     pool.upload(flat, offsets, pages, [n - 1 for n in lengths])
     split_pages, items, records = pool.decode_plan()
-    log(f"config2: {sum(lengths)} tokens, plan: chunks of {split_pages} pages, {items} items, "
+    name = "longrow" if long_row else "config2"
+    log(f"{name}: {sum(lengths)} tokens, plan: chunks of {split_pages} pages, {items} items, "
         f"{records} records")
     for _ in range(args.warmup * 10):
         pool.decode(0, q, Q_HEADS, scale, out)
@@ -235,10 +241,20 @@ def bench_config2(args):
     elapsed = time.perf_counter() - t0
     launch_ms = start.elapsed_time(end) / steps
     kv_bytes = sum(lengths) * F * 2 * 2
-    per_launch = kv_bytes + 2 * CONFIG2_BATCH * Q_HEADS * HEAD_DIM * 2 + 4 * sum(pages)
+    per_launch = kv_bytes + 2 * batch * Q_HEADS * HEAD_DIM * 2 + 4 * sum(pages)
     achieved = per_launch / (launch_ms / 1e3) / 1e9
+    if long_row:
+        metric = ("paged decode KV-read GB/s (% HBM peak), Qwen3-0.6B KV, one layer, one row of "
+                  f"{LONG_ROW_TOKENS} tokens")
+        workload = (f"longrow: single-layer paged GQA decode attention over one row of "
+                    f"{LONG_ROW_TOKENS} tokens, pages from a seeded permutation of a 65,536-page "
+                    "pool")
+    else:
+        metric = "paged decode KV-read GB/s (% HBM peak), Qwen3-0.6B KV, one layer, batch 32"
+        workload = ("config2: single-layer paged GQA decode attention, batch 32, context "
+                    "U[256,4096], pages from a seeded permutation of a 65,536-page pool")
     result = {
-        "metric": "paged decode KV-read GB/s (% HBM peak), Qwen3-0.6B KV, one layer, batch 32",
+        "metric": metric,
         "value": round(kv_bytes / (launch_ms / 1e3) / 1e9, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -252,9 +268,8 @@ def bench_config2(args):
         "dtype": "bf16",
         "data": "synthetic N(0,1) K/V/Q, seeded lengths and page permutation",
         "config": {
-            "workload": "config2: single-layer paged GQA decode attention, batch 32, context "
-                        "U[256,4096], pages from a seeded permutation of a 65,536-page pool",
-            "batch": CONFIG2_BATCH, "kv_heads": KV_HEADS, "q_heads": Q_HEADS,
+            "workload": workload,
+            "batch": batch, "kv_heads": KV_HEADS, "q_heads": Q_HEADS,
             "head_dim": HEAD_DIM, "block_size": BLOCK, "pool_pages": CONFIG2_POOL,
             "tokens": sum(lengths), "plan": {"split_pages": split_pages, "items": items,
                                              "records": records},
@@ -267,7 +282,7 @@ def bench_config2(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_bytes("config2", "decode"),
+            "traffic": None if long_row else traffic_bytes("config2", "decode"),
             "avg_launch_us": round(launch_ms * 1e3, 3),
             "algorithmic_bytes_per_launch": int(per_launch),
         },
@@ -281,7 +296,7 @@ def bench_config2(args):
         log(f"CPU baseline on {threads} threads")
         base = cpu_decode_baseline(lengths, threads, runs=5)
         base["sample"] = (f"the whole workload: oracle/oracle.c decode attention (restated "
-                          f"paged_attention_f32, fp32 accumulate) over the same {CONFIG2_BATCH} "
+                          f"paged_attention_f32, fp32 accumulate) over the same {batch} "
                           f"rows ({sum(lengths)} tokens, {kv_bytes / 1e9:.3f} GB of bf16 K/V), "
                           f"median of 5 runs on {threads} threads and 5 on one")
         result["cpu_baseline"] = base
@@ -894,11 +909,12 @@ def main():
                          "written), the known-size copy the HBM counters are scaled by")
     ap.add_argument("--no-fuse", action="store_true",
                     help="append and decode as two launches instead of ckv_append_decode")
-    ap.add_argument("--workload", choices=["config2", "config3", "config4", "config5", "spill"],
+    ap.add_argument("--workload",
+                    choices=["config2", "config3", "config4", "config5", "spill", "longrow"],
                     default="config3",
                     help="config3 (default): the headline decode step; config2: one layer of "
                          "decode attention, batch 32 (a step is one launch, default 2000 "
-                         "steps); config4: chunked "
+                         "steps); longrow: the same over one 32,768-token row; config4: chunked "
                          "prefill of 64 sequences over a shared prefix (MFMA tiles); config5: "
                          "the continuous-batching churn trace (C++ scheduler driver); spill: "
                          "a cached prefix exported to host memory and imported back")
@@ -922,6 +938,8 @@ def main():
 
     if args.workload == "config2":
         result = bench_config2(args)
+    elif args.workload == "longrow":
+        result = bench_config2(args, long_row=True)
     elif args.workload == "config4":
         result = bench_config4(args)
     elif args.workload == "config5":

@@ -249,7 +249,7 @@ bool all_distinct(ckv_pool* pool, const uint32_t* keys, size_t n, size_t bound)
     return true;
 }
 
-// Words of the fast decode plan in the metadata block: the work items'
+// Words of the fast decode plan in the metadata block: the segments'
 // entries, each row's first partial record, then the cut rows.
 size_t plan_words(const decode_plan_shape& shape, size_t rows)
 {
@@ -269,7 +269,8 @@ void put_plan(ckv_pool* pool, const decode_plan_shape& shape, uint32_t* words,
     m.plan = device;
     m.split_first = device + s_first;
     m.cut = device + s_cut;
-    m.n_plan = shape.n_items;
+    m.n_plan = shape.n_wgs;
+    m.n_segments = shape.n_items;
     m.split_pages = shape.split_pages;
     m.n_records = shape.n_records;
     m.n_cut = shape.n_cut;
@@ -1040,7 +1041,7 @@ void adopt_batch(ckv_pool* pool, size_t rows, size_t n_entries, bool with_slots,
     m.chunk = 0;
     if (!plan_uploaded) {
         m.plan = m.split_first = m.cut = nullptr;
-        m.n_plan = m.split_pages = m.n_records = m.n_cut = 0;
+        m.n_plan = m.n_segments = m.split_pages = m.n_records = m.n_cut = 0;
     }
     pool->has_slots = with_slots;
     pool->slot_rows = with_slots ? rows : 0;
@@ -1454,7 +1455,7 @@ int ckv_decode_plan(ckv_pool* pool, uint32_t* split_pages, uint32_t* work_items,
     if (split_pages)
         *split_pages = pool->meta.split_pages;
     if (work_items)
-        *work_items = pool->meta.n_plan;
+        *work_items = pool->meta.n_segments;
     if (records)
         *records = pool->meta.n_records;
     return CKV_OK;

@@ -41,11 +41,12 @@ struct meta_view {
     // prefill query tiles, tile_entry_words each: (first row, row count, the
     // first row's position, the rows' table offset)
     const uint32_t* tiles;
-    // fast decode plan: one entry of plan_entry_words per work item in dispatch
-    // order, longest work first: (row, page chunk, the row's position, the flat
-    // table index of the chunk's first page); a row's chunk c covers pages
-    // [c*split_pages, (c+1)*split_pages). A workgroup needs nothing else from
-    // the batch to issue its first page loads.
+    // fast decode plan, plan_entry_words per entry: a segment (pages
+    // [first, end) of a row) per entry, (row, the segment's chunk index in
+    // the row, the row's position, the flat table index of page `first`,
+    // first, end, the row's chunk count, the workgroup's next entry or
+    // plan_last). Workgroup w (per kv head) starts at entry w. A workgroup
+    // needs nothing else from the batch to issue its first page loads.
     const uint32_t* plan;
     const uint32_t* split_first; // first partial record of each row cut into chunks
     const uint32_t* cut;         // the rows cut into chunks
@@ -55,8 +56,9 @@ struct meta_view {
     uint32_t chunk; // tokens per decode work item, a multiple of 16
     uint32_t n_tiles;
     uint32_t mean_pages; // pages attended per row, mean over the batch (host side)
-    uint32_t n_plan;      // entries of plan
-    uint32_t split_pages; // pages per chunk of the fast decode; 0: one chunk per row
+    uint32_t n_plan;      // workgroups per kv head of the fast decode (the entries they start at)
+    uint32_t n_segments;  // entries of plan
+    uint32_t split_pages; // the plan's pages per chunk or per workgroup; 0: one row per workgroup
     uint32_t n_records;   // partial records of the rows cut into chunks
     uint32_t n_cut;       // rows cut into chunks
 };
@@ -252,22 +254,32 @@ hipError_t launch_expand_batch(hipStream_t s, const uint32_t* items, uint32_t n_
                                uint32_t* lengths, uint32_t* positions, uint32_t* slots);
 
 // ---- decode plan (kernels_decode.hip) -------------------------------------------
-// The fast decode's plan of a batch, from its rows' positions: how many pages
-// each workgroup covers (0: a row per workgroup), the (row, chunk) items in
-// dispatch order (longest first) and each cut row's first partial record.
-// A row is cut into chunks when one workgroup per (row, kv head) would leave
-// the batch bound by its longest rows: when a row holds more than half of
-// one compute unit's share of the batch's pages. CKV_DECODE_SPLIT=<pages>
-// forces the chunk size (0: no cut).
+// The fast decode's plan of a batch, from its rows' positions: which pages
+// each workgroup covers, as segments of rows, and each cut row's first
+// partial record. A row per workgroup (longest first) while that keeps every
+// compute unit busy; otherwise, when one workgroup per (row, kv head) would
+// leave the batch bound by its longest rows (a row holds more than half of
+// one compute unit's share of the batch's pages), the batch's pages in row
+// order are dealt out evenly to as many workgroups as the GPU holds at once,
+// each taking a run of whole rows and row pieces (balanced). The fixed form
+// cuts each row into chunks of split_pages pages, a workgroup per chunk.
+// CKV_DECODE_SPLIT=<pages> forces the fixed form (0: no cut),
+// CKV_DECODE_BALANCE=<pages> the balanced form with that many pages per
+// workgroup.
 struct decode_plan_shape {
-    uint32_t split_pages;
-    uint32_t n_items;
+    uint32_t split_pages; // pages per chunk (fixed) or per workgroup (balanced); 0: no cut
+    uint32_t n_items;     // plan entries (segments)
     uint32_t n_records;
     uint32_t n_cut;
+    uint32_t n_wgs;       // workgroups per kv head
+    uint32_t n_deal;      // balanced: the workgroups per kv head the pages are dealt to
+    uint64_t deal_work;   // balanced: the work dealt out (pages and segment costs)
+    bool balanced;
 };
 decode_plan_shape shape_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
                                     uint32_t kv_heads, int cu_count);
-constexpr size_t plan_entry_words = 4;
+constexpr size_t plan_entry_words = 8;
+constexpr uint32_t plan_last = 0xFFFFFFFFu; // no next entry
 // Writes shape.n_items plan entries to plan, rows words to split_first and the
 // shape.n_cut cut rows to cut; offsets are the rows' table offsets.
 void write_decode_plan(const std::vector<uint32_t>& positions,

@@ -163,15 +163,16 @@ __host__ __device__ constexpr uint32_t record_floats(uint32_t head_dim)
     return head_dim + 4;
 }
 
-// Fast path, one workgroup per (plan item, kv_head), W waves. A plan item is
-// a row, or one chunk of split_pages pages of a row that the plan cuts (the
-// split-K of paged_attention_partial_f32 / paged_attention_reduce_f32,
+// Fast path, one workgroup per (plan workgroup, kv_head), W waves. A
+// workgroup runs its plan segments one after another: each a row, or a piece
+// (a run of pages) of a row that the plan cuts (the split-K of
+// paged_attention_partial_f32 / paged_attention_reduce_f32,
 // src/metal/kernels/attention.metal:446-615, for any row). With FUSED, the
 // row's new token (position = the row's last) is taken from k_in/v_in rows
 // instead of the cache and stored into its slot by the wave that owns the
 // last page: the append of store_kv and the attention in one pass. Wave w
-// walks pages first+w, first+w+W, ... of its chunk (16-token pages, one scalar
-// table read per page); the next page's K/V loads are issued before the
+// walks pages first+w, first+w+W, ... of its segment (16-token pages, one
+// scalar table read per page); the next page's K/V loads are issued before the
 // current page is processed. Lane 16*group + part reads features 8*part..8*part+7 of token
 // 4j + group of the page (j = 0..3): four 1 KiB wave loads per page for K and
 // four for V. The wave's four row-group softmax states are merged with
@@ -201,381 +202,405 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
     constexpr uint32_t BS = 16;
     extern __shared__ float lds[];
     const uint32_t W = blockDim.x >> 6;
-    const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t group = lane >> 4;
-    const uint32_t part = lane & 15;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // a scalar
     const uint32_t H = p.kv_heads;
-    const uint32_t item = blockIdx.x / H;
-    const uint4 entry = *reinterpret_cast<const uint4*>(m.plan + plan_entry_words * item);
-    const uint32_t row = entry.x;
-    const uint32_t chunk = entry.y;
     const uint32_t kv_head = blockIdx.x % H;
-    const uint32_t position = entry.z;
-    const uint32_t n_pages = position / BS + 1;
-    const uint32_t last_in_page = position % BS;
-    // this workgroup's pages [pg_first, pg_end) of the row's n_chunks chunks
-    const uint32_t span = m.split_pages ? m.split_pages : n_pages;
-    const uint32_t n_chunks = (n_pages + span - 1) / span;
-    const uint32_t pg_first = chunk * span;
-    const uint32_t pg_end = min(pg_first + span, n_pages);
-    uint32_t gate_early = 0; // the first epilogue iteration's gate value (one register)
-    if constexpr (GATED) {
-        if (threadIdx.x < G * D)
-            gate_early = gate[((uint64_t)row * q_heads + kv_head * G) * D + threadIdx.x];
-    }
     const uint32_t row_bytes = p.features * 2u;
     const uint64_t page_bytes = (uint64_t)BS * row_bytes;
     const char* kl = static_cast<const char*>(p.keys) + (uint64_t)layer * p.layer_elems * 2u;
     const char* vl = static_cast<const char*>(p.values) + (uint64_t)layer * p.layer_elems * 2u;
-    const uint32_t* tbl = m.table + (entry.w - pg_first); // the row's table
-    const uint32_t head_off = kv_head * (D * 2u) + part * 16u;
     // the layer's bases and the table are known from the arguments alone: load
     // them now, beside the plan entry, not after it
     asm volatile("" ::"s"(kl), "s"(vl), "s"(m.table), "s"(row_bytes), "s"(q));
 
-    uint4 qv[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-        qv[g] = *reinterpret_cast<const uint4*>(
-            q + ((uint64_t)row * q_heads + kv_head * G + g) * D + part * 8);
+    // One segment: pages [pg_first, pg_end) of a row, chunk `chunk` of the
+    // row's n_chunks (e0 = row, chunk, the row's position, the flat table
+    // index of page pg_first; e1 = pg_first, pg_end, n_chunks, next entry).
+    auto segment = [&](const uint4 e0, const uint4 e1) {
+        // The lane's index, computed anew in each segment (a volatile asm, so it
+        // is not held in a register across the segment loop), and the thread's.
+        uint32_t lane;
+        asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+        const uint32_t tid = wave * 64 + lane;
+        const uint32_t group = lane >> 4;
+        const uint32_t part = lane & 15;
+        const uint32_t head_off = kv_head * (D * 2u) + part * 16u;
+        const uint32_t row = e0.x;
+        const uint32_t chunk = e0.y;
+        const uint32_t position = e0.z;
+        const uint32_t n_pages = position / BS + 1;
+        const uint32_t last_in_page = position % BS;
+        const uint32_t pg_first = e1.x;
+        const uint32_t pg_end = e1.y;
+        const uint32_t n_chunks = e1.z;
+        uint32_t gate_early = 0; // the first epilogue iteration's gate value (one register)
+        if constexpr (GATED) {
+            if (tid < G * D)
+                gate_early = gate[((uint64_t)row * q_heads + kv_head * G) * D + tid];
+        }
+        const uint32_t* tbl = m.table + (e0.w - pg_first); // the row's table
 
-    // ROPE: this lane's 8 features (pairs j0 .. j0 + 7) and their rotation;
-    // every lane of the wave takes part in the exchanges. The queries and the
-    // new token's key share the row's position: both are rotated while the
-    // wave's first page loads, and the rotated key (this lane's 16 bytes of
-    // it) takes the new token's place when the last page is processed. The
-    // row's rotary/2 angles are computed once, by wave 0, into LDS past the
-    // merge area.
-    const uint32_t rot_mask = ROPE ? rotary / 16 : 1; // lane parts per half of the rotary width
-    const bool rot_on = ROPE && part < 2 * rot_mask;
-    const bool rot_first = part < rot_mask;
-    auto angles = [&](float (&rc)[8], float (&rs)[8]) {
-        float* table = lds + W * G * (D + 2); // (cos, sin) per pair
-        if (wave == 0 && lane < rotary / 2) {
-            float sn, cs;
-            sincosf(static_cast<float>(position) * freq.inv_freq[lane], &sn, &cs);
-            table[2 * lane] = cs;
-            table[2 * lane + 1] = sn;
-        }
-        __syncthreads();
-        const uint32_t j0 = 8 * (part & (rot_mask - 1));
+        uint4 qv[G];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            rc[e] = rot_on ? table[2 * (j0 + e)] : 1.0f;
-            rs[e] = rot_on ? table[2 * (j0 + e) + 1] : 0.0f;
-        }
-    };
-    auto rotate = [&](const uint4& w, const float (&rc)[8], const float (&rs)[8]) {
-        const uint32_t in[4] = { w.x, w.y, w.z, w.w };
-        uint32_t r[4];
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const uint32_t pw = __shfl_xor(in[d], (int)rot_mask);
-            const float own[2] = { ops::lo(in[d]), ops::hi(in[d]) };
-            const float par[2] = { ops::lo(pw), ops::hi(pw) };
-            float x[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                float ra, rb;
-                rope_pair(rot_first ? own[h] : par[h], rot_first ? par[h] : own[h], rc[2 * d + h],
-                          rs[2 * d + h], ra, rb);
-                x[h] = rot_first ? ra : rb;
+        for (int g = 0; g < G; ++g)
+            qv[g] = *reinterpret_cast<const uint4*>(
+                q + ((uint64_t)row * q_heads + kv_head * G + g) * D + part * 8);
+
+        // ROPE: this lane's 8 features (pairs j0 .. j0 + 7) and their rotation;
+        // every lane of the wave takes part in the exchanges. The queries and the
+        // new token's key share the row's position: both are rotated while the
+        // wave's first page loads, and the rotated key (this lane's 16 bytes of
+        // it) takes the new token's place when the last page is processed. The
+        // row's rotary/2 angles are computed once, by wave 0, into LDS past the
+        // merge area.
+        const uint32_t rot_mask = ROPE ? rotary / 16 : 1; // lane parts per half of the rotary width
+        const bool rot_on = ROPE && part < 2 * rot_mask;
+        const bool rot_first = part < rot_mask;
+        auto angles = [&](float (&rc)[8], float (&rs)[8]) {
+            float* table = lds + W * G * (D + 2); // (cos, sin) per pair
+            if (wave == 0 && lane < rotary / 2) {
+                float sn, cs;
+                sincosf(static_cast<float>(position) * freq.inv_freq[lane], &sn, &cs);
+                table[2 * lane] = cs;
+                table[2 * lane + 1] = sn;
             }
-            r[d] = rot_on ? ops::pack(x[0], x[1]) : in[d];
-        }
-        return make_uint4(r[0], r[1], r[2], r[3]);
-    };
-    const uint64_t in_row = (uint64_t)row * row_bytes + head_off;
-    uint4 k_new = make_uint4(0, 0, 0, 0); // ROPE: the new token's key, rotated once loaded
-    if constexpr (ROPE)
-        k_new = *reinterpret_cast<const uint4*>(k_in + in_row);
-
-    float mx[G], den[G], acc[G][8];
+            __syncthreads();
+            const uint32_t j0 = 8 * (part & (rot_mask - 1));
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        mx[g] = -INFINITY;
-        den[g] = 0.0f;
-#pragma unroll
-        for (int f = 0; f < 8; ++f)
-            acc[g][f] = 0.0f;
-    }
-
-    // rows past the row's last token re-read that token (in bounds, written)
-    auto load_page = [&](uint32_t pg, uint4* k, uint4* v) {
-        const uint64_t base = (uint64_t)tbl[pg] * page_bytes;
-        const char* kb = kl + base;
-        const char* vb = vl + base;
-        const bool last_page = pg == n_pages - 1;
-        const uint32_t last = last_page ? last_in_page : BS - 1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t r = min(4u * j + group, last);
-            const uint32_t off = r * row_bytes + head_off;
-            const bool fresh = FUSED && last_page && r == last_in_page;
-            // ROPE: the new token's slot is read too and replaced in process
-            k[j] = load_stream(fresh && !ROPE ? k_in + in_row : kb + off);
-            v[j] = load_stream(fresh ? v_in + in_row : vb + off);
-        }
-    };
-
-    auto process = [&](uint4* k, const uint4* v, uint32_t pg) {
-        const uint32_t valid = pg == n_pages - 1 ? last_in_page + 1 : BS;
-        if (FUSED && pg == n_pages - 1) {
-            if constexpr (ROPE) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (4u * j + group == last_in_page)
-                        k[j] = k_new;
+            for (int e = 0; e < 8; ++e) {
+                rc[e] = rot_on ? table[2 * (j0 + e)] : 1.0f;
+                rs[e] = rot_on ? table[2 * (j0 + e) + 1] : 0.0f;
             }
-            // append: the lanes holding the new token write it into its slot
+        };
+        auto rotate = [&](const uint4& w, const float (&rc)[8], const float (&rs)[8]) {
+            const uint32_t in[4] = { w.x, w.y, w.z, w.w };
+            uint32_t r[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t pw = __shfl_xor(in[d], (int)rot_mask);
+                const float own[2] = { ops::lo(in[d]), ops::hi(in[d]) };
+                const float par[2] = { ops::lo(pw), ops::hi(pw) };
+                float x[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    float ra, rb;
+                    rope_pair(rot_first ? own[h] : par[h], rot_first ? par[h] : own[h],
+                              rc[2 * d + h], rs[2 * d + h], ra, rb);
+                    x[h] = rot_first ? ra : rb;
+                }
+                r[d] = rot_on ? ops::pack(x[0], x[1]) : in[d];
+            }
+            return make_uint4(r[0], r[1], r[2], r[3]);
+        };
+        const uint64_t in_row = (uint64_t)row * row_bytes + head_off;
+        uint4 k_new = make_uint4(0, 0, 0, 0); // ROPE: the new token's key, rotated once loaded
+        if constexpr (ROPE)
+            k_new = *reinterpret_cast<const uint4*>(k_in + in_row);
+
+        float mx[G], den[G], acc[G][8];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            mx[g] = -INFINITY;
+            den[g] = 0.0f;
+#pragma unroll
+            for (int f = 0; f < 8; ++f)
+                acc[g][f] = 0.0f;
+        }
+
+        // rows past the row's last token re-read that token (in bounds, written)
+        auto load_page = [&](uint32_t pg, uint4* k, uint4* v) {
             const uint64_t base = (uint64_t)tbl[pg] * page_bytes;
-            const uint32_t off = last_in_page * row_bytes + head_off;
+            const char* kb = kl + base;
+            const char* vb = vl + base;
+            const bool last_page = pg == n_pages - 1;
+            const uint32_t last = last_page ? last_in_page : BS - 1;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                if (4u * j + group == last_in_page) {
-                    *reinterpret_cast<uint4*>(const_cast<char*>(kl) + base + off) = k[j];
-                    *reinterpret_cast<uint4*>(const_cast<char*>(vl) + base + off) = v[j];
+                const uint32_t r = min(4u * j + group, last);
+                const uint32_t off = r * row_bytes + head_off;
+                const bool fresh = FUSED && last_page && r == last_in_page;
+                // ROPE: the new token's slot is read too and replaced in process
+                k[j] = load_stream(fresh && !ROPE ? k_in + in_row : kb + off);
+                v[j] = load_stream(fresh ? v_in + in_row : vb + off);
+            }
+        };
+
+        auto process = [&](uint4* k, const uint4* v, uint32_t pg) {
+            const uint32_t valid = pg == n_pages - 1 ? last_in_page + 1 : BS;
+            if (FUSED && pg == n_pages - 1) {
+                if constexpr (ROPE) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (4u * j + group == last_in_page)
+                            k[j] = k_new;
+                }
+                // append: the lanes holding the new token write it into its slot
+                const uint64_t base = (uint64_t)tbl[pg] * page_bytes;
+                const uint32_t off = last_in_page * row_bytes + head_off;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (4u * j + group == last_in_page) {
+                        *reinterpret_cast<uint4*>(const_cast<char*>(kl) + base + off) = k[j];
+                        *reinterpret_cast<uint4*>(const_cast<char*>(vl) + base + off) = v[j];
+                    }
+                }
+            }
+            bool ok[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                ok[j] = 4u * j + group < valid;
+            float pw[G][4];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float s[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float d = ops::dot2(qv[g].x, k[j].x, 0.0f);
+                    d = ops::dot2(qv[g].y, k[j].y, d);
+                    d = ops::dot2(qv[g].z, k[j].z, d);
+                    d = ops::dot2(qv[g].w, k[j].w, d);
+                    const float r = row16_sum(d) * scale_log2;
+                    s[j] = ok[j] ? r : -INFINITY;
+                }
+                const float nm = fmaxf(mx[g], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+                // rescale only when some lane's running max grew (alpha is 1 elsewhere)
+                if (__builtin_amdgcn_ballot_w64(nm > mx[g])) {
+                    const float alpha = nm == -INFINITY ? 1.0f : fast_exp2(mx[g] - nm);
+                    den[g] *= alpha;
+#pragma unroll
+                    for (int f = 0; f < 8; ++f)
+                        acc[g][f] *= alpha;
+                    mx[g] = nm;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    pw[g][j] = ok[j] ? fast_exp2(s[j] - mx[g]) : 0.0f;
+                den[g] += (pw[g][0] + pw[g][1]) + (pw[g][2] + pw[g][3]);
+            }
+            // token by token: widen the V row once, accumulate it into every q head
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float vf[8] = { ops::lo(v[j].x), ops::hi(v[j].x), ops::lo(v[j].y),
+                                      ops::hi(v[j].y), ops::lo(v[j].z), ops::hi(v[j].z),
+                                      ops::lo(v[j].w), ops::hi(v[j].w) };
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+#pragma unroll
+                    for (int f = 0; f < 8; ++f)
+                        acc[g][f] += pw[g][j] * vf[f];
+            }
+        };
+
+        uint4 ka[4], va[4], kb[4], vb[4];
+        uint32_t pg = pg_first + wave;
+        if (pg < pg_end)
+            load_page(pg, ka, va);
+        // ROPE: rotate the queries and the new key while the first page loads
+        if constexpr (ROPE) {
+            float rc[8], rs[8];
+            angles(rc, rs);
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+                qv[g] = rotate(qv[g], rc, rs);
+            k_new = rotate(k_new, rc, rs);
+        }
+        while (pg < pg_end) {
+            uint32_t next = pg + W;
+            if (next < pg_end)
+                load_page(next, kb, vb);
+            process(ka, va, pg);
+            pg = next;
+            if (pg >= pg_end)
+                break;
+            next = pg + W;
+            if (next < pg_end)
+                load_page(next, ka, va);
+            process(kb, vb, pg);
+            pg = next;
+        }
+
+        // merge the wave's four row-group states (lanes l, l^16, l^32, l^48)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float M = fmaxf(mx[g], __shfl_xor(mx[g], 16));
+            M = fmaxf(M, __shfl_xor(M, 32));
+            const float w = mx[g] == -INFINITY ? 0.0f : fast_exp2(mx[g] - M);
+            float d = den[g] * w;
+            d += __shfl_xor(d, 16);
+            d += __shfl_xor(d, 32);
+#pragma unroll
+            for (int f = 0; f < 8; ++f) {
+                float a = acc[g][f] * w;
+                a += __shfl_xor(a, 16);
+                a += __shfl_xor(a, 32);
+                acc[g][f] = a;
+            }
+            den[g] = d;
+            mx[g] = M;
+        }
+        // LDS: acc [W][G][D], then (max, denominator) [W][G][2]
+        float* lds_acc = lds;
+        float* lds_ml = lds + W * G * D;
+        if (group == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float4* dst = reinterpret_cast<float4*>(lds_acc + (wave * G + g) * D + part * 8);
+                dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+                dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+                if (part == 0) {
+                    lds_ml[(wave * G + g) * 2] = mx[g];
+                    lds_ml[(wave * G + g) * 2 + 1] = den[g];
                 }
             }
         }
-        bool ok[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            ok[j] = 4u * j + group < valid;
-        float pw[G][4];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float s[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float d = ops::dot2(qv[g].x, k[j].x, 0.0f);
-                d = ops::dot2(qv[g].y, k[j].y, d);
-                d = ops::dot2(qv[g].z, k[j].z, d);
-                d = ops::dot2(qv[g].w, k[j].w, d);
-                const float r = row16_sum(d) * scale_log2;
-                s[j] = ok[j] ? r : -INFINITY;
+        __syncthreads();
+        // the workgroup's state of q head g, feature f: the W wave states merged
+        auto wg_state = [&](uint32_t g, uint32_t f, float& M, float& d, float& a) {
+            M = -INFINITY;
+            for (uint32_t w = 0; w < W; ++w)
+                M = fmaxf(M, lds_ml[(w * G + g) * 2]);
+            d = 0.0f;
+            a = 0.0f;
+            for (uint32_t w = 0; w < W; ++w) {
+                const float mw = lds_ml[(w * G + g) * 2];
+                const float weight = mw == -INFINITY ? 0.0f : fast_exp2(mw - M);
+                d += lds_ml[(w * G + g) * 2 + 1] * weight;
+                a += lds_acc[(w * G + g) * D + f] * weight;
             }
-            const float nm = fmaxf(mx[g], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
-            // rescale only when some lane's running max grew (alpha is 1 elsewhere)
-            if (__builtin_amdgcn_ballot_w64(nm > mx[g])) {
-                const float alpha = nm == -INFINITY ? 1.0f : fast_exp2(mx[g] - nm);
-                den[g] *= alpha;
-#pragma unroll
-                for (int f = 0; f < 8; ++f)
-                    acc[g][f] *= alpha;
-                mx[g] = nm;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                pw[g][j] = ok[j] ? fast_exp2(s[j] - mx[g]) : 0.0f;
-            den[g] += (pw[g][0] + pw[g][1]) + (pw[g][2] + pw[g][3]);
-        }
-        // token by token: widen the V row once, accumulate it into every q head
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float vf[8] = { ops::lo(v[j].x), ops::hi(v[j].x), ops::lo(v[j].y),
-                                  ops::hi(v[j].y), ops::lo(v[j].z), ops::hi(v[j].z),
-                                  ops::lo(v[j].w), ops::hi(v[j].w) };
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int f = 0; f < 8; ++f)
-                    acc[g][f] += pw[g][j] * vf[f];
-        }
-    };
-
-    uint4 ka[4], va[4], kb[4], vb[4];
-    uint32_t pg = pg_first + wave;
-    if (pg < pg_end)
-        load_page(pg, ka, va);
-    // ROPE: rotate the queries and the new key while the first page loads
-    if constexpr (ROPE) {
-        float rc[8], rs[8];
-        angles(rc, rs);
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-            qv[g] = rotate(qv[g], rc, rs);
-        k_new = rotate(k_new, rc, rs);
-    }
-    while (pg < pg_end) {
-        uint32_t next = pg + W;
-        if (next < pg_end)
-            load_page(next, kb, vb);
-        process(ka, va, pg);
-        pg = next;
-        if (pg >= pg_end)
-            break;
-        next = pg + W;
-        if (next < pg_end)
-            load_page(next, ka, va);
-        process(kb, vb, pg);
-        pg = next;
-    }
-
-    // merge the wave's four row-group states (lanes l, l^16, l^32, l^48)
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float M = fmaxf(mx[g], __shfl_xor(mx[g], 16));
-        M = fmaxf(M, __shfl_xor(M, 32));
-        const float w = mx[g] == -INFINITY ? 0.0f : fast_exp2(mx[g] - M);
-        float d = den[g] * w;
-        d += __shfl_xor(d, 16);
-        d += __shfl_xor(d, 32);
-#pragma unroll
-        for (int f = 0; f < 8; ++f) {
-            float a = acc[g][f] * w;
-            a += __shfl_xor(a, 16);
-            a += __shfl_xor(a, 32);
-            acc[g][f] = a;
-        }
-        den[g] = d;
-        mx[g] = M;
-    }
-    // LDS: acc [W][G][D], then (max, denominator) [W][G][2]
-    float* lds_acc = lds;
-    float* lds_ml = lds + W * G * D;
-    if (group == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float4* dst = reinterpret_cast<float4*>(lds_acc + (wave * G + g) * D + part * 8);
-            dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-            dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-            if (part == 0) {
-                lds_ml[(wave * G + g) * 2] = mx[g];
-                lds_ml[(wave * G + g) * 2 + 1] = den[g];
-            }
-        }
-    }
-    __syncthreads();
-    // the workgroup's state of q head g, feature f: the W wave states merged
-    auto wg_state = [&](uint32_t g, uint32_t f, float& M, float& d, float& a) {
-        M = -INFINITY;
-        for (uint32_t w = 0; w < W; ++w)
-            M = fmaxf(M, lds_ml[(w * G + g) * 2]);
-        d = 0.0f;
-        a = 0.0f;
-        for (uint32_t w = 0; w < W; ++w) {
-            const float mw = lds_ml[(w * G + g) * 2];
-            const float weight = mw == -INFINITY ? 0.0f : fast_exp2(mw - M);
-            d += lds_ml[(w * G + g) * 2 + 1] * weight;
-            a += lds_acc[(w * G + g) * D + f] * weight;
-        }
-    };
-    auto emit = [&](uint32_t g, uint32_t f, uint32_t it, float o) {
-        const uint64_t at = ((uint64_t)row * q_heads + kv_head * G + g) * D + f;
-        if constexpr (GATED) {
-            const uint16_t gb = it == 0 ? (uint16_t)gate_early : gate[at];
-            o *= sigmoid(half_value<F16>(gb));
-        }
-        out[at] = static_cast<uint16_t>(F16 ? f16_bits(o) : bf16_bits(o));
-    };
-    if (n_chunks == 1) {
-        uint32_t it = 0;
-        for (uint32_t t = threadIdx.x; t < G * D; t += blockDim.x, ++it) {
-            float M, d, a;
-            wg_state(t / D, t % D, M, d, a);
-            emit(t / D, t % D, it, a / d);
-        }
-        return;
-    }
-    // a chunk of a cut row: record [max, denominator, 0, 0, acc[D]] per q head,
-    // stored at agent scope (through to where every XCD reads it)
-    constexpr uint32_t RF = D + 4;
-    const uint64_t record_stride = (uint64_t)q_heads * RF; // between a row's chunks
-    float* const records = split.records
-        + ((uint64_t)m.split_first[row] * q_heads + kv_head * G) * RF;
-    for (uint32_t t = threadIdx.x; t < G * D; t += blockDim.x) {
-        const uint32_t g = t / D, f = t % D;
-        float M, d, a;
-        wg_state(g, f, M, d, a);
-        float* rec = records + chunk * record_stride + g * RF;
-        agent_store(rec + 4 + f, a);
-        if (f == 0) {
-            agent_store(rec, M);
-            agent_store(rec + 1, d);
-        }
-    }
-    // Arrival: every wave waits until its record stores are complete, then
-    // one thread counts the chunk in. The chunk that arrives last resets the
-    // counter and merges the row's records (agent-scope loads, so none comes
-    // from a stale cache line); the others are done.
-    wait_vector_memory();
-    __syncthreads();
-    uint32_t* const arrivals = split.arrivals + (uint64_t)m.split_first[row] * H + kv_head;
-    uint32_t* const last_flag = reinterpret_cast<uint32_t*>(lds_ml); // lds_ml is read out
-    if (threadIdx.x == 0) {
-        const uint32_t before =
-            __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t last = before == n_chunks - 1;
-        if (last)
-            __hip_atomic_store(arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *last_flag = last;
-    }
-    __syncthreads();
-    if (!*last_flag)
-        return;
-    // Thread (slice, g, f) folds chunks slice, slice + S, ... of q head g with
-    // weights 2^(m_c - M) (paged_attention_reduce_f32,
-    // src/metal/kernels/attention.metal:567-615, done online); the S slices are
-    // folded through LDS and the result normalised, gated and rounded once.
-    const uint32_t S = blockDim.x >= G * D ? blockDim.x / (G * D) : 1;
-    for (uint32_t t = threadIdx.x; t < S * G * D; t += blockDim.x) {
-        const uint32_t slice = t / (G * D), g = (t / D) % G, f = t % D;
-        const float* rec = records + g * RF;
-        float M = -INFINITY, d = 0.0f, a = 0.0f;
-        auto fold = [&](float mc, float dc, float ac) {
-            const float nm = fmaxf(M, mc);
-            const float keep = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
-            const float take = fast_exp2(mc - nm);
-            d = d * keep + dc * take;
-            a = a * keep + ac * take;
-            M = nm;
         };
-        uint32_t c = slice;
-        for (; c + 3 * S < n_chunks; c += 4 * S) {
-            float mc[4], dc[4], ac[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float* r = rec + (c + u * S) * record_stride;
-                mc[u] = agent_load(r);
-                dc[u] = agent_load(r + 1);
-                ac[u] = agent_load(r + 4 + f);
+        auto emit = [&](uint32_t g, uint32_t f, uint32_t it, float o) {
+            const uint64_t at = ((uint64_t)row * q_heads + kv_head * G + g) * D + f;
+            if constexpr (GATED) {
+                const uint16_t gb = it == 0 ? (uint16_t)gate_early : gate[at];
+                o *= sigmoid(half_value<F16>(gb));
             }
+            out[at] = static_cast<uint16_t>(F16 ? f16_bits(o) : bf16_bits(o));
+        };
+        if (n_chunks == 1) {
+            uint32_t it = 0;
+            for (uint32_t t = tid; t < G * D; t += blockDim.x, ++it) {
+                float M, d, a;
+                wg_state(t / D, t % D, M, d, a);
+                emit(t / D, t % D, it, a / d);
+            }
+            return;
+        }
+        // a chunk of a cut row: record [max, denominator, 0, 0, acc[D]] per q head,
+        // stored at agent scope (through to where every XCD reads it)
+        constexpr uint32_t RF = D + 4;
+        const uint64_t record_stride = (uint64_t)q_heads * RF; // between a row's chunks
+        float* const records = split.records
+            + ((uint64_t)m.split_first[row] * q_heads + kv_head * G) * RF;
+        for (uint32_t t = tid; t < G * D; t += blockDim.x) {
+            const uint32_t g = t / D, f = t % D;
+            float M, d, a;
+            wg_state(g, f, M, d, a);
+            float* rec = records + chunk * record_stride + g * RF;
+            agent_store(rec + 4 + f, a);
+            if (f == 0) {
+                agent_store(rec, M);
+                agent_store(rec + 1, d);
+            }
+        }
+        // Arrival: every wave waits until its record stores are complete, then
+        // one thread counts the chunk in. The chunk that arrives last resets the
+        // counter and merges the row's records (agent-scope loads, so none comes
+        // from a stale cache line); the others are done.
+        wait_vector_memory();
+        __syncthreads();
+        uint32_t* const arrivals = split.arrivals + (uint64_t)m.split_first[row] * H + kv_head;
+        uint32_t* const last_flag = reinterpret_cast<uint32_t*>(lds_ml); // lds_ml is read out
+        if (tid == 0) {
+            const uint32_t before =
+                __hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t last = before == n_chunks - 1;
+            if (last)
+                __hip_atomic_store(arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *last_flag = last;
+        }
+        __syncthreads();
+        if (!*last_flag)
+            return;
+        // Thread (slice, g, f) folds chunks slice, slice + S, ... of q head g with
+        // weights 2^(m_c - M) (paged_attention_reduce_f32,
+        // src/metal/kernels/attention.metal:567-615, done online); the S slices are
+        // folded through LDS and the result normalised, gated and rounded once.
+        const uint32_t S = blockDim.x >= G * D ? blockDim.x / (G * D) : 1;
+        for (uint32_t t = tid; t < S * G * D; t += blockDim.x) {
+            const uint32_t slice = t / (G * D), g = (t / D) % G, f = t % D;
+            const float* rec = records + g * RF;
+            float M = -INFINITY, d = 0.0f, a = 0.0f;
+            auto fold = [&](float mc, float dc, float ac) {
+                const float nm = fmaxf(M, mc);
+                const float keep = M == -INFINITY ? 0.0f : fast_exp2(M - nm);
+                const float take = fast_exp2(mc - nm);
+                d = d * keep + dc * take;
+                a = a * keep + ac * take;
+                M = nm;
+            };
+            uint32_t c = slice;
+            for (; c + 3 * S < n_chunks; c += 4 * S) {
+                float mc[4], dc[4], ac[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                fold(mc[u], dc[u], ac[u]);
+                for (int u = 0; u < 4; ++u) {
+                    const float* r = rec + (c + u * S) * record_stride;
+                    mc[u] = agent_load(r);
+                    dc[u] = agent_load(r + 1);
+                    ac[u] = agent_load(r + 4 + f);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    fold(mc[u], dc[u], ac[u]);
+            }
+            for (; c < n_chunks; c += S) {
+                const float* r = rec + c * record_stride;
+                fold(agent_load(r), agent_load(r + 1), agent_load(r + 4 + f));
+            }
+            if (S == 1) {
+                emit(g, f, 1, a / d);
+                continue;
+            }
+            lds_acc[(slice * G + g) * D + f] = a;
+            if (f == 0) {
+                lds_ml[2 + (slice * G + g) * 2] = M;
+                lds_ml[2 + (slice * G + g) * 2 + 1] = d;
+            }
         }
-        for (; c < n_chunks; c += S) {
-            const float* r = rec + c * record_stride;
-            fold(agent_load(r), agent_load(r + 1), agent_load(r + 4 + f));
-        }
-        if (S == 1) {
+        if (S == 1)
+            return;
+        __syncthreads();
+        for (uint32_t t = tid; t < G * D; t += blockDim.x) {
+            const uint32_t g = t / D, f = t % D;
+            float M = -INFINITY;
+            for (uint32_t sl = 0; sl < S; ++sl)
+                M = fmaxf(M, lds_ml[2 + (sl * G + g) * 2]);
+            float d = 0.0f, a = 0.0f;
+            for (uint32_t sl = 0; sl < S; ++sl) {
+                const float ms = lds_ml[2 + (sl * G + g) * 2];
+                // a slice may hold no chunk
+                const float w = ms == -INFINITY ? 0.0f : fast_exp2(ms - M);
+                d += lds_ml[2 + (sl * G + g) * 2 + 1] * w;
+                a += lds_acc[(sl * G + g) * D + f] * w;
+            }
             emit(g, f, 1, a / d);
-            continue;
         }
-        lds_acc[(slice * G + g) * D + f] = a;
-        if (f == 0) {
-            lds_ml[2 + (slice * G + g) * 2] = M;
-            lds_ml[2 + (slice * G + g) * 2 + 1] = d;
-        }
-    }
-    if (S == 1)
-        return;
-    __syncthreads();
-    for (uint32_t t = threadIdx.x; t < G * D; t += blockDim.x) {
-        const uint32_t g = t / D, f = t % D;
-        float M = -INFINITY;
-        for (uint32_t sl = 0; sl < S; ++sl)
-            M = fmaxf(M, lds_ml[2 + (sl * G + g) * 2]);
-        float d = 0.0f, a = 0.0f;
-        for (uint32_t sl = 0; sl < S; ++sl) {
-            const float ms = lds_ml[2 + (sl * G + g) * 2];
-            const float w = ms == -INFINITY ? 0.0f : fast_exp2(ms - M); // a slice may hold no chunk
-            d += lds_ml[2 + (sl * G + g) * 2 + 1] * w;
-            a += lds_acc[(sl * G + g) * D + f] * w;
-        }
-        emit(g, f, 1, a / d);
+    };
+
+    // Workgroup blockIdx.x / H starts at that plan entry and follows the
+    // entries' links through its segments.
+    uint32_t at = blockIdx.x / H;
+    for (;;) {
+        // scalar loads (the plan is constant during the launch)
+        using c4 = const __attribute__((address_space(4))) u32x4_t;
+        const auto* e = (c4*)(uintptr_t)(m.plan + plan_entry_words * at);
+        const u32x4_t a = e[0], b = e[1];
+        const uint4 e0 = make_uint4(a.x, a.y, a.z, a.w);
+        const uint4 e1 = make_uint4(b.x, b.y, b.z, b.w);
+        segment(e0, e1);
+        at = e1.w;
+        if (at == plan_last)
+            break;
+        __syncthreads(); // the next segment's merge reuses the LDS
     }
 }
 
@@ -613,18 +638,30 @@ __device__ __forceinline__ float wave_sum(float v)
 
 constexpr int generic_max_features_per_lane = 16; // head_dim <= 1024
 
-// Cut rows (shape_decode_plan): a chunk is a quarter of a compute unit's
-// share of the batch's (page, kv head) units, at least split_min_pages, and
-// no row has more than split_max_chunks chunks (the merge of a row reads its
-// chunks' records: measured on MI355X, a 32K-token row cut into 128 chunks of
-// 16 pages decodes in 24 us and merges in 7.5 us, in 32 chunks of 64 pages
-// the pair takes 29 us in all); its workgroup has split_waves waves. On one
-// MI355X layer (bf16, 8 kv heads): batch 32 of U[256, 4096] tokens 54-55 us
-// for chunks of 16-48 pages (62.5 us uncut); one 5,000-token row 10.8 us at
-// 12 pages (49 us uncut); one 32K-token row 29-32 us at 16-64 pages (356 us
-// uncut).
-constexpr uint64_t split_per_share = 4;
+// Cut rows (shape_decode_plan). The balanced plan deals the batch's pages to
+// split_wgs_per_cu workgroups of split_waves waves per compute unit (all of
+// them resident at once), with a segment costing split_segment_pages pages
+// and no piece shorter than split_min_piece; no more workgroups than rows
+// where pieces would fall under split_min_pages, and no row in more than
+// split_max_chunks pieces (the merge of a row reads its pieces' records:
+// measured on MI355X, a 32K-token row cut into 128 chunks of 16 pages
+// decodes in 24 us and merges in 7.5 us, in 32 chunks of 64 pages the pair
+// takes 29 us in all). With more rows than workgroups, or under
+// split_balance_min_pages pages per workgroup, the round trips of the
+// segments a workgroup runs one after another cost more than the balance
+// gains, and rows are cut into fixed chunks of a quarter of a compute unit's
+// share instead (the config-5 churn took 3 % longer dealing its batches of
+// hundreds of rows).
+// Measured on one MI355X layer (bf16, 8 kv heads, fused append + decode,
+// against fixed chunks throughout): batch 32 of U[256, 4096] tokens -2.8 %
+// time (-0.7 % unfused), 32 rows of 1,024 tokens -14 %, of 4,096 -1.3 %,
+// 64 rows of U[64, 2048] and one 32K-token row within 0.6 %.
+constexpr uint64_t split_wgs_per_cu = 2;
 constexpr uint64_t split_min_pages = 12;
+constexpr uint64_t split_min_piece = 4;
+constexpr uint64_t split_balance_min_pages = 32;
+constexpr uint64_t split_per_share = 4;
+constexpr uint64_t split_segment_pages = 4;
 constexpr uint64_t split_max_chunks = 32;
 constexpr uint32_t split_waves = 8;
 
@@ -835,41 +872,185 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
 
 } // namespace
 
-decode_plan_shape shape_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
-                                    uint32_t kv_heads, int cu_count)
+namespace {
+
+// Pages of a row at `position`, and the batch's total and longest.
+void batch_pages(const std::vector<uint32_t>& positions, uint32_t block_size, uint64_t& total,
+                 uint64_t& longest)
 {
-    decode_plan_shape shape { 0, (uint32_t)positions.size(), 0, 0 };
-    uint64_t total = 0, longest = 0;
+    total = longest = 0;
     for (const uint32_t p : positions) {
         const uint64_t pages = p / block_size + 1;
         total += pages;
         longest = std::max(longest, pages);
     }
-    uint64_t span = 0;
-    if (const char* forced = std::getenv("CKV_DECODE_SPLIT")) {
-        span = (uint64_t)std::max(0L, std::strtol(forced, nullptr, 10));
-    } else {
+}
+
+// The balanced plan's segments: the batch's pages, row after row, dealt to
+// `n` workgroups. A segment costs split_segment_pages pages of work besides
+// its pages (its first loads and its merge wait on memory round trips), so
+// the work dealt out (balanced_work) is the pages plus that cost for every
+// segment, and workgroup k ends at ceil((k + 1) * work / n) of it. No row is cut into a
+// piece shorter than split_min_piece pages (a workgroup takes such a rest
+// with it, or ends early and leaves the row to the next one). Calls
+// emit(row, first page, end page, workgroup) in row order; returns the
+// workgroups used (at most n).
+template <class Emit>
+uint32_t balanced_segments(const std::vector<uint32_t>& positions, uint32_t block_size,
+                           uint64_t work, uint64_t n, Emit&& emit)
+{
+    auto cut = [&](uint64_t i) { return (work * (i + 1) + n - 1) / n; };
+    uint64_t k = 0; // the current workgroup's end, as an index of the cuts
+    uint64_t end = cut(0), done = 0;
+    uint32_t wg = 0;
+    bool empty = true;
+    auto next_wg = [&]() {
+        ++wg;
+        empty = true;
+        if (k + 1 < n)
+            end = cut(++k);
+        while (k + 1 < n && end <= done)
+            end = cut(++k);
+    };
+    for (size_t r = 0; r < positions.size(); ++r) {
+        const uint64_t pages = positions[r] / block_size + 1;
+        uint64_t pg = 0;
+        while (pg < pages) {
+            const uint64_t left = pages - pg;
+            uint64_t take = left;
+            if (k + 1 < n) { // the last workgroup takes what is left
+                const uint64_t cost = done + split_segment_pages;
+                take = std::min(left, end > cost ? end - cost : 0);
+                if (take < left && take < split_min_piece) { // too short a piece to cut off
+                    if (!empty) {
+                        next_wg();
+                        continue;
+                    }
+                    take = std::min(left, split_min_piece);
+                }
+                if (left - take < split_min_piece) // nor leave a short rest
+                    take = left;
+            }
+            emit((uint32_t)r, (uint32_t)pg, (uint32_t)(pg + take), wg);
+            empty = false;
+            pg += take;
+            done += take + split_segment_pages;
+            if (k + 1 < n && done >= end)
+                next_wg();
+        }
+    }
+    return empty ? wg : wg + 1;
+}
+
+// The work balanced_segments deals out: the batch's pages plus the segment
+// cost of as many segments as dealing that work makes (every row and every
+// workgroup has one; found by dealing again until the count holds, at most
+// four times), so the last workgroup's share comes out like the others.
+uint64_t balanced_work(const std::vector<uint32_t>& positions, uint32_t block_size,
+                       uint64_t total, uint64_t n)
+{
+    uint64_t segments = std::max<uint64_t>(positions.size(), n);
+    for (int round = 0; round < 4; ++round) {
+        uint64_t count = 0;
+        balanced_segments(positions, block_size, total + split_segment_pages * segments, n,
+                          [&](uint32_t, uint32_t, uint32_t, uint32_t) { ++count; });
+        if (count == segments)
+            break;
+        segments = count;
+    }
+    return total + split_segment_pages * segments;
+}
+
+uint64_t forced_pages(const char* name, bool& set)
+{
+    const char* v = std::getenv(name);
+    set = v != nullptr;
+    return v ? (uint64_t)std::max(0L, std::strtol(v, nullptr, 10)) : 0;
+}
+
+} // namespace
+
+decode_plan_shape shape_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
+                                    uint32_t kv_heads, int cu_count)
+{
+    const uint32_t rows = (uint32_t)positions.size();
+    decode_plan_shape shape { 0, rows, 0, 0, rows, 0, 0, false };
+    uint64_t total, longest;
+    batch_pages(positions, block_size, total, longest);
+    bool fixed_set, balanced_set;
+    uint64_t span = forced_pages("CKV_DECODE_SPLIT", fixed_set);
+    const uint64_t target = forced_pages("CKV_DECODE_BALANCE", balanced_set);
+    uint64_t deal = 0; // workgroups per kv head the balanced plan deals the pages to
+    if (balanced_set) {
+        deal = target ? (total + target - 1) / target : 0;
+    } else if (!fixed_set) {
         // a compute unit's share of the batch, in (page, kv head) units
-        const uint64_t share = total * kv_heads / (uint64_t)std::max(cu_count, 1);
-        if (2 * longest > share)
-            span = std::max({ split_min_pages, (share + split_per_share - 1) / split_per_share,
-                              (longest + split_max_chunks - 1) / split_max_chunks });
+        const uint64_t cus = (uint64_t)std::max(cu_count, 1);
+        const uint64_t share = total * kv_heads / cus;
+        if (2 * longest > share) {
+            // as many workgroups as the GPU holds at once, but no more than a
+            // row each where rows are short (pieces of at least
+            // split_min_pages), nor more than split_max_chunks to a row
+            const uint64_t slots = std::max<uint64_t>(1, cus * split_wgs_per_cu / kv_heads);
+            const uint64_t piece = std::max(split_min_pages,
+                                            (longest + split_max_chunks - 1) / split_max_chunks);
+            deal = std::max<uint64_t>(1, std::min(slots, std::max<uint64_t>(rows, total / piece)));
+            // More rows than workgroups (the balanced plan would run several
+            // whole rows one after another in a workgroup, each paying its
+            // round trips) or too little work per workgroup to pay for a
+            // second segment: fixed chunks instead, a quarter of a compute
+            // unit's share, dispatched longest first.
+            if (rows > deal || total < deal * split_balance_min_pages) {
+                deal = 0;
+                span = std::max({ split_min_pages, (share + split_per_share - 1) / split_per_share,
+                                  (longest + split_max_chunks - 1) / split_max_chunks });
+                fixed_set = true;
+            }
+        }
     }
-    if (span == 0 || span >= longest)
+    uint64_t items = 0, records = 0, cut = 0, wgs = 0, per_wg = 0;
+    if (deal) {
+        uint32_t run_row = UINT32_MAX;
+        uint64_t run = 0;
+        auto close_run = [&]() {
+            records += run > 1 ? run : 0;
+            cut += run > 1 ? 1 : 0;
+        };
+        shape.deal_work = balanced_work(positions, block_size, total, deal);
+        wgs = balanced_segments(positions, block_size, shape.deal_work, deal,
+                                [&](uint32_t r, uint32_t, uint32_t, uint32_t) {
+                                    ++items;
+                                    if (r != run_row) {
+                                        close_run();
+                                        run_row = r;
+                                        run = 0;
+                                    }
+                                    ++run;
+                                });
+        close_run();
+        shape.balanced = true;
+        per_wg = balanced_set ? target : (total + deal - 1) / deal;
+    } else if (fixed_set && span && span < longest) {
+        for (const uint32_t p : positions) {
+            const uint64_t n = (p / block_size + span) / span; // chunks of (p / bs + 1) pages
+            items += n;
+            records += n > 1 ? n : 0;
+            cut += n > 1 ? 1 : 0;
+        }
+        wgs = items;
+        per_wg = span;
+    } else {
         return shape; // a row per workgroup
-    uint64_t items = 0, records = 0, cut = 0;
-    for (const uint32_t p : positions) {
-        const uint64_t n = (p / block_size + span) / span; // chunks of (p / bs + 1) pages
-        items += n;
-        records += n > 1 ? n : 0;
-        cut += n > 1 ? 1 : 0;
     }
-    if (items > UINT32_MAX / kv_heads || records > UINT32_MAX || cut > UINT32_MAX / kv_heads)
-        return shape;
-    shape.split_pages = (uint32_t)span;
+    if (items > UINT32_MAX / plan_entry_words || wgs > UINT32_MAX / kv_heads
+        || records > UINT32_MAX / kv_heads)
+        return decode_plan_shape { 0, rows, 0, 0, rows, 0, 0, false };
+    shape.split_pages = (uint32_t)per_wg;
+    shape.n_deal = (uint32_t)deal;
     shape.n_items = (uint32_t)items;
     shape.n_records = (uint32_t)records;
     shape.n_cut = (uint32_t)cut;
+    shape.n_wgs = (uint32_t)wgs;
     return shape;
 }
 
@@ -880,13 +1061,19 @@ void write_decode_plan(const std::vector<uint32_t>& positions,
 {
     const size_t rows = positions.size();
     const uint32_t span = shape.split_pages;
-    auto entry = [&](size_t at, uint32_t r, uint32_t chunk) {
+    auto entry = [&](size_t at, uint32_t r, uint32_t chunk, uint32_t first, uint32_t end,
+                     uint32_t n_chunks, uint32_t next) {
         uint32_t* e = plan + plan_entry_words * at;
         e[0] = r;
         e[1] = chunk;
         e[2] = positions[r];
-        e[3] = offsets[r] + chunk * span;
+        e[3] = offsets[r] + first;
+        e[4] = first;
+        e[5] = end;
+        e[6] = n_chunks;
+        e[7] = next;
     };
+    auto pages_of = [&](size_t r) { return positions[r] / block_size + 1; };
     if (!span) {
         // rows by decreasing position (ties in row order): the longest first
         sort_keys.resize(rows);
@@ -894,32 +1081,75 @@ void write_decode_plan(const std::vector<uint32_t>& positions,
             sort_keys[r] = ((uint64_t)(UINT32_MAX - positions[r]) << 32) | r;
         std::sort(sort_keys.begin(), sort_keys.end());
         for (size_t r = 0; r < rows; ++r) {
-            entry(r, (uint32_t)sort_keys[r], 0);
+            const uint32_t row = (uint32_t)sort_keys[r];
+            entry(r, row, 0, 0, pages_of(row), 1, plan_last);
             split_first[r] = 0;
         }
         return;
     }
-    // chunks by decreasing page count: the full chunks of every row (row after
-    // row), then the short last chunks, longest first
+    if (shape.balanced) {
+        // the segments in row order, two words each: (row, first), (end, workgroup)
+        sort_keys.clear();
+        balanced_segments(positions, block_size, shape.deal_work, shape.n_deal,
+                          [&](uint32_t r, uint32_t first, uint32_t end, uint32_t wg) {
+                              sort_keys.push_back(((uint64_t)r << 32) | first);
+                              sort_keys.push_back(((uint64_t)end << 32) | wg);
+                          });
+        // Workgroup w's first segment is entry w, its others follow the
+        // first segments in order, each entry linking to the next.
+        const size_t n = sort_keys.size() / 2;
+        auto row_at = [&](size_t i) { return (uint32_t)(sort_keys[2 * i] >> 32); };
+        auto wg_at = [&](size_t i) { return (uint32_t)sort_keys[2 * i + 1]; };
+        std::fill(split_first, split_first + rows, 0u);
+        size_t more = shape.n_wgs, n_cut = 0;
+        uint32_t record = 0, run = 0, chunk = 0;
+        for (size_t i = 0; i < n; ++i) {
+            const uint32_t r = row_at(i), wg = wg_at(i);
+            if (i == 0 || r != row_at(i - 1)) { // a row's first segment: count its segments
+                run = 1;
+                while (i + run < n && row_at(i + run) == r)
+                    ++run;
+                chunk = 0;
+                if (run > 1) {
+                    split_first[r] = record;
+                    record += run;
+                    cut[n_cut++] = r;
+                }
+            }
+            const size_t at = i == 0 || wg != wg_at(i - 1) ? wg : more++;
+            const uint32_t next = i + 1 < n && wg_at(i + 1) == wg ? (uint32_t)more : plan_last;
+            const uint32_t first = (uint32_t)sort_keys[2 * i];
+            const uint32_t end = (uint32_t)(sort_keys[2 * i + 1] >> 32);
+            entry(at, r, chunk++, first, end, run, next);
+        }
+        return;
+    }
+    // fixed chunks by decreasing page count: the full chunks of every row (row
+    // after row), then the short last chunks, longest first
     uint32_t record = 0;
     size_t at = 0, n_cut = 0;
+    auto chunk_entry = [&](size_t at, uint32_t r, uint32_t c) {
+        const uint32_t pages = pages_of(r);
+        entry(at, r, c, c * span, std::min(c * span + span, pages), (pages + span - 1) / span,
+              plan_last);
+    };
     sort_keys.clear();
     for (size_t r = 0; r < rows; ++r) {
-        const uint32_t pages = positions[r] / block_size + 1;
+        const uint32_t pages = pages_of(r);
         const uint32_t n = (pages + span - 1) / span, full = pages / span;
         split_first[r] = n > 1 ? record : 0;
         record += n > 1 ? n : 0;
         if (n > 1)
             cut[n_cut++] = (uint32_t)r;
         for (uint32_t c = 0; c < full; ++c, ++at)
-            entry(at, (uint32_t)r, c);
+            chunk_entry(at, (uint32_t)r, c);
         if (full < n)
             sort_keys.push_back(((uint64_t)(span - (pages - full * span)) << 32) | r);
     }
     std::sort(sort_keys.begin(), sort_keys.end());
     for (const uint64_t key : sort_keys) {
         const uint32_t r = (uint32_t)key;
-        entry(at++, r, (positions[r] / block_size + 1) / span); // the last chunk
+        chunk_entry(at++, r, pages_of(r) / span); // the last chunk
     }
 }
 

@@ -242,10 +242,12 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
                      const uint32_t* token_count, size_t n_items, int with_slots);
 
 /* The fast decode's plan of the current batch (deriving it if a decode launch
- * has not yet): pages per workgroup chunk (0 when every (row, kv head) is one
- * workgroup), work items (rows or row chunks) and partial records. A row is
- * cut into chunks when one workgroup per (row, kv head) would leave the batch
- * bound by its longest rows; the chunks are merged as
+ * has not yet): pages per workgroup (0 when every (row, kv head) is one
+ * workgroup), work items (rows or row pieces; a workgroup may take several)
+ * and partial records. Rows are cut when one workgroup per (row, kv head)
+ * would leave the batch bound by its longest rows: the batch's pages are then
+ * dealt out evenly to as many workgroups as the GPU holds at once, and a
+ * row's pieces are merged as
  * paged_attention_reduce_f32 merges (src/metal/kernels/attention.metal:567-615).
  * A diagnostic with no counterpart in the reference, for tests and tuning. */
 int ckv_decode_plan(ckv_pool* pool, uint32_t* split_pages, uint32_t* work_items,

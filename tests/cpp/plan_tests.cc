@@ -1,0 +1,266 @@
+// The fast decode's batch planner (shape_decode_plan / write_decode_plan in
+// libckv), on the CPU: every plan covers each row's pages exactly once, in
+// segments whose chunk indices, chunk counts, table offsets and partial
+// records agree; each workgroup's entries link from entry w through its
+// segments; the balanced plan evens out the work; the fixed and forced forms
+// follow their definitions. The plans' outputs on the GPU are checked against
+// the oracle by the -m gpu tests.
+#include <algorithm>
+#include <cstdlib>
+#include <random>
+#include <utility>
+
+#include "check.h"
+#include "ckv_internal.h"
+
+namespace {
+
+constexpr uint32_t bs = 16;
+
+struct plan_view {
+    ckv::decode_plan_shape shape;
+    std::vector<uint32_t> entries, split_first, cut;
+    std::vector<std::vector<uint32_t>> wg_segments; // entry indices per workgroup
+    std::vector<uint64_t> wg_pages;
+};
+
+uint32_t pages_of(uint32_t position)
+{
+    return position / bs + 1;
+}
+
+// Builds the plan of `positions` (rows' table offsets packed in row order)
+// and checks every structural property; returns it for further checks.
+plan_view plan_and_check(const std::vector<uint32_t>& positions, uint32_t kv_heads, int cus)
+{
+    plan_view v;
+    v.shape = ckv::shape_decode_plan(positions, bs, kv_heads, cus);
+    std::vector<uint32_t> offsets(positions.size());
+    uint32_t at = 0;
+    for (size_t r = 0; r < positions.size(); ++r) {
+        offsets[r] = at;
+        at += pages_of(positions[r]);
+    }
+    const auto& s = v.shape;
+    v.entries.assign(ckv::plan_entry_words * s.n_items, 0xDEADBEEFu);
+    v.split_first.assign(positions.size(), 0xDEADBEEFu);
+    v.cut.assign(s.n_cut, 0xDEADBEEFu);
+    std::vector<uint64_t> scratch;
+    ckv::write_decode_plan(positions, offsets, bs, s, scratch, v.entries.data(),
+                           v.split_first.data(), v.cut.data());
+    REQUIRE(s.n_wgs >= 1 && s.n_wgs <= s.n_items);
+    // walk every workgroup's links; each entry is reached once
+    std::vector<int> seen(s.n_items, 0);
+    std::vector<std::vector<std::pair<uint32_t, uint32_t>>> cover(positions.size());
+    std::vector<uint32_t> chunk_count(positions.size(), 0);
+    for (uint32_t w = 0; w < s.n_wgs; ++w) {
+        std::vector<uint32_t> segs;
+        uint64_t pages = 0;
+        for (uint32_t e = w;;) {
+            REQUIRE(e < s.n_items);
+            REQUIRE(!seen[e]);
+            seen[e] = 1;
+            segs.push_back(e);
+            const uint32_t* x = &v.entries[ckv::plan_entry_words * e];
+            const uint32_t row = x[0];
+            REQUIRE(row < positions.size());
+            CHECK(x[2] == positions[row]);
+            REQUIRE(x[4] < x[5] && x[5] <= pages_of(positions[row]));
+            CHECK(x[3] == offsets[row] + x[4]);
+            REQUIRE(x[1] < x[6]);
+            cover[row].push_back({ x[4], x[5] });
+            chunk_count[row] = x[6];
+            pages += x[5] - x[4];
+            if (x[7] == ckv::plan_last)
+                break;
+            e = x[7];
+        }
+        v.wg_segments.push_back(segs);
+        v.wg_pages.push_back(pages);
+    }
+    for (uint32_t e = 0; e < s.n_items; ++e)
+        CHECK(seen[e]);
+    // each row: pages 0..n covered once, by its n_chunks pieces in chunk order
+    uint32_t records = 0, n_cut = 0;
+    std::vector<std::pair<uint32_t, uint32_t>> record_ranges;
+    for (size_t r = 0; r < positions.size(); ++r) {
+        auto c = cover[r];
+        std::sort(c.begin(), c.end());
+        uint32_t pg = 0;
+        for (const auto& piece : c) {
+            CHECK(piece.first == pg);
+            pg = piece.second;
+        }
+        CHECK(pg == pages_of(positions[r]));
+        CHECK(chunk_count[r] == c.size());
+        if (c.size() > 1) {
+            records += (uint32_t)c.size();
+            CHECK(v.cut[n_cut] == r);
+            ++n_cut;
+            record_ranges.push_back({ v.split_first[r], v.split_first[r] + (uint32_t)c.size() });
+        }
+    }
+    CHECK(records == s.n_records);
+    CHECK(n_cut == s.n_cut);
+    // the cut rows' records are disjoint ranges inside [0, n_records)
+    std::sort(record_ranges.begin(), record_ranges.end());
+    for (size_t i = 0; i < record_ranges.size(); ++i) {
+        CHECK(record_ranges[i].second <= s.n_records);
+        if (i)
+            CHECK(record_ranges[i - 1].second <= record_ranges[i].first);
+    }
+    // chunk c of a row covers the row's c-th range of pages
+    for (uint32_t e = 0; e < s.n_items; ++e) {
+        const uint32_t* x = &v.entries[ckv::plan_entry_words * e];
+        auto c = cover[x[0]];
+        std::sort(c.begin(), c.end());
+        CHECK(c[x[1]].first == x[4]);
+    }
+    return v;
+}
+
+std::vector<uint32_t> uniform_rows(std::mt19937_64& g, size_t n, uint32_t lo, uint32_t hi)
+{
+    std::vector<uint32_t> p(n);
+    for (auto& x : p)
+        x = lo + (uint32_t)(g() % (hi - lo + 1)) - 1; // positions of rows of lo..hi tokens
+    return p;
+}
+
+struct env_guard {
+    const char* name;
+    env_guard(const char* n, const char* value) : name(n) { setenv(n, value, 1); }
+    ~env_guard() { unsetenv(name); }
+};
+
+} // namespace
+
+TEST("config-2 batch: balanced, every workgroup within a few pages of its share")
+{
+    std::mt19937_64 g(0);
+    const auto p = uniform_rows(g, 32, 256, 4096);
+    const auto v = plan_and_check(p, 8, 256);
+    CHECK(v.shape.balanced);
+    CHECK(v.shape.n_wgs == 64); // two 8-wave workgroups per compute unit, 8 kv heads
+    // work per workgroup (pages plus 4 per segment): all within 16 of each
+    // other (a row's short rest stays with its neighbour), 60 of the 64 within
+    // 2 of the median
+    std::vector<uint64_t> work;
+    for (size_t w = 0; w < v.wg_pages.size(); ++w)
+        work.push_back(v.wg_pages[w] + 4 * v.wg_segments[w].size());
+    std::sort(work.begin(), work.end());
+    const uint64_t median = work[work.size() / 2];
+    CHECK(work.back() - work.front() <= 16);
+    size_t near = 0;
+    for (const uint64_t x : work)
+        near += x + 2 >= median && x <= median + 2;
+    CHECK(near >= 60);
+    for (const auto& segs : v.wg_segments)
+        CHECK(segs.size() <= 3);
+}
+
+TEST("uniform rows: balanced pieces of one row each")
+{
+    for (uint32_t tokens : { 1024u, 4096u, 16384u }) {
+        const std::vector<uint32_t> p(32, tokens - 1);
+        const auto v = plan_and_check(p, 8, 256);
+        CHECK(v.shape.balanced);
+        CHECK(v.shape.n_wgs == 64);
+        for (size_t w = 0; w < v.wg_pages.size(); ++w) {
+            CHECK(v.wg_segments[w].size() == 1);
+            CHECK(v.wg_pages[w] == pages_of(tokens - 1) / 2);
+        }
+    }
+}
+
+TEST("short rows, small batches and many rows keep the fixed plan")
+{
+    // one page per row: a row per workgroup
+    auto v = plan_and_check(std::vector<uint32_t>(32, 15), 8, 256);
+    CHECK(!v.shape.balanced && v.shape.split_pages == 0 && v.shape.n_wgs == 32);
+    // 16-page rows: too little work to balance; fixed chunks of 12 pages
+    v = plan_and_check(std::vector<uint32_t>(32, 255), 8, 256);
+    CHECK(!v.shape.balanced && v.shape.split_pages == 12 && v.shape.n_items == 64);
+    // 128 rows of 1K-8K tokens fill the GPU with whole rows
+    std::mt19937_64 g(1);
+    v = plan_and_check(uniform_rows(g, 128, 1024, 8192), 8, 256);
+    CHECK(!v.shape.balanced && v.shape.split_pages == 0 && v.shape.n_items == 128);
+    // hundreds of rows with one far longer: more rows than workgroups, so fixed chunks
+    auto many = uniform_rows(g, 300, 1, 600);
+    many.push_back(200000);
+    v = plan_and_check(many, 8, 256);
+    CHECK(!v.shape.balanced && v.shape.split_pages > 0);
+    for (const auto& segs : v.wg_segments)
+        CHECK(segs.size() == 1);
+}
+
+TEST("one long row: at most 32 pieces")
+{
+    for (uint32_t tokens : { 5000u, 32768u, 40960u, 1000000u }) {
+        const auto v = plan_and_check({ tokens - 1 }, 8, 256);
+        CHECK(v.shape.n_items <= 32);
+        CHECK(v.shape.n_records == v.shape.n_items);
+        CHECK(v.shape.n_cut == 1);
+    }
+}
+
+TEST("fixed chunks follow their definition (CKV_DECODE_SPLIT)")
+{
+    const env_guard e("CKV_DECODE_SPLIT", "5");
+    const std::vector<uint32_t> p = { 2999, 699, 63, 2499, 0, 79 };
+    const auto v = plan_and_check(p, 8, 256);
+    CHECK(!v.shape.balanced && v.shape.split_pages == 5);
+    uint32_t items = 0, records = 0;
+    for (const uint32_t x : p) {
+        const uint32_t n = (pages_of(x) + 4) / 5;
+        items += n;
+        records += n > 1 ? n : 0;
+    }
+    CHECK(v.shape.n_items == items && v.shape.n_wgs == items && v.shape.n_records == records);
+    for (size_t w = 0; w < v.wg_pages.size(); ++w)
+        CHECK(v.wg_pages[w] <= 5);
+}
+
+TEST("forced balance: several rows and pieces to a workgroup (CKV_DECODE_BALANCE)")
+{
+    const std::vector<uint32_t> p = { 0, 15, 16, 31, 32, 111, 112, 126, 499, 1998 };
+    {
+        const env_guard e("CKV_DECODE_BALANCE", "40");
+        const auto v = plan_and_check(p, 8, 256);
+        CHECK(v.shape.balanced && v.shape.split_pages == 40);
+        size_t most = 0;
+        for (const auto& segs : v.wg_segments)
+            most = std::max(most, segs.size());
+        CHECK(most >= 3);
+    }
+    {
+        const env_guard e("CKV_DECODE_BALANCE", "100000");
+        const auto v = plan_and_check(p, 8, 256);
+        CHECK(v.shape.n_wgs == 1 && v.shape.n_items == p.size() && v.shape.n_records == 0);
+    }
+    for (const char* t : { "1", "2", "7" }) {
+        const env_guard e("CKV_DECODE_BALANCE", t);
+        plan_and_check(p, 8, 256);
+    }
+}
+
+TEST("random batches at random GPU sizes: every plan is well formed")
+{
+    std::mt19937_64 g(7);
+    for (int t = 0; t < 1500; ++t) {
+        std::vector<uint32_t> p(1 + g() % 70);
+        for (auto& x : p)
+            x = (uint32_t)(g() % ((g() % 3) ? 2000 : 20000));
+        const uint32_t heads = 1 + (uint32_t)(g() % 16);
+        const int cus = 1 + (int)(g() % 320);
+        if (t % 3 == 1) {
+            const env_guard e("CKV_DECODE_BALANCE", std::to_string(1 + g() % 90).c_str());
+            plan_and_check(p, heads, cus);
+        } else if (t % 3 == 2) {
+            const env_guard e("CKV_DECODE_SPLIT", std::to_string(g() % 40).c_str());
+            plan_and_check(p, heads, cus);
+        } else {
+            plan_and_check(p, heads, cus);
+        }
+    }
+}

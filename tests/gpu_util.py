@@ -60,3 +60,16 @@ def approx(got, expected, eps, scale=0.0):
     a = np.asarray(got, dtype=np.float64)
     e = np.asarray(expected, dtype=np.float64)
     return bool(np.all(np.abs(a - e) <= eps * (scale + np.maximum(np.abs(a), np.abs(e)))))
+
+
+def force_plan(monkeypatch, split):
+    """Forces the fast decode's batch plan: None keeps the default, "N" cuts
+    every row into fixed chunks of N pages (CKV_DECODE_SPLIT; "0": no cut),
+    "bN" deals the batch's pages out N to a workgroup (CKV_DECODE_BALANCE), so
+    a workgroup may take several rows and row pieces."""
+    if split is None:
+        return
+    if split.startswith("b"):
+        monkeypatch.setenv("CKV_DECODE_BALANCE", split[1:])
+    else:
+        monkeypatch.setenv("CKV_DECODE_SPLIT", split)

@@ -16,7 +16,8 @@ import torch
 
 from chibillm_amd import ckv
 from oracle import oracle as orc
-from tests.gpu_util import assert_close, new_context, new_pool, to_dev, to_f32, to_host
+from tests.gpu_util import (assert_close, force_plan, new_context, new_pool, to_dev, to_f32,
+                            to_host)
 
 pytestmark = pytest.mark.gpu
 
@@ -165,14 +166,13 @@ def test_gated_prefill_tiles(ctx, group):
     pool.close()
 
 
-@pytest.mark.parametrize("split", [None, "3"])
+@pytest.mark.parametrize("split", [None, "3", "b5"])
 def test_append_decode_gated_equals_fused_pair(ctx, split, monkeypatch):
     """The decode step's fused append + attention with the gate: pages bit-exact
     with ckv_append_decode, output within tolerance of the oracle; also with
-    every row cut into chunks of 3 pages (the gate applied by the chunk that
-    merges)."""
-    if split:
-        monkeypatch.setenv("CKV_DECODE_SPLIT", split)
+    every row cut into chunks of 3 pages and with the batch dealt out 5 pages
+    to a workgroup (the gate applied by the chunk that merges)."""
+    force_plan(monkeypatch, split)
     code = orc.BF16
     rng, lengths, tables, blocks = decode_case(5, batch=16)
     H, Hq = 8, 16

@@ -12,8 +12,8 @@ import torch
 from chibillm_amd import ckv
 from oracle import oracle as orc
 from tests.golden import config1
-from tests.gpu_util import (approx, assert_close, new_context, new_pool, to_dev, to_f32,
-                            to_host)
+from tests.gpu_util import (approx, assert_close, force_plan, new_context, new_pool, to_dev,
+                            to_f32, to_host)
 
 pytestmark = pytest.mark.gpu
 
@@ -291,14 +291,15 @@ def fill_by_append(pool, lengths, tables, ks, vs, layer=0, code=orc.BF16):
         pool.append(layer, to_dev(k, code), to_dev(v, code))
 
 
-@pytest.mark.parametrize("split", [None, "0", "4", "17", "64"])
+@pytest.mark.parametrize("split", [None, "0", "4", "17", "64", "b9", "b300"])
 def test_config2_bf16_decode_over_permuted_pages(ctx, split, monkeypatch):
-    """Config 2 through the fast decode kernel: the batch plan's default cut
-    (rows of up to 256 pages on 256 compute units are cut into chunks), no cut,
-    and forced chunks of 4, 17 and 64 pages; each checked against the oracle
-    and against the plan the library reports."""
-    if split is not None:
-        monkeypatch.setenv("CKV_DECODE_SPLIT", split)
+    """Config 2 through the fast decode kernel: the batch plan's default
+    (rows of up to 256 pages on 256 compute units: the batch's pages dealt out
+    evenly to the workgroups, rows cut where a workgroup's share ends), no
+    cut, forced chunks of 4, 17 and 64 pages, and 9 or 300 pages to a
+    workgroup; each checked against the oracle and against the plan the
+    library reports."""
+    force_plan(monkeypatch, split)
     lengths, tables, ks, vs, q = config2_inputs()
     pool, _, _ = new_pool(ctx, (1, 65536, 16, 8, 128), orc.BF16)
     fill_by_append(pool, lengths, tables, ks, vs)
@@ -317,8 +318,12 @@ def test_config2_bf16_decode_over_permuted_pages(ctx, split, monkeypatch):
     pages = [-(-n // 16) for n in lengths]
     if split == "0":
         assert (span, items, records) == (0, 32, 0)
+    elif split is None or split.startswith("b"):
+        # balanced: a workgroup's share is `span` pages or fewer
+        assert span == (int(split[1:]) if split else span) and span > 0
+        assert items >= 32 and records > 0, "some row must be cut"
     else:
-        assert span == (int(split) if split else span) and span > 0
+        assert span == int(split)
         assert items == sum(-(-p // span) for p in pages)
         assert records == sum(-(-p // span) for p in pages if p > span)
         assert records > 0, "some row must be cut into several chunks"

@@ -14,7 +14,8 @@ import torch
 
 from chibillm_amd import ckv
 from oracle import oracle as orc
-from tests.gpu_util import assert_close, approx, new_context, new_pool, to_dev, to_f32, to_host
+from tests.gpu_util import (assert_close, approx, force_plan, new_context, new_pool, to_dev,
+                            to_f32, to_host)
 
 pytestmark = pytest.mark.gpu
 
@@ -204,7 +205,7 @@ def decode_rows(rng, code, batch, H, Hq, bs=16, D=128):
     (orc.BF16, 2, 0, False, None), (orc.F16, 2, 0, False, None), (orc.BF16, 1, 64, False, None),
     (orc.BF16, 8, 32, False, None), (orc.BF16, 2, 0, True, None), (orc.F16, 4, 16, True, None),
     (orc.BF16, 2, 48, False, None), (orc.F32, 2, 0, True, None), (orc.BF16, 2, 0, True, "2"),
-    (orc.F16, 4, 32, False, "3")])
+    (orc.F16, 4, 32, False, "3"), (orc.BF16, 2, 0, True, "b6"), (orc.F16, 1, 64, False, "b2")])
 def test_rope_append_decode_equals_unfused_sequence(ctx, code, group, rotary, gated, split,
                                                    monkeypatch):
     """ckv_rope_append_decode (the fused decode kernel rotating queries and the
@@ -217,8 +218,9 @@ def test_rope_append_decode_equals_unfused_sequence(ctx, code, group, rotary, ga
     (the unfused form's own outputs are compared bit for bit: same kernels)."""
     print(f"rope_append_decode dtype {code} group {group} rotary {rotary} gated {gated} "
           f"split {split}", flush=True)
-    if split:  # rows cut into chunks of `split` pages (the chunk that merges applies the gate)
-        monkeypatch.setenv("CKV_DECODE_SPLIT", split)
+    # rows cut into chunks of `split` pages, or dealt out a few pages to a
+    # workgroup ("b"): the chunk that merges applies the gate
+    force_plan(monkeypatch, split)
     rng = orc.Mt64(60 + 7 * group + code + rotary + gated)
     H = 8 if group <= 2 else 2
     Hq = H * group

@@ -12,7 +12,8 @@ import torch
 
 from chibillm_amd import ckv
 from oracle import oracle as orc
-from tests.gpu_util import assert_close, new_context, new_pool, to_dev, to_f32, to_host
+from tests.gpu_util import (assert_close, force_plan, new_context, new_pool, to_dev, to_f32,
+                            to_host)
 from tests.test_gpu_parity import compact_oracle, fill_by_append
 
 pytestmark = pytest.mark.gpu
@@ -87,7 +88,7 @@ def test_long_rows_cut_into_chunks(ctx, lengths):
     outs, caches, (span, items, records) = fused_and_unfused(ctx, lengths, B, tables, ks, vs, q)
     assert span > 0 and records > 0, "a long row must be cut"
     pages = [-(-n // 16) for n in lengths]
-    assert items == sum(-(-p // span) for p in pages)
+    assert items >= sum(-(-p // span) for p in pages)
     assert torch.equal(caches[0][0].view(torch.int16), caches[1][0].view(torch.int16))
     assert torch.equal(caches[0][1].view(torch.int16), caches[1][1].view(torch.int16))
     assert torch.equal(outs[0], outs[1])
@@ -95,17 +96,40 @@ def test_long_rows_cut_into_chunks(ctx, lengths):
     assert_close(to_f32(outs[0]), expected, what=f"rows {lengths} (chunks of {span} pages)")
 
 
-@pytest.mark.parametrize("split", ["1", "2", "7"])
+@pytest.mark.parametrize("split", ["b3", "b25", "b400"])
+def test_fused_append_in_balanced_workgroups(ctx, split, monkeypatch):
+    """The fused append + decode with the batch dealt out 3, 25 or 400 pages
+    to a workgroup over 40 rows of 1-700 tokens: a workgroup attends to
+    several rows (and row pieces) in turn and appends a row's new token when
+    it reaches the row's last page. Fused equals append-then-decode bit for
+    bit (pages and outputs), and the oracle within tolerance."""
+    force_plan(monkeypatch, split)
+    print(f"fused balanced {split}", flush=True)
+    rng = np.random.default_rng(5)
+    lengths = [int(n) for n in rng.integers(1, 701, size=40)]
+    B, tables, ks, vs, q = rows_case(95, lengths)
+    outs, caches, (span, items, records) = fused_and_unfused(ctx, lengths, B, tables, ks, vs, q)
+    assert span == int(split[1:]) and items >= len(lengths)
+    assert torch.equal(caches[0][0].view(torch.int16), caches[1][0].view(torch.int16))
+    assert torch.equal(caches[0][1].view(torch.int16), caches[1][1].view(torch.int16))
+    assert torch.equal(outs[0], outs[1])
+    expected = compact_oracle((8, 128), lengths, tables, ks, vs, q, 16)
+    assert_close(to_f32(outs[0]), expected, what=f"40 rows, plan {split}")
+
+
+@pytest.mark.parametrize("split", ["1", "2", "7", "b1", "b7", "b40", "b1000"])
 def test_tiny_chunks_and_chunk_boundaries(ctx, split, monkeypatch):
     """Chunks of 1, 2 and 7 pages over rows ending on, just past and inside
     page and chunk boundaries, at every GQA group size of the fast kernel;
-    rows shorter than a chunk are not cut."""
-    monkeypatch.setenv("CKV_DECODE_SPLIT", split)
+    rows shorter than a chunk are not cut. Also the balanced plan with 1, 7,
+    40 and 1000 pages to a workgroup: workgroups that take several whole rows
+    and row pieces one after another (all rows in one workgroup at 1000)."""
+    force_plan(monkeypatch, split)
     lengths = [1, 16, 17, 32, 33, 112, 113, 127, 500, 1999]
     for group in (1, 2, 4, 8):
         H = 16 // group if group < 8 else 2
         q_heads = H * group
-        rng = orc.Mt64(70 + group + int(split))
+        rng = orc.Mt64(70 + group + int(split.lstrip("b")))
         B = sum(-(-n // 16) for n in lengths) + 3
         perm = rng.permutation(B)
         tables, at = [], 0
@@ -123,8 +147,11 @@ def test_tiny_chunks_and_chunk_boundaries(ctx, split, monkeypatch):
         pool.upload(flat, offsets, [len(t) for t in tables], [n - 1 for n in lengths])
         span, items, records = pool.decode_plan()
         pages = [-(-n // 16) for n in lengths]
-        assert span == int(split)
-        assert records == sum(-(-p // span) for p in pages if p > span)
+        if split.startswith("b"):  # balanced: whole rows and row pieces per workgroup
+            assert span == int(split[1:]) and items >= len(lengths)
+        else:
+            assert span == int(split)
+            assert records == sum(-(-p // span) for p in pages if p > span)
         out = torch.empty(len(lengths), q_heads * 128, dtype=torch.bfloat16, device="cuda")
         pool.decode(0, to_dev(q, orc.BF16), q_heads, SCALE, out)
         expected = compact_oracle((H, 128), lengths, tables, ks, vs, q, q_heads)

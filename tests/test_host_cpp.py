@@ -27,6 +27,13 @@ def test_host_layer_cpu():
     _run("host_tests", 120)
 
 
+def test_decode_planner_cpu():
+    """libckv's fast decode planner on the CPU (tests/cpp/plan_tests.cc): every
+    plan covers each row's pages once, its workgroups' entries link up, and
+    the balanced plan evens out the work."""
+    _run("plan_tests", 120)
+
+
 @pytest.mark.gpu
 def test_host_layer_gpu():
     _run("host_gpu_tests", 100)

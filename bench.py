@@ -226,8 +226,8 @@ def bench_config2(args, long_row=False):
     pool.upload(flat, offsets, pages, [n - 1 for n in lengths])
     split_pages, items, records = pool.decode_plan()
     name = "longrow" if long_row else "config2"
-    log(f"{name}: {sum(lengths)} tokens, plan: chunks of {split_pages} pages, {items} items, "
-        f"{records} records")
+    log(f"{name}: {sum(lengths)} tokens, plan: {split_pages} pages per workgroup or chunk, "
+        f"{items} row segments, {records} records")
     for _ in range(args.warmup * 10):
         pool.decode(0, q, Q_HEADS, scale, out)
     torch.cuda.synchronize()
@@ -271,8 +271,8 @@ def bench_config2(args, long_row=False):
             "workload": workload,
             "batch": batch, "kv_heads": KV_HEADS, "q_heads": Q_HEADS,
             "head_dim": HEAD_DIM, "block_size": BLOCK, "pool_pages": CONFIG2_POOL,
-            "tokens": sum(lengths), "plan": {"split_pages": split_pages, "items": items,
-                                             "records": records},
+            "tokens": sum(lengths), "plan": {"pages_per_workgroup": split_pages,
+                                             "segments": items, "records": records},
         },
         "hbm_frac": round(kv_bytes / (launch_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {

@@ -16,7 +16,8 @@ import torch
 
 from chibillm_amd import ckv
 from oracle import oracle as orc
-from tests.gpu_util import assert_close, new_context, new_pool, to_dev, to_f32, to_host
+from tests.gpu_util import (assert_close, force_plan, new_context, new_pool, to_dev, to_f32,
+                            to_host)
 
 pytestmark = pytest.mark.gpu
 
@@ -144,10 +145,15 @@ def test_batch_upload_equals_host_upload_prefill_decode_append(ctx):
     pb.close()
 
 
-def test_decode_steps_with_growing_tables_and_fused_append(ctx):
+@pytest.mark.parametrize("plan", [None, "2", "b2", "b9"])
+def test_decode_steps_with_growing_tables_and_fused_append(ctx, plan, monkeypatch):
     """A decode loop: each step appends one token per sequence (the fused
     append + decode launch), sequences cross page boundaries and take new
-    pages, one finishes and its row is reused; only table deltas are sent."""
+    pages, one finishes and its row is reused; only table deltas are sent.
+    Also with the rows cut into 2-page chunks and with the balanced plan of 2
+    and 9 pages to a workgroup (several rows and row pieces per workgroup)
+    over the device-expanded batch."""
+    force_plan(monkeypatch, plan)
     geom = (1, 128, BS, H, D)
     (pa, ka, va), (pb, kb, vb) = random_pools(ctx, geom, 2, seed=2)
     cap = 8

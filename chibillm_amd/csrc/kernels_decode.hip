@@ -870,10 +870,6 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
     return hipGetLastError();
 }
 
-} // namespace
-
-namespace {
-
 // Pages of a row at `position`, and the batch's total and longest.
 void batch_pages(const std::vector<uint32_t>& positions, uint32_t block_size, uint64_t& total,
                  uint64_t& longest)
@@ -890,9 +886,9 @@ void batch_pages(const std::vector<uint32_t>& positions, uint32_t block_size, ui
 // `n` workgroups. A segment costs split_segment_pages pages of work besides
 // its pages (its first loads and its merge wait on memory round trips), so
 // the work dealt out (balanced_work) is the pages plus that cost for every
-// segment, and workgroup k ends at ceil((k + 1) * work / n) of it. No row is cut into a
-// piece shorter than split_min_piece pages (a workgroup takes such a rest
-// with it, or ends early and leaves the row to the next one). Calls
+// segment, and workgroup k ends at ceil((k + 1) * work / n) of it. No row is
+// cut into a piece shorter than split_min_piece pages (a workgroup takes such
+// a rest with it, or ends early and leaves the row to the next one). Calls
 // emit(row, first page, end page, workgroup) in row order; returns the
 // workgroups used (at most n).
 template <class Emit>

@@ -693,6 +693,11 @@ def bench_config4(args):
         result["rope_append"] = {"avg_launch_us": round(ms / n * 1e3, 2),
                                  "bytes_per_launch": per,
                                  "achieved_gbs": round(per / (ms / n / 1e3) / 1e9, 2)}
+        # the queries' rotation in place: query rows read and written, positions
+        ms, n = kernels["rope"]
+        per = rows * (2 * Q_HEADS * HEAD_DIM * 2 + 4)
+        result["rope"] = {"avg_launch_us": round(ms / n * 1e3, 2), "bytes_per_launch": per,
+                          "achieved_gbs": round(per / (ms / n / 1e3) / 1e9, 2)}
         result["config"]["workload"] += "; keys rotated inside the append, queries by ckv_rope"
     pool.close()
     del keys, values, q, k_new, v_new, out

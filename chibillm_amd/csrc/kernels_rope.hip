@@ -118,7 +118,10 @@ __global__ __launch_bounds__(block_threads) void rope_kernel(
 // 16-bit rows with rotary == head_dim and half a head a multiple of 8: a
 // thread rotates 8 consecutive pairs, reading and writing 16 bytes of each
 // half (two 128-bit loads and stores per tensor instead of sixteen 2-byte
-// accesses).
+// accesses). A row's angles are the same for every head, so the workgroup
+// computes the (cosine, sine) of each (row, pair) its threads touch into LDS,
+// one sincosf per entry instead of one per (row, head, pair), while its
+// threads' loads are in flight.
 template <int DT, bool APPEND>
 __global__ __launch_bounds__(block_threads) void rope_kernel_x8(
     const void* in, void* out, uint32_t rows, uint32_t heads, uint32_t head_dim,
@@ -126,20 +129,41 @@ __global__ __launch_bounds__(block_threads) void rope_kernel_x8(
     const uint32_t* __restrict__ slots, uint32_t layer, const void* __restrict__ values)
 {
     using E = element<DT>;
+    extern __shared__ float2 angles[]; // (cosine, sine) per (row of the workgroup, pair)
     const uint32_t half = head_dim / 2, groups = half / 8;
     const uint32_t per_row = heads * groups;
-    const uint64_t t = (uint64_t)blockIdx.x * block_threads + threadIdx.x;
-    if (t >= (uint64_t)rows * per_row)
-        return;
+    const uint64_t total = (uint64_t)rows * per_row;
+    const uint64_t first = (uint64_t)blockIdx.x * block_threads;
+    // the rows this workgroup's items fall in: first_row .. last_row
+    const uint32_t first_row = (uint32_t)(first / per_row);
+    const uint32_t last_row = (uint32_t)((min(first + block_threads, total) - 1) / per_row);
+    const uint32_t entries = (last_row - first_row + 1) * half;
+    // this thread's item (its loads go out before the angles are computed)
+    const uint64_t t = min(first + threadIdx.x, total - 1);
     const uint32_t row = (uint32_t)(t / per_row), rest = (uint32_t)(t % per_row);
     const uint32_t head = rest / groups, p0 = (rest % groups) * 8;
     const uint64_t width = (uint64_t)heads * head_dim;
     const uint64_t src = row * width + head * head_dim + p0;
     const uint4 a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(in) + src);
     const uint4 b = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(in) + src + half);
+    uint4 va = make_uint4(0, 0, 0, 0), vb = va;
+    if constexpr (APPEND) {
+        const uint16_t* vs = static_cast<const uint16_t*>(values) + src;
+        va = *reinterpret_cast<const uint4*>(vs);
+        vb = *reinterpret_cast<const uint4*>(vs + half);
+    }
+    for (uint32_t e = threadIdx.x; e < entries; e += block_threads) {
+        const uint32_t r = first_row + e / half, pair = e % half;
+        float sine, cosine;
+        sincosf(static_cast<float>(positions[r]) * freq.inv_freq[pair], &sine, &cosine);
+        angles[e] = make_float2(cosine, sine);
+    }
+    __syncthreads();
+    if (first + threadIdx.x >= total)
+        return;
+    const float2* cs = angles + (row - first_row) * half + p0;
     const uint32_t wa[4] = { a.x, a.y, a.z, a.w }, wb[4] = { b.x, b.y, b.z, b.w };
     uint32_t ra[4], rb[4];
-    const float pos = static_cast<float>(positions[row]);
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
         uint32_t oa = 0, ob = 0;
@@ -147,10 +171,9 @@ __global__ __launch_bounds__(block_threads) void rope_kernel_x8(
         for (int h = 0; h < 2; ++h) {
             const float x1 = E::load(static_cast<uint16_t>(wa[d] >> (16 * h)));
             const float x2 = E::load(static_cast<uint16_t>(wb[d] >> (16 * h)));
-            float sine, cosine;
-            sincosf(pos * freq.inv_freq[p0 + 2 * d + h], &sine, &cosine);
+            const float2 c = cs[2 * d + h];
             float r1, r2;
-            rope_pair(x1, x2, cosine, sine, r1, r2);
+            rope_pair(x1, x2, c.x, c.y, r1, r2);
             oa |= static_cast<uint32_t>(E::store(r1)) << (16 * h);
             ob |= static_cast<uint32_t>(E::store(r2)) << (16 * h);
         }
@@ -162,10 +185,9 @@ __global__ __launch_bounds__(block_threads) void rope_kernel_x8(
         const uint64_t off = layer * p.layer_elems + (uint64_t)slots[row] * p.features
             + head * head_dim + p0;
         dst = static_cast<uint16_t*>(p.keys) + off;
-        const uint16_t* vs = static_cast<const uint16_t*>(values) + src;
         uint16_t* vd = static_cast<uint16_t*>(p.values) + off;
-        *reinterpret_cast<uint4*>(vd) = *reinterpret_cast<const uint4*>(vs);
-        *reinterpret_cast<uint4*>(vd + half) = *reinterpret_cast<const uint4*>(vs + half);
+        *reinterpret_cast<uint4*>(vd) = va;
+        *reinterpret_cast<uint4*>(vd + half) = vb;
     } else {
         dst = static_cast<uint16_t*>(out) + src;
     }
@@ -190,13 +212,20 @@ hipError_t launch(hipStream_t s, int dtype, const void* in, void* out, uint32_t 
         && aligned16(in) && (APPEND ? aligned16(values) && aligned16(p.keys) && aligned16(p.values)
                                     : aligned16(out));
     if (x8) {
-        const uint64_t total = (uint64_t)rows * heads * (head_dim / 16);
-        const dim3 grid((uint32_t)((total + block_threads - 1) / block_threads));
+        const uint32_t per_row = heads * (head_dim / 16);
+        const uint64_t total = (uint64_t)rows * per_row;
+        const uint64_t blocks = (total + block_threads - 1) / block_threads;
+        if (blocks > 0x7FFFFFFFull)
+            return hipErrorInvalidValue;
+        const dim3 grid((uint32_t)blocks);
+        // the angle table: the rows a workgroup's items fall in, half a head each
+        const uint32_t table_rows = std::min<uint32_t>(rows, (block_threads - 1) / per_row + 2);
+        const size_t lds = (size_t)table_rows * (head_dim / 2) * sizeof(float2);
         if (dtype == CKV_BF16)
-            rope_kernel_x8<CKV_BF16, APPEND><<<grid, block_threads, 0, s>>>(
+            rope_kernel_x8<CKV_BF16, APPEND><<<grid, block_threads, lds, s>>>(
                 in, out, rows, heads, head_dim, freq, positions, p, slots, layer, values);
         else
-            rope_kernel_x8<CKV_F16, APPEND><<<grid, block_threads, 0, s>>>(
+            rope_kernel_x8<CKV_F16, APPEND><<<grid, block_threads, lds, s>>>(
                 in, out, rows, heads, head_dim, freq, positions, p, slots, layer, values);
         return hipGetLastError();
     }

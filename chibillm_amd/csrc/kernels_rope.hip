@@ -265,6 +265,40 @@ __global__ __launch_bounds__(block_threads) void sigmoid_mul_kernel(const void* 
     }
 }
 
+// The same with 16 bytes of each tensor per thread and step (8 16-bit or 4
+// f32 elements, the same arithmetic per element), the last n % per elements
+// one at a time; gate, in and out 16-byte aligned.
+template <int DT>
+__global__ __launch_bounds__(block_threads) void sigmoid_mul_x16_kernel(const void* gate,
+                                                                       const void* in, void* out,
+                                                                       uint64_t n)
+{
+    using E = element<DT>;
+    using T = typename E::type;
+    constexpr uint32_t per = 16 / sizeof(T);
+    const uint64_t stride = (uint64_t)gridDim.x * block_threads;
+    const uint64_t vecs = n / per;
+    union lanes {
+        uint4 v;
+        T e[per];
+    };
+    for (uint64_t i = (uint64_t)blockIdx.x * block_threads + threadIdx.x; i < vecs; i += stride) {
+        lanes g, x, o;
+        g.v = static_cast<const uint4*>(gate)[i];
+        x.v = static_cast<const uint4*>(in)[i];
+#pragma unroll
+        for (uint32_t e = 0; e < per; ++e)
+            o.e[e] = E::store(1.0f / (1.0f + __expf(-E::load(g.e[e]))) * E::load(x.e[e]));
+        static_cast<uint4*>(out)[i] = o.v;
+    }
+    for (uint64_t i = vecs * per + (uint64_t)blockIdx.x * block_threads + threadIdx.x; i < n;
+         i += stride) {
+        const float gv = E::load(static_cast<const T*>(gate)[i]);
+        const float xv = E::load(static_cast<const T*>(in)[i]);
+        static_cast<T*>(out)[i] = E::store(1.0f / (1.0f + __expf(-gv)) * xv);
+    }
+}
+
 } // namespace
 
 hipError_t launch_sigmoid_mul(hipStream_t s, int dtype, const void* gate, const void* in,
@@ -272,17 +306,28 @@ hipError_t launch_sigmoid_mul(hipStream_t s, int dtype, const void* gate, const 
 {
     if (!n)
         return hipSuccess;
-    const uint64_t want = (n + block_threads - 1) / block_threads;
-    const dim3 grid((uint32_t)std::min<uint64_t>(want, 65536));
+    const bool x16 = aligned16(gate) && aligned16(in) && aligned16(out);
+    const uint64_t per = x16 ? (dtype == CKV_F32 ? 4 : 8) : 1;
+    const uint64_t want = (n / per + block_threads - 1) / block_threads;
+    const dim3 grid((uint32_t)std::clamp<uint64_t>(want, 1, 65536));
     switch (dtype) {
     case CKV_F32:
-        sigmoid_mul_kernel<CKV_F32><<<grid, block_threads, 0, s>>>(gate, in, out, n);
+        if (x16)
+            sigmoid_mul_x16_kernel<CKV_F32><<<grid, block_threads, 0, s>>>(gate, in, out, n);
+        else
+            sigmoid_mul_kernel<CKV_F32><<<grid, block_threads, 0, s>>>(gate, in, out, n);
         break;
     case CKV_BF16:
-        sigmoid_mul_kernel<CKV_BF16><<<grid, block_threads, 0, s>>>(gate, in, out, n);
+        if (x16)
+            sigmoid_mul_x16_kernel<CKV_BF16><<<grid, block_threads, 0, s>>>(gate, in, out, n);
+        else
+            sigmoid_mul_kernel<CKV_BF16><<<grid, block_threads, 0, s>>>(gate, in, out, n);
         break;
     default:
-        sigmoid_mul_kernel<CKV_F16><<<grid, block_threads, 0, s>>>(gate, in, out, n);
+        if (x16)
+            sigmoid_mul_x16_kernel<CKV_F16><<<grid, block_threads, 0, s>>>(gate, in, out, n);
+        else
+            sigmoid_mul_kernel<CKV_F16><<<grid, block_threads, 0, s>>>(gate, in, out, n);
         break;
     }
     return hipGetLastError();

@@ -57,13 +57,26 @@ def test_sigmoid_mul_known_answer_and_oracle(ctx):
     assert np.allclose(got, expected, rtol=1e-5, atol=0)
     assert got[4] == 0.0 and got[5] == 6.0
     rng = orc.Mt64(3)
+    # 16-byte vectors (n a multiple of 8), a scalar tail (n % 8 == 3), and views one
+    # element off 16-byte alignment (the per-element kernel)
     for code in (orc.BF16, orc.F16):
-        g = orc.from_f32(4 * orc.to_f32(rng.normal(5000, code), code), code)
-        x = rng.normal(5000, code)
-        out = torch.empty_like(to_dev(x, code))
-        ctx.sigmoid_mul(to_dev(g, code), to_dev(x, code), out)
+        for n, off in ((5000, 0), (5003, 0), (4999, 1)):
+            g = orc.from_f32(4 * orc.to_f32(rng.normal(n + off, code), code), code)
+            x = rng.normal(n + off, code)
+            out = torch.empty_like(to_dev(x, code))[off:]
+            ctx.sigmoid_mul(to_dev(g, code)[off:], to_dev(x, code)[off:], out)
+            ctx.sync()
+            got = to_host(out, code)
+            assert ulps(got, orc.sigmoid_mul(g[off:], x[off:], code)).max() <= 1, (code, n, off)
+    for n, off in ((4003, 0), (4001, 1)):  # f32: 4 a vector, and unaligned
+        g = 4 * rng.normal(n + off, orc.F32).astype(np.float32)
+        x = rng.normal(n + off, orc.F32).astype(np.float32)
+        gd, xd = torch.from_numpy(g).cuda()[off:], torch.from_numpy(x).cuda()[off:]
+        out = torch.empty_like(xd)
+        ctx.sigmoid_mul(gd, xd, out)
         ctx.sync()
-        assert ulps(to_host(out, code), orc.sigmoid_mul(g, x, code)).max() <= 1
+        ref = x[off:] / (1 + np.exp(-g[off:].astype(np.float64)))
+        assert np.allclose(out.cpu().numpy(), ref, rtol=4e-6, atol=1e-30), (n, off)
     with pytest.raises(ckv.CkvError) as e:
         ctx.sigmoid_mul(gate, query, query, dtype=7)
     assert e.value.name == "tensor_op.unsupported_dtype"

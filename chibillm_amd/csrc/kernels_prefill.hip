@@ -429,10 +429,11 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
                 o[mt] = mfma<F16>(va[mt][h], pt[h], o[mt]);
     };
     // causal mask and maxima of S(kb); moves it to sp; true when some lane's
-    // maximum grew past the rescale threshold (m = -inf before block 0)
-    auto stats = [&](uint32_t kb) {
+    // maximum grew past the rescale threshold (m = -inf before block 0).
+    // `clear`: block kb is known to end before the q-block's first position.
+    auto stats = [&](uint32_t kb, bool clear) {
         const uint32_t key0 = kb * block_keys;
-        if (key0 + block_keys - 1 > pos_lo) { // the causal diagonal crosses this block
+        if (!clear && key0 + block_keys - 1 > pos_lo) { // the diagonal crosses this block
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t kpos = key0 + 16 * (r >> 3) + 8 * g + (r & 7);
@@ -478,7 +479,7 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
         uint4 ka[8];
         read_k(0, ka);
         qk(ka);
-        stats(0);
+        stats(0, false);
         rescale();
     }
     // Iteration kb finishes block kb - 1 and scores block kb. The steady
@@ -488,6 +489,12 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
     // fetches and waits take no checks, and the barrier's place is fixed (ODD).
     // Cutting the per-block scalar work this way (with the 32-bit page
     // offsets) made config 4's prefill 4.6 % faster.
+    // A steady iteration's blocks end at least 129 positions before the tile's
+    // last one ((kb + 2) * 32 <= (n_blocks - 5) * 32 <= pos_last - 128), so
+    // with tiles of at most 128 rows (G >= 2) they end before the tile's first
+    // position and need no mask: the scores' maxima then follow P.V in the
+    // same basic block (1.2 % faster on config 4).
+    constexpr bool steady_clear = G >= 2;
     auto iteration = [&](uint32_t kb, auto steady, auto odd) {
         constexpr bool STEADY = decltype(steady)::value;
         if constexpr (STEADY)
@@ -503,7 +510,7 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
         qk(ka);            // matrix: block kb
         read_v(kb - 1, va);
         pv(va, pt);                  // matrix: block kb - 1
-        const bool grew = stats(kb); // vector: block kb
+        const bool grew = stats(kb, STEADY && steady_clear); // vector: block kb
         if (STEADY ? decltype(odd)::value : (kb & 1) != 0) {
             // this wave's loads of blocks kb + 1, kb + 2 (in the steady state
             // those of kb + 3 and kb + 4 stay in flight)

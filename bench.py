@@ -901,6 +901,125 @@ def bench_config5(args):
     return result
 
 
+CEILING_POOL = 65536  # pages of 16 tokens x 2 KiB per tensor: 2 GiB each for K and V
+CEILING_PAGES_PER_ROW = 288  # config 3's mean row: 4,600 tokens
+
+
+def bench_ceiling(args):
+    """What the part itself allows, measured by libckv_probes.so: one pass over an
+    8 GiB buffer with plain and with nontemporal 16-byte loads; the decode's page
+    pattern without its arithmetic (a seeded permutation of a 65,536-page K and V
+    pool read as config 3's rows, one workgroup per 288 pages and kv head reading
+    that head's 256 bytes of every token row, or one per 36 pages reading whole
+    2 KiB rows, and the same over pages in pool order; 8, 10 or 16 waves, one,
+    two or any number of workgroups per compute unit); and
+    back-to-back bf16 32x32x16 products, one 8-wave workgroup per compute unit.
+    Each figure is the best of its settings, timed with one event pair around
+    `reps` launches after two untimed ones."""
+    import torch
+
+    from chibillm_amd import probes
+
+    device = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    handle = stream.cuda_stream
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(4, dtype=torch.int32, device=device)
+
+    def timed(launch, reps):
+        for _ in range(2):
+            launch()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            launch()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / reps / 1e3  # seconds per launch
+
+    # streaming reads
+    buf = torch.empty(8 << 30, dtype=torch.uint8, device=device)
+    reads = {}
+    for nt in (False, True):
+        for per_cu in (8, 16, 32, 64):
+            grid = cus * per_cu
+            s = timed(lambda: probes.read(buf, nt, grid, sink, handle), 10)
+            reads[f"{'nontemporal' if nt else 'plain'}_grid{grid}"] = round(buf.numel() / s / 1e9, 1)
+    del buf
+    torch.cuda.empty_cache()
+    best_plain = max(v for k, v in reads.items() if k.startswith("plain"))
+    best_nt = max(v for k, v in reads.items() if k.startswith("nontemporal"))
+    log(f"streaming reads GB/s: {reads}")
+
+    # the decode's page pattern
+    page_bytes = BLOCK * KV_HEADS * HEAD_DIM * 2
+    row_bytes = KV_HEADS * HEAD_DIM * 2
+    keys = torch.empty(CEILING_POOL * page_bytes, dtype=torch.uint8, device=device)
+    values = torch.empty_like(keys)
+    gen = np.random.default_rng(args.seed)
+    permuted = torch.from_numpy(gen.permutation(CEILING_POOL).astype(np.int32)).to(device)
+    ordered = torch.arange(CEILING_POOL, dtype=torch.int32, device=device)
+    patterns = {}
+    for order, plist in (("permuted", permuted), ("pool_order", ordered)):
+        for name, slice_bytes, per_wg in (("head_slice", HEAD_DIM * 2, CEILING_PAGES_PER_ROW),
+                                          ("whole_rows", row_bytes,
+                                           CEILING_PAGES_PER_ROW // KV_HEADS)):
+            best = (0.0, None)
+            # waves per workgroup x workgroups per compute unit (an LDS reservation caps
+            # them; 0: as many as the registers allow)
+            for waves in (8, 10, 16):
+                for per_cu in (1, 2, 0):
+                    lds = 160 * 1024 // per_cu - 1024 if per_cu else 0
+                    s = timed(lambda: probes.pages(keys, values, CEILING_POOL, plist, page_bytes,
+                                                   row_bytes, slice_bytes, per_wg, waves, lds,
+                                                   sink, handle), 20)
+                    gbs = round(2 * CEILING_POOL * page_bytes / s / 1e9, 1)
+                    if gbs > best[0]:
+                        best = (gbs, f"{waves} waves, {per_cu or 'any'} per CU")
+            patterns[f"{order}_{name}"] = {"gbs": best[0], "best_setting": best[1]}
+    del keys, values
+    torch.cuda.empty_cache()
+    log(f"page pattern GB/s: {patterns}")
+
+    # matrix cores
+    mfma = {}
+    iters = 20000
+    for chains in (1, 2, 4):
+        s = timed(lambda: probes.mfma(iters, chains, 8, cus, sink, handle), 3)
+        flops = cus * 8 * chains * iters * 32 * 32 * 16 * 2
+        mfma[f"chains{chains}"] = round(flops / s / 1e12, 1)
+    log(f"bf16 MFMA TFLOP/s: {mfma}")
+
+    return {
+        "metric": "hardware ceilings: HBM read GB/s (best streaming pass), page-pattern reads, "
+                  "bf16 MFMA TFLOP/s",
+        "value": best_nt,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": 10,
+        "warmup": 2,
+        "ms_per_step": round((8 << 30) / best_nt / 1e6, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "uninitialised device buffers (only the loads are measured)",
+        "config": {"workload": "ceiling: streaming reads of 8 GiB, the decode's page pattern "
+                               "over a 65,536-page pool, back-to-back bf16 MFMA",
+                   "compute_units": cus},
+        "roofline": {"kernel": "probe_read_kernel (nontemporal)", "bound": "hbm",
+                     "achieved": best_nt, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(best_nt / HBM_PEAK_GBS, 4), "traffic": None},
+        "streaming_read_gbs": reads,
+        "best_plain_read_gbs": best_plain,
+        "page_pattern_gbs": patterns,
+        "mfma_bf16_tflops": mfma,
+        "mfma_frac_of_2500": round(max(mfma.values()) / 2500.0, 4),
+        "cpu_baseline": None,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -915,14 +1034,15 @@ def main():
     ap.add_argument("--no-fuse", action="store_true",
                     help="append and decode as two launches instead of ckv_append_decode")
     ap.add_argument("--workload",
-                    choices=["config2", "config3", "config4", "config5", "spill", "longrow"],
+                    choices=["config2", "config3", "config4", "config5", "spill", "longrow", "ceiling"],
                     default="config3",
                     help="config3 (default): the headline decode step; config2: one layer of "
                          "decode attention, batch 32 (a step is one launch, default 2000 "
                          "steps); longrow: the same over one 32,768-token row; config4: chunked "
                          "prefill of 64 sequences over a shared prefix (MFMA tiles); config5: "
                          "the continuous-batching churn trace (C++ scheduler driver); spill: "
-                         "a cached prefix exported to host memory and imported back")
+                         "a cached prefix exported to host memory and imported back; ceiling: the "
+                         "part's own streaming-read, page-pattern and MFMA rates (probes)")
     ap.add_argument("--gate", action="store_true",
                     help="config3: the Qwen3.5 sigmoid gate applied in the decode epilogue "
                          "(ckv_append_decode_gated)")
@@ -951,6 +1071,8 @@ def main():
         result = bench_config5(args)
     elif args.workload == "spill":
         result = bench_spill(args)
+    elif args.workload == "ceiling":
+        result = bench_ceiling(args)
     else:
         result = bench_config3(args)
     print(json.dumps(result), flush=True)

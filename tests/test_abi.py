@@ -67,3 +67,29 @@ def test_header_compiles_as_c_and_cxx():
                             "-x", "c" if compiler == "gcc" else "c++", "-"], input=src, text=True,
                            capture_output=True)
         assert r.returncode == 0, r.stderr
+
+
+def test_probe_library_loads_and_rejects_bad_geometry():
+    """libckv_probes.so (bench.py --workload ceiling) exports its three probes and
+    refuses, before any launch, what its kernels do not cover."""
+    import ctypes as C
+
+    from chibillm_amd import probes
+
+    lib = probes.load()
+    invalid = 1  # hipErrorInvalidValue
+    buf = C.c_void_p(256)  # never dereferenced: every call below fails its checks
+    assert lib.ckv_probe_read(None, 16, 1, 1, buf, None) == invalid
+    assert lib.ckv_probe_read(C.c_void_p(264), 16, 1, 1, buf, None) == invalid  # unaligned
+    assert lib.ckv_probe_read(buf, 17, 1, 1, buf, None) == invalid  # not whole 16-byte loads
+    assert lib.ckv_probe_read(buf, 16, 1, 0, buf, None) == invalid  # empty grid
+    # slice of 96 bytes does not divide a 2 KiB row; 16 rows x 8 chunks is not a multiple of 256
+    args = [buf, buf, 64, buf, 64, 32768, 2048]
+    assert lib.ckv_probe_pages(*args, 96, 8, 10, 0, buf, None) == invalid
+    assert lib.ckv_probe_pages(*args, 128, 8, 10, 0, buf, None) == invalid
+    assert lib.ckv_probe_pages(*args, 256, 8, 17, 0, buf, None) == invalid  # 17 waves
+    assert lib.ckv_probe_pages(*args, 256, 8, 10, 160 * 1024 + 1, buf, None) == invalid
+    assert lib.ckv_probe_pages(buf, buf, 0, buf, 64, 32768, 2048, 256, 8, 10, 0, buf,
+                               None) == invalid
+    assert lib.ckv_probe_mfma(10, 3, 8, 1, buf, None) == invalid  # chains 1, 2 or 4
+    assert lib.ckv_probe_mfma(10, 1, 0, 1, buf, None) == invalid

@@ -249,6 +249,30 @@ bool all_distinct(ckv_pool* pool, const uint32_t* keys, size_t n, size_t bound)
     return true;
 }
 
+// Query tiles heaviest first, ties in their order: the prefill's workgroups
+// start in tile order as compute units free up, so the launch's last round
+// holds the lightest tiles. A tile of n rows from position p attends
+// n (p + 1) + n (n - 1) / 2 keys.
+void heaviest_first(std::vector<uint32_t>& tiles)
+{
+    const size_t n = tiles.size() / tile_entry_words;
+    if (n < 2)
+        return;
+    std::vector<std::pair<uint64_t, uint32_t>> work(n);
+    for (size_t t = 0; t < n; ++t) {
+        const uint64_t rows = tiles[tile_entry_words * t + 1];
+        const uint64_t first = tiles[tile_entry_words * t + 2];
+        work[t] = { rows * (first + 1) + rows * (rows - 1) / 2, (uint32_t)t };
+    }
+    std::stable_sort(work.begin(), work.end(),
+                     [](const auto& a, const auto& b) { return a.first > b.first; });
+    std::vector<uint32_t> sorted(tiles.size());
+    for (size_t t = 0; t < n; ++t)
+        std::copy_n(tiles.begin() + tile_entry_words * work[t].second, tile_entry_words,
+                    sorted.begin() + tile_entry_words * t);
+    tiles.swap(sorted);
+}
+
 // Words of the fast decode plan in the metadata block: the segments'
 // entries, each row's first partial record, then the cut rows.
 size_t plan_words(const decode_plan_shape& shape, size_t rows)
@@ -1102,6 +1126,7 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
         shared = shared || n > 1;
         r += n;
     }
+    heaviest_first(tiles);
 
     // append + decode can run as one launch when every row appends the token at
     // its own position and no two rows attend through the same table range
@@ -1342,6 +1367,7 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
         first_row += span;
         i = end;
     }
+    heaviest_first(tiles);
     // one decode row per sequence at its own position's slot: fusable
     bool fusable = with_slots != 0 && rows == n_items; // every item a single row
     fusable = fusable && all_distinct(pool, seq, n_items, pool->seq_max);

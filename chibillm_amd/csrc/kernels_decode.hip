@@ -691,6 +691,15 @@ constexpr uint64_t split_per_share = 4;
 constexpr uint64_t split_segment_pages = 4;
 constexpr uint64_t split_max_chunks = 32;
 constexpr uint32_t split_waves = 8;
+// Pages (about 12 us of one workgroup's reads) by which the longest row may
+// exceed 9/8 of a compute unit's share and still stay whole. Measured on one
+// MI355X layer (fused, bf16, 8 kv heads) against cutting: 32 rows of
+// U[512, 1536] tokens -15 %, U[768, 1280] -9 %, 1,024 tokens -7 %, 2,048 -6 %,
+// 64 rows of U[64, 2048] -5 %, 48 rows of U[256, 4096] -3.5 %; config 2's 32
+// rows of U[256, 4096] (longest 256 pages, share 144) still cut, as do batches
+// of fewer (row, kv head) units than compute units (8 rows of 1,024 tokens
+// whole: +36 %).
+constexpr uint64_t split_uncut_slack = 47;
 
 // One wave per (work item, kv_head); the group's q heads are processed one
 // after another, each with the per-token online softmax of
@@ -1010,7 +1019,13 @@ decode_plan_shape shape_decode_plan(const std::vector<uint32_t>& positions, uint
         // a compute unit's share of the batch, in (page, kv head) units
         const uint64_t cus = (uint64_t)std::max(cu_count, 1);
         const uint64_t share = total * kv_heads / cus;
-        if (2 * longest > share) {
+        // Rows stay whole when they give every compute unit a (row, kv head)
+        // unit and the longest is within split_uncut_slack of the share: a
+        // cut costs its merge and second segment, about 12 us, and the cut
+        // plan's pages run about 12 % slower than a whole row's.
+        const bool fill = (uint64_t)rows * kv_heads >= cus;
+        if (2 * longest > share
+            && (!fill || longest > share + share / 8 + split_uncut_slack)) {
             // as many workgroups as the GPU holds at once, but no more than a
             // row each where rows are short (pieces of at least
             // split_min_pages), nor more than split_max_chunks to a row

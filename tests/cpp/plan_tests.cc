@@ -159,18 +159,37 @@ TEST("config-2 batch: balanced, every workgroup within a few pages of its share"
         CHECK(segs.size() <= 3);
 }
 
-TEST("uniform rows: balanced pieces of one row each")
+TEST("uniform rows: whole rows when they fill the GPU, balanced pieces when they do not")
 {
     for (uint32_t tokens : { 1024u, 4096u, 16384u }) {
-        const std::vector<uint32_t> p(32, tokens - 1);
-        const auto v = plan_and_check(p, 8, 256);
+        // 32 rows x 8 kv heads = one (row, kv head) unit per compute unit
+        const auto v = plan_and_check(std::vector<uint32_t>(32, tokens - 1), 8, 256);
+        CHECK(!v.shape.balanced && v.shape.split_pages == 0 && v.shape.n_items == 32);
+    }
+    for (uint32_t tokens : { 4096u, 16384u }) {
+        // 16 rows leave half the compute units without a unit: each row in 4 pieces
+        const auto v = plan_and_check(std::vector<uint32_t>(16, tokens - 1), 8, 256);
         CHECK(v.shape.balanced);
-        CHECK(v.shape.n_wgs == 64);
+        CHECK(v.shape.n_wgs == 64); // two 8-wave workgroups per compute unit, 8 kv heads
         for (size_t w = 0; w < v.wg_pages.size(); ++w) {
             CHECK(v.wg_segments[w].size() == 1);
-            CHECK(v.wg_pages[w] == pages_of(tokens - 1) / 2);
+            CHECK(v.wg_pages[w] == pages_of(tokens - 1) / 4);
         }
     }
+}
+
+TEST("rows near the share stay whole, far longer ones are cut")
+{
+    // 32 rows of U[512, 1536] tokens: longest 96 pages against a share of about 64
+    std::mt19937_64 g(3);
+    auto p = uniform_rows(g, 32, 512, 1536);
+    p[0] = 1535;
+    auto v = plan_and_check(p, 8, 256);
+    CHECK(v.shape.split_pages == 0 && v.shape.n_items == 32);
+    // one row of 5,000 tokens among them exceeds 9/8 of the share by more than 47 pages
+    p[0] = 4999;
+    v = plan_and_check(p, 8, 256);
+    CHECK(v.shape.n_records > 0);
 }
 
 TEST("short rows, small batches and many rows keep the fixed plan")
@@ -178,9 +197,12 @@ TEST("short rows, small batches and many rows keep the fixed plan")
     // one page per row: a row per workgroup
     auto v = plan_and_check(std::vector<uint32_t>(32, 15), 8, 256);
     CHECK(!v.shape.balanced && v.shape.split_pages == 0 && v.shape.n_wgs == 32);
-    // 16-page rows: too little work to balance; fixed chunks of 12 pages
+    // 32 rows of 16 pages fill the GPU with whole rows
     v = plan_and_check(std::vector<uint32_t>(32, 255), 8, 256);
-    CHECK(!v.shape.balanced && v.shape.split_pages == 12 && v.shape.n_items == 64);
+    CHECK(!v.shape.balanced && v.shape.split_pages == 0 && v.shape.n_items == 32);
+    // 8 of them do not, and are too little work to balance: fixed chunks of 12 pages
+    v = plan_and_check(std::vector<uint32_t>(8, 255), 8, 256);
+    CHECK(!v.shape.balanced && v.shape.split_pages == 12 && v.shape.n_items == 16);
     // 128 rows of 1K-8K tokens fill the GPU with whole rows
     std::mt19937_64 g(1);
     v = plan_and_check(uniform_rows(g, 128, 1024, 8192), 8, 256);

@@ -692,7 +692,8 @@ constexpr uint64_t split_segment_pages = 4;
 constexpr uint64_t split_max_chunks = 32;
 constexpr uint32_t split_waves = 8;
 // Pages (about 12 us of one workgroup's reads) by which the longest row may
-// exceed 9/8 of a compute unit's share and still stay whole. Measured on one
+// exceed 9/8 of a compute unit's share and still stay whole, for batches of
+// one or two (row, kv head) units per compute unit. Measured on one
 // MI355X layer (fused, bf16, 8 kv heads) against cutting: 32 rows of
 // U[512, 1536] tokens -15 %, U[768, 1280] -9 %, 1,024 tokens -7 %, 2,048 -6 %,
 // 64 rows of U[64, 2048] -5 %, 48 rows of U[256, 4096] -3.5 %; config 2's 32
@@ -1019,11 +1020,14 @@ decode_plan_shape shape_decode_plan(const std::vector<uint32_t>& positions, uint
         // a compute unit's share of the batch, in (page, kv head) units
         const uint64_t cus = (uint64_t)std::max(cu_count, 1);
         const uint64_t share = total * kv_heads / cus;
-        // Rows stay whole when they give every compute unit a (row, kv head)
-        // unit and the longest is within split_uncut_slack of the share: a
-        // cut costs its merge and second segment, about 12 us, and the cut
-        // plan's pages run about 12 % slower than a whole row's.
-        const bool fill = (uint64_t)rows * kv_heads >= cus;
+        // Rows stay whole when they give every compute unit one or two (row,
+        // kv head) units and the longest is within split_uncut_slack of the
+        // share: a cut costs its merge and second segment, about 12 us, and
+        // the cut plan's pages run about 12 % slower than a whole row's. With
+        // more units per compute unit the fixed chunks balance better (the
+        // config-5 churn's batches of hundreds of rows: 1.5 % faster cut).
+        const uint64_t units = (uint64_t)rows * kv_heads;
+        const bool fill = units >= cus && units <= 2 * cus;
         if (2 * longest > share
             && (!fill || longest > share + share / 8 + split_uncut_slack)) {
             // as many workgroups as the GPU holds at once, but no more than a

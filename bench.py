@@ -33,7 +33,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
 # HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE /
-# WRITE_SIZE passes scaled by a known-size copy (chibillm_amd/rocprof_summary.py
+# WRITE_SIZE passes scaled by a known-size copy (measure/rocprof_summary.py
 # traffic writes these files from those passes)
 TRAFFIC_FILES = {
     "config3": os.path.join(ROOT, "profiles", "append_decode_config3_traffic.json"),
@@ -936,7 +936,7 @@ def bench_ceiling(args):
     `reps` launches after two untimed ones."""
     import torch
 
-    from chibillm_amd import probes
+    from measure import probes
 
     device = torch.device("cuda:0")
     stream = torch.cuda.current_stream()

@@ -3,6 +3,7 @@
   chibillm_amd/libckv.so        HIP kernels + C ABI (hipcc --offload-arch=gfx950)
   chibillm_amd/libchibillm_host.so, host tests   C++ host layer over the ABI
   oracle/liboracle.so           CPU oracle (test infrastructure only)
+  measure/libckv_probes.so      hardware-ceiling probes of bench.py (measurement only)
 """
 import os
 import subprocess
@@ -12,6 +13,7 @@ TARGETS = [
     os.path.join(ROOT, "chibillm_amd", "csrc"),
     os.path.join(ROOT, "chibillm_amd", "host"),
     os.path.join(ROOT, "oracle"),
+    os.path.join(ROOT, "measure"),
 ]
 
 

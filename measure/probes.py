@@ -1,4 +1,4 @@
-"""ctypes binding of libckv_probes.so (chibillm_amd/csrc/probes.hip): the
+"""ctypes binding of libckv_probes.so (measure/probes.hip): the
 hardware-ceiling probes that `bench.py --workload ceiling` runs. They are not
 part of the libckv boundary. Raises if the library has not been built."""
 import ctypes as C

@@ -1,9 +1,9 @@
 """Summaries of rocprofv3 CSV output (`-f csv`) for profiles/.
 
-  python -m chibillm_amd.rocprof_summary stats <prefix>_kernel_stats.csv [--top N]
+  python -m measure.rocprof_summary stats <prefix>_kernel_stats.csv [--top N]
       per-kernel calls / average / min / max in microseconds, as a markdown table
 
-  python -m chibillm_amd.rocprof_summary traffic --fetch F.csv --write W.csv \\
+  python -m measure.rocprof_summary traffic --fetch F.csv --write W.csv \\
           --kernel <symbol substring> --name <profile name> [--out traffic.json]
       HBM bytes per dispatch of one kernel from a FETCH_SIZE pass and a
       WRITE_SIZE pass (<prefix>_counter_collection.csv, values in KiB), each

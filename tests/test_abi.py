@@ -74,7 +74,7 @@ def test_probe_library_loads_and_rejects_bad_geometry():
     refuses, before any launch, what its kernels do not cover."""
     import ctypes as C
 
-    from chibillm_amd import probes
+    from measure import probes
 
     lib = probes.load()
     invalid = 1  # hipErrorInvalidValue

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from chibillm_amd import probes
+from measure import probes
 
 pytestmark = pytest.mark.gpu
 

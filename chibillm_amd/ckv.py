@@ -58,6 +58,7 @@ _SIGNATURES = [
     ("ckv_seq_tables_update", _i, [_vp, _u32p, _u32p, _u32p, _sz, _u32p, _u32p, _sz]),
     ("ckv_batch_upload", _i, [_vp, _u32p, _u32p, _u32p, _sz, _i]),
     ("ckv_decode_plan", _i, [_vp, _u32p, _u32p, _u32p]),
+    ("ckv_debug_allocations", _i, [_vp, C.POINTER(C.c_uint64)]),
     ("ckv_append", _i, [_vp, _sz, _vp, _vp, _sz]),
     ("ckv_gather", _i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp]),
     ("ckv_decode_attention", _i, [_vp, _sz, _vp, _sz, C.c_float, _vp, _sz]),
@@ -177,6 +178,13 @@ class Context:
 
     def sync(self) -> None:
         self.check(load().ckv_sync(self.handle))
+
+    def allocations(self) -> int:
+        """Device and pinned host allocations and frees the library has made on
+        this context (ckv_debug_allocations)."""
+        n = C.c_uint64()
+        self.check(load().ckv_debug_allocations(self.handle, C.byref(n)))
+        return n.value
 
     def host_alloc(self, nbytes: int) -> np.ndarray:
         """Pinned host memory (ckv_host_alloc) as a uint8 numpy array; freed by

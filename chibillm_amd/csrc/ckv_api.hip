@@ -126,6 +126,33 @@ int run_kernel(ckv_context* ctx, const char* name, Launch&& launch)
     return CKV_OK;
 }
 
+// Every device and pinned host allocation and free the library makes goes
+// through these, which count them per context (ckv_debug_allocations): the
+// no-allocation entry point is checked by that count staying put.
+hipError_t dev_malloc(ckv_context* ctx, void** ptr, size_t bytes)
+{
+    ++ctx->allocations;
+    return hipMalloc(ptr, bytes);
+}
+
+hipError_t dev_free(ckv_context* ctx, void* ptr)
+{
+    ++ctx->allocations;
+    return hipFree(ptr);
+}
+
+hipError_t host_malloc(ckv_context* ctx, void** ptr, size_t bytes)
+{
+    ++ctx->allocations;
+    return hipHostMalloc(ptr, bytes, hipHostMallocDefault);
+}
+
+hipError_t host_free(ckv_context* ctx, void* ptr)
+{
+    ++ctx->allocations;
+    return hipHostFree(ptr);
+}
+
 // Returns pinned staging memory of at least `bytes`: the ring's next slot,
 // after the copy last made from it has completed. upload_staged copies from
 // this slot and advances the ring.
@@ -140,11 +167,11 @@ int stage(ckv_context* ctx, size_t bytes, void** host)
     }
     if (bytes > slot.bytes) {
         if (slot.pinned)
-            (void)hipHostFree(slot.pinned);
+            (void)host_free(ctx, slot.pinned);
         slot.pinned = nullptr;
         slot.bytes = 0;
         const size_t size = std::max<size_t>(bytes, 1 << 20);
-        const hipError_t e = hipHostMalloc(&slot.pinned, size, hipHostMallocDefault);
+        const hipError_t e = host_malloc(ctx, &slot.pinned, size);
         if (e != hipSuccess)
             return hip_error(ctx, e, "pinned staging allocation");
         slot.bytes = size;
@@ -178,11 +205,11 @@ int ensure_device(ckv_context* ctx, T** ptr, size_t* capacity, size_t needed, co
     const size_t count = std::max({ needed, *capacity + *capacity / 2, (size_t)1024 });
     if (*ptr) {
         (void)hipStreamSynchronize(ctx->stream);
-        (void)hipFree(*ptr);
+        (void)dev_free(ctx, *ptr);
         *ptr = nullptr;
         *capacity = 0;
     }
-    const hipError_t e = hipMalloc(reinterpret_cast<void**>(ptr), count * sizeof(T));
+    const hipError_t e = dev_malloc(ctx, reinterpret_cast<void**>(ptr), count * sizeof(T));
     if (e != hipSuccess)
         return hip_error(ctx, e, what);
     *capacity = count;
@@ -247,6 +274,41 @@ bool all_distinct(ckv_pool* pool, const uint32_t* keys, size_t n, size_t bound)
         pool->stamp[keys[i]] = g;
     }
     return true;
+}
+
+// The fused append + decode writes each row's new token into its own page
+// while the batch's workgroups read their rows' pages: it keeps the semantics
+// of store_kv followed by paged_attention only if no row reads a row's own
+// page through any other table entry. own_pages_clash marks every row's own
+// page (own(r): its table index) and scans the entries each row reads
+// (entries(r): the first and one-past-last table index), reporting whether an
+// own page is reached through an index other than its own.
+template <class Own, class Entries>
+bool own_pages_clash(ckv_pool* pool, const uint32_t* table, size_t rows, Own own, Entries entries)
+{
+    if (pool->own_stamp.size() < pool->blocks) {
+        pool->own_stamp.assign(pool->blocks, 0);
+        pool->own_at.assign(pool->blocks, 0);
+    }
+    if (++pool->own_generation == 0) {
+        std::fill(pool->own_stamp.begin(), pool->own_stamp.end(), 0);
+        pool->own_generation = 1;
+    }
+    const uint32_t g = pool->own_generation;
+    for (size_t r = 0; r < rows; ++r) {
+        const uint32_t at = own(r), page = table[at];
+        if (pool->own_stamp[page] == g && pool->own_at[page] != at)
+            return true; // two rows append into one page
+        pool->own_stamp[page] = g;
+        pool->own_at[page] = at;
+    }
+    for (size_t r = 0; r < rows; ++r) {
+        const auto [first, end] = entries(r);
+        for (uint32_t i = first; i < end; ++i)
+            if (pool->own_stamp[table[i]] == g && pool->own_at[table[i]] != i)
+                return true;
+    }
+    return false;
 }
 
 // Query tiles heaviest first, ties in their order: the prefill's workgroups
@@ -357,7 +419,7 @@ int ensure_split(ckv_pool* pool, size_t q_heads, split_scratch& split)
         });
         if (status) {
             // not known to be zero: allocate and clear again next time
-            (void)hipFree(pool->d_arrivals);
+            (void)dev_free(ctx, pool->d_arrivals);
             pool->d_arrivals = nullptr;
             pool->d_arrivals_words = 0;
             return status;
@@ -647,12 +709,12 @@ int create_pool(ckv_context* ctx, size_t layers, size_t blocks, size_t block_siz
         pool->owned = false;
     } else {
         (void)hipSetDevice(ctx->device);
-        hipError_t e = hipMalloc(&pool->keys, bytes);
+        hipError_t e = dev_malloc(ctx, &pool->keys, bytes);
         if (e == hipSuccess)
-            e = hipMalloc(&pool->values, bytes);
+            e = dev_malloc(ctx, &pool->values, bytes);
         if (e != hipSuccess) {
             if (pool->keys)
-                (void)hipFree(pool->keys);
+                (void)dev_free(ctx, pool->keys);
             delete pool;
             (void)hipGetLastError();
             return set_error(ctx, CKV_E_KV_ALLOCATION_FAILED,
@@ -799,7 +861,7 @@ int ckv_context_destroy(ckv_context* ctx)
         (void)hipEventDestroy(e);
     for (auto& slot : ctx->staging) {
         if (slot.pinned)
-            (void)hipHostFree(slot.pinned);
+            (void)host_free(ctx, slot.pinned);
         (void)hipEventDestroy(slot.done);
     }
     (void)hipStreamDestroy(ctx->own_stream);
@@ -837,13 +899,21 @@ int ckv_sync(ckv_context* ctx)
     return CKV_OK;
 }
 
+int ckv_debug_allocations(const ckv_context* ctx, uint64_t* count)
+{
+    if (!ctx || !count)
+        return CKV_E_INVALID_ARGUMENT;
+    *count = ctx->allocations;
+    return CKV_OK;
+}
+
 int ckv_device_alloc(ckv_context* ctx, size_t bytes, void** out)
 {
     if (!ctx || !out)
         return CKV_E_INVALID_ARGUMENT;
     *out = nullptr;
     (void)hipSetDevice(ctx->device);
-    const hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+    const hipError_t e = dev_malloc(ctx, out, bytes ? bytes : 1);
     if (e != hipSuccess) {
         *out = nullptr;
         return hip_error(ctx, e, "device buffer allocation");
@@ -859,7 +929,7 @@ int ckv_device_free(ckv_context* ctx, void* ptr)
         return CKV_OK;
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (e == hipSuccess)
-        e = hipFree(ptr);
+        e = dev_free(ctx, ptr);
     if (e != hipSuccess)
         return hip_error(ctx, e, "device buffer free");
     return CKV_OK;
@@ -871,7 +941,7 @@ int ckv_host_alloc(ckv_context* ctx, size_t bytes, void** out)
         return CKV_E_INVALID_ARGUMENT;
     *out = nullptr;
     (void)hipSetDevice(ctx->device);
-    const hipError_t e = hipHostMalloc(out, bytes ? bytes : 1, hipHostMallocDefault);
+    const hipError_t e = host_malloc(ctx, out, bytes ? bytes : 1);
     if (e != hipSuccess) {
         *out = nullptr;
         return hip_error(ctx, e, "pinned host allocation");
@@ -888,7 +958,7 @@ int ckv_host_free(ckv_context* ctx, void* ptr)
     // copies to or from the buffer may still be queued
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (e == hipSuccess)
-        e = hipHostFree(ptr);
+        e = host_free(ctx, ptr);
     if (e != hipSuccess)
         return hip_error(ctx, e, "pinned host free");
     return CKV_OK;
@@ -984,29 +1054,30 @@ int ckv_pool_destroy(ckv_pool* pool)
 {
     if (!pool)
         return CKV_E_INVALID_ARGUMENT;
-    (void)hipStreamSynchronize(pool->ctx->stream);
+    ckv_context* ctx = pool->ctx;
+    (void)hipStreamSynchronize(ctx->stream);
     if (pool->owned) {
-        (void)hipFree(pool->keys);
-        (void)hipFree(pool->values);
+        (void)dev_free(ctx, pool->keys);
+        (void)dev_free(ctx, pool->values);
     }
     if (pool->d_meta)
-        (void)hipFree(pool->d_meta);
+        (void)dev_free(ctx, pool->d_meta);
     if (pool->d_partials)
-        (void)hipFree(pool->d_partials);
+        (void)dev_free(ctx, pool->d_partials);
     if (pool->d_arrivals)
-        (void)hipFree(pool->d_arrivals);
+        (void)dev_free(ctx, pool->d_arrivals);
     if (pool->d_pairs)
-        (void)hipFree(pool->d_pairs);
+        (void)dev_free(ctx, pool->d_pairs);
     if (pool->d_seq)
-        (void)hipFree(pool->d_seq);
+        (void)dev_free(ctx, pool->d_seq);
     if (pool->d_plan)
-        (void)hipFree(pool->d_plan);
+        (void)dev_free(ctx, pool->d_plan);
     if (pool->d_work)
-        (void)hipFree(pool->d_work);
+        (void)dev_free(ctx, pool->d_work);
     if (pool->d_spill)
-        (void)hipFree(pool->d_spill);
+        (void)dev_free(ctx, pool->d_spill);
     if (pool->d_rope_q)
-        (void)hipFree(pool->d_rope_q);
+        (void)dev_free(ctx, pool->d_rope_q);
     delete pool;
     return CKV_OK;
 }
@@ -1137,6 +1208,14 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
         fusable = own == slots[r];
     }
     fusable = fusable && all_distinct(pool, offsets, rows, n_entries + 1);
+    fusable = fusable
+        && !own_pages_clash(
+            pool, block_table, rows,
+            [&](size_t r) { return (uint32_t)(offsets[r] + positions[r] / bs); },
+            [&](size_t r) {
+                return std::pair<uint32_t, uint32_t> { offsets[r],
+                                                       (uint32_t)(offsets[r] + positions[r] / bs + 1) };
+            });
     // the checks passed: from here the batch's host state and device metadata
     // are replaced, so until this batch is adopted launches report no tables
     // (never the previous batch's pointers with this batch's positions)
@@ -1238,16 +1317,28 @@ int ckv_tables_patch(ckv_pool* pool, const uint32_t* idx, const uint32_t* val, s
     // moves a row's own page elsewhere, only the unfused pair keeps the
     // semantics of store_kv followed by paged_attention. The last write of
     // an index wins, as on the device.
+    // A patch that points another entry at a row's own page would have that
+    // page read while the fused append writes it: the batch then takes the
+    // unfused pair as well.
     if (pool->fusable) {
         std::unordered_map<uint32_t, uint32_t> patched;
         for (size_t i = 0; i < n; ++i)
             patched[idx[i]] = val[i];
         const size_t bs = pool->block_size;
+        std::unordered_map<uint32_t, uint32_t> own_page; // page -> its own table index
         for (size_t r = 0; r < pool->own_index.size() && pool->fusable; ++r) {
             const auto at = patched.find(pool->own_index[r]);
             if (at != patched.end())
                 pool->fusable = (uint64_t)at->second * bs + pool->positions[r] % bs
                     == pool->own_slot[r];
+            own_page[(uint32_t)(pool->own_slot[r] / bs)] = pool->own_index[r];
+        }
+        for (const auto& [index, page] : patched) {
+            if (!pool->fusable)
+                break;
+            const auto own = own_page.find(page);
+            if (own != own_page.end() && own->second != index)
+                pool->fusable = false;
         }
     }
     return CKV_OK;
@@ -1371,6 +1462,16 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
     // one decode row per sequence at its own position's slot: fusable
     bool fusable = with_slots != 0 && rows == n_items; // every item a single row
     fusable = fusable && all_distinct(pool, seq, n_items, pool->seq_max);
+    const size_t cap = pool->seq_cap;
+    fusable = fusable
+        && !own_pages_clash(
+            pool, pool->seq_host.data(), n_items,
+            [&](size_t i) { return (uint32_t)(seq[i] * cap + first_position[i] / bs); },
+            [&](size_t i) {
+                return std::pair<uint32_t, uint32_t> {
+                    (uint32_t)(seq[i] * cap), (uint32_t)(seq[i] * cap + first_position[i] / bs + 1)
+                };
+            });
     // the checks passed: from here the batch's host state and device metadata
     // are replaced, so until this batch is adopted launches report no tables
     pool->uploaded = false;
@@ -1859,7 +1960,9 @@ int ckv_append_decode_noalloc(ckv_pool* pool, size_t layer, const void* keys, co
                           "no-allocation decode: needs a bf16/fp16 pool with head_dim 128, "
                           "16-token pages, 1, 2, 4 or 8 q heads per kv head and 16-byte "
                           "aligned pools, queries and output");
-    if (!pool->plan_ready)
+    // a batch of multi-row query tiles is refused whatever ran on it before
+    // (a decode launch or ckv_decode_plan would have derived its plan)
+    if (pool->shared_tile || !pool->plan_ready)
         return fail_fixed(ctx, CKV_E_INVALID_ARGUMENT,
                           "no-allocation decode: the batch has multi-row query tiles, so its "
                           "decode plan was not uploaded with it");

@@ -156,6 +156,10 @@ struct ckv_context {
     // if that failed)
     void* noalloc_scratch = nullptr;
 
+    // device and pinned host allocations and frees made by the library on
+    // this context (ckv_debug_allocations)
+    uint64_t allocations = 0;
+
     bool profile = false;
     std::vector<ckv::pending_timing> pending;
     std::vector<hipEvent_t> spare_events;
@@ -195,6 +199,10 @@ struct ckv_pool {
     std::vector<uint64_t> sort_keys;
     std::vector<uint32_t> stamp; // distinctness checks (all_distinct)
     uint32_t stamp_generation = 0;
+    // pages the fused append writes, by page id: the generation that marked
+    // them and the table index each is written through (own_pages_clash)
+    std::vector<uint32_t> own_stamp, own_at;
+    uint32_t own_generation = 0;
 
     // device copies
     uint32_t* d_meta = nullptr;

@@ -47,6 +47,29 @@ __device__ __forceinline__ float fast_exp2(float x)
     return __builtin_amdgcn_exp2f(x);
 }
 
+// The split-K handoff between workgroups (a cut row's chunks store partial
+// records, count themselves in, and the last to arrive merges) is a protocol
+// of this target's memory system, not a release/acquire pair of the HIP
+// memory model:
+//   - records are written with relaxed agent-scope atomic stores and read
+//     with relaxed agent-scope atomic loads; on gfx950 (the GFX942 rows of
+//     LLVM's AMDGPU memory model) these are global_store/global_load with sc1,
+//     which write through and bypass any L2 line that could be stale, so
+//     every XCD sees them in memory without an L2 writeback;
+//   - each writer waits with s_waitcnt vmcnt(0) for its stores to complete
+//     (on GFX9-family parts vmcnt counts stores too) before one thread's
+//     relaxed agent-scope fetch-add counts the chunk in; the last arriver's
+//     loads are issued after that RMW returns.
+// A model-level handoff costs far more here: an agent-scope release lowers to
+// buffer_wbl2 sc1, a writeback of the XCD's L2 (a release RMW +27 % and an
+// acq_rel RMW +29 % on config 2's decode; a separate merge launch +1.3 %;
+// an acquire fence in the last arriver alone +1.5 %). The guard below keeps
+// the protocol off targets where the vmcnt wait would not cover stores
+// (GFX10+, which count them with vscnt) or where sc1 means something else.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "kernels_decode.hip's split-K handoff relies on gfx950's memory system; build for gfx950"
+#endif
+
 // Relaxed agent-scope accesses: coherent across the XCDs on their own (the
 // store writes through, the load misses any cache line that could be stale),
 // so data passed this way between workgroups needs no L2 writeback, only

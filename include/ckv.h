@@ -252,6 +252,12 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
  * A diagnostic with no counterpart in the reference, for tests and tuning. */
 int ckv_decode_plan(ckv_pool* pool, uint32_t* split_pages, uint32_t* work_items,
                     uint32_t* records);
+/* The number of device and pinned host allocations and frees (hipMalloc,
+ * hipFree, hipHostMalloc, hipHostFree) the library has made on this context:
+ * pools, their metadata and scratch buffers, staging, ckv_device_alloc and
+ * ckv_host_alloc. A diagnostic with no counterpart in the reference, for tests
+ * of ckv_append_decode_noalloc, which must leave it unchanged. */
+int ckv_debug_allocations(const ckv_context* ctx, uint64_t* count);
 
 /* ---- Ops -------------------------------------------------------------------------- */
 /* store_kv (src/tensor/tensor_ops.cc:412-463; kernel src/metal/kernels/attention.metal:3-33):
@@ -318,7 +324,8 @@ int ckv_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_he
  * a batch of single-row query tiles uploaded with ckv_tables_upload or
  * ckv_batch_upload (its plan goes up with it), and the fast decode's geometry
  * (bf16/fp16, head_dim 128, 16-token pages, 1, 2, 4 or 8 q heads per kv head,
- * 16-byte aligned pools, queries and output). Otherwise, and when the batch's
+ * 16-byte aligned pools, queries and output); a batch with a multi-row query
+ * tile is refused whatever ran on it before. Otherwise, and when the batch's
  * records exceed the array (n_records * q_heads * 528 bytes > 16 MiB - 256 KiB
  * or n_records * kv_heads * 4 bytes > 256 KiB, see ckv_decode_plan), it
  * returns invalid_argument with a reason in ckv_last_error. Every call on one

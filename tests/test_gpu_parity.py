@@ -631,6 +631,96 @@ def test_append_decode_equals_append_then_decode(ctx):
         pool.close()
 
 
+def _own_page_case():
+    """Row 0 appends position 20 into page 9 (its table [3, 9]); row 1 appends
+    position 40 into page 6 and attends positions 0..40 through [5, x, 6], so
+    with x = 9 it reads (as its positions 16..31) the page row 0 writes: such
+    a batch must take store_kv then paged_attention."""
+    rng = orc.Mt64(29)
+    F = 1024
+    k = [rng.normal(21 * F, orc.BF16).reshape(21, F), rng.normal(41 * F, orc.BF16).reshape(41, F)]
+    v = [rng.normal(21 * F, orc.BF16).reshape(21, F), rng.normal(41 * F, orc.BF16).reshape(41, F)]
+    q = rng.normal(2 * 2048, orc.BF16).reshape(2, 2048)
+    return k, v, q
+
+
+def _fused_launches(ctx, run):
+    """Runs `run` with profiling on; (fused launches, store_kv launches)."""
+    ctx.sync()
+    ctx.profile(True)
+    ctx.profile_reset()
+    run()
+    ctx.sync()
+    fused = ctx.profile_query("append_decode")[1]
+    stores = ctx.profile_query("store_kv")[1]
+    ctx.profile(False)
+    return fused, stores
+
+
+@pytest.mark.parametrize("how", ["upload", "patch", "sequence_tables"])
+def test_append_decode_unfused_when_another_row_reads_an_own_page(ctx, how):
+    """A row's own page (where the fused append writes its token) reached
+    through another row's table entry: set by ckv_tables_upload, by a later
+    ckv_tables_patch, or through sequence tables and ckv_batch_upload, the
+    batch leaves the fused path, and its outputs equal store_kv followed by
+    paged_attention bit for bit."""
+    k, v, q = _own_page_case()
+    geom = (1, 16, 16, 8, 128)
+    scale = float(np.float32(1 / math.sqrt(128)))
+    t0 = np.array([3, 9], np.uint32)
+    clash = np.array([5, 9, 6], np.uint32)
+    clean = np.array([5, 11, 6], np.uint32)
+    positions = [20, 40]
+    slots = [orc.slot(t0, 20, 16), orc.slot(clash, 40, 16)]
+    outs = []
+    for which in range(2):
+        pool, _, _ = new_pool(ctx, geom, orc.BF16)
+        fill_by_append(pool, [40], [clash], [k[1][:40]], [v[1][:40]])
+        fill_by_append(pool, [20], [t0], [k[0][:20]], [v[0][:20]])
+        k_new = to_dev(np.stack([k[0][20], k[1][40]]), orc.BF16)
+        v_new = to_dev(np.stack([v[0][20], v[1][40]]), orc.BF16)
+        out = torch.empty(2, 2048, dtype=torch.bfloat16, device="cuda")
+        if how == "sequence_tables":
+            pool.reserve_sequences(2, 4)
+            pool.update_sequences(seq=[0, 0, 1, 1, 1], index=[0, 1, 0, 1, 2],
+                                  block=[3, 9, 5, 9, 6], len_seq=[0, 1], length=[2, 3])
+            pool.upload_batch([0, 1], positions, [1, 1])
+        elif how == "upload":
+            pool.upload(np.concatenate([t0, clash]), [0, 2], [2, 3], positions, slots)
+        else:  # a clean batch, then row 1's second entry patched onto page 9
+            pool.upload(np.concatenate([t0, clean]), [0, 2], [2, 3], positions, slots)
+            pool.patch([3], [9])
+        if which == 0:
+            fused, stores = _fused_launches(ctx, lambda: pool.append_decode(
+                0, k_new, v_new, to_dev(q, orc.BF16), 16, scale, out))
+            assert fused == 0 and stores == 1, (how, fused, stores)
+        else:
+            pool.append(0, k_new, v_new)
+            pool.decode(0, to_dev(q, orc.BF16), 16, scale, out)
+        ctx.sync()
+        outs.append(out)
+        pool.close()
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_append_decode_stays_fused_without_a_shared_own_page(ctx):
+    """The same batch with row 1's second entry on a page of its own keeps the
+    fused launch."""
+    k, v, q = _own_page_case()
+    pool, _, _ = new_pool(ctx, (1, 16, 16, 8, 128), orc.BF16)
+    t0 = np.array([3, 9], np.uint32)
+    t1 = np.array([5, 11, 6], np.uint32)
+    pool.upload(np.concatenate([t0, t1]), [0, 2], [2, 3], [20, 40],
+                [orc.slot(t0, 20, 16), orc.slot(t1, 40, 16)])
+    out = torch.empty(2, 2048, dtype=torch.bfloat16, device="cuda")
+    fused, stores = _fused_launches(ctx, lambda: pool.append_decode(
+        0, to_dev(np.stack([k[0][20], k[1][40]]), orc.BF16),
+        to_dev(np.stack([v[0][20], v[1][40]]), orc.BF16), to_dev(q, orc.BF16), 16,
+        float(np.float32(1 / math.sqrt(128))), out))
+    assert fused == 1 and stores == 0
+    pool.close()
+
+
 def test_append_decode_falls_back_when_rows_share_a_sequence(ctx):
     # two rows of one sequence (positions 40 and 41) cannot be fused: the
     # second row attends to the token the first row appends

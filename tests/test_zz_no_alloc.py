@@ -118,6 +118,64 @@ def test_noalloc_back_to_back_calls_are_bit_identical(ctx):
     pool.close()
 
 
+def test_noalloc_makes_no_allocation(ctx):
+    """The library's own count of device and pinned allocations and frees
+    (ckv_debug_allocations) does not move across ckv_append_decode_noalloc
+    calls, the first of them on a pool on which no allocating decode ever ran
+    (so its partial-record and arrival-counter buffers do not exist), while
+    one ckv_append_decode on the same batch allocates them."""
+    lengths = [15000, 6000, 90]
+    B = sum(-(-n // 16) for n in lengths) + 4
+    tables, ks, vs, q = batch(404, lengths, B)
+    pool, _, _ = new_pool(ctx, (1, B, 16, 8, 128), orc.BF16)
+    fill_by_append(pool, [n - 1 for n in lengths], tables, [k[:-1] for k in ks],
+                   [v[:-1] for v in vs])
+    flat = np.concatenate(tables)
+    offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
+    positions = [n - 1 for n in lengths]
+    pool.upload(flat, offsets, [len(t) for t in tables], positions,
+                [orc.slot(t, p, 16) for t, p in zip(tables, positions)])
+    span, _, records = pool.decode_plan()
+    assert span > 0 and records > 0, "the batch must use the scratch records"
+    k_new = to_dev(np.stack([k[-1] for k in ks]), orc.BF16)
+    v_new = to_dev(np.stack([v[-1] for v in vs]), orc.BF16)
+    qd = to_dev(q, orc.BF16)
+    out = torch.empty(len(lengths), 2048, dtype=torch.bfloat16, device="cuda")
+    ctx.sync()
+    before = ctx.allocations()
+    for _ in range(3):
+        pool.append_decode_noalloc(0, k_new, v_new, qd, 16, SCALE, out)
+    ctx.sync()
+    assert ctx.allocations() == before, "ckv_append_decode_noalloc allocated"
+    first = out.clone()
+    pool.append_decode(0, k_new, v_new, qd, 16, SCALE, out)
+    ctx.sync()
+    assert ctx.allocations() > before, "the allocating decode made its scratch buffers"
+    assert torch.equal(out, first)
+    pool.close()
+
+
+def test_noalloc_refuses_a_tiled_batch_whatever_ran_before(ctx):
+    """A batch with a multi-row query tile is refused even after
+    ckv_decode_plan derived its decode plan (the refusal depends on the
+    batch, not on the calls made on it)."""
+    q = torch.zeros(4, 2048, dtype=torch.bfloat16, device="cuda")
+    kv = torch.zeros(4, 1024, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty_like(q)
+    pool, _, _ = new_pool(ctx, (1, 64, 16, 8, 128), orc.BF16)
+    pool.upload([0, 1], [0] * 4, [2] * 4, [3, 4, 5, 6], slots=[3, 4, 5, 6])
+    pool.decode_plan()
+    with pytest.raises(ckv.CkvError) as e:
+        pool.append_decode_noalloc(0, kv, kv, q, 16, SCALE, out)
+    assert e.value.name == "ckv.invalid_argument" and "query tiles" in str(e.value)
+    pool.decode(0, q, 16, SCALE, out)  # an allocating decode launch on it
+    with pytest.raises(ckv.CkvError) as e:
+        pool.append_decode_noalloc(0, kv, kv, q, 16, SCALE, out)
+    assert e.value.name == "ckv.invalid_argument" and "query tiles" in str(e.value)
+    ctx.sync()
+    pool.close()
+
+
 def test_noalloc_refuses_instead_of_allocating(ctx, monkeypatch):
     """A batch of multi-row query tiles (no decode plan uploaded), an f32 pool
     and a plan whose records exceed the 16 MiB array are refused with

@@ -1884,8 +1884,10 @@ int ckv_rope_append_decode(ckv_pool* pool, size_t layer, const void* keys, const
         return status;
     const pool_view view = view_of(pool);
     const auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-    // the fused kernel rotates in lane pairs part ^ (rotary / 16) of a 128-wide head
-    const bool lane_pairs = rotary >= 16 && rotary <= 128 && (rotary & (rotary - 1)) == 0;
+    // the fused kernel rotates 16-bit pages in lane pairs part ^ (rotary / 16)
+    // of a 128-wide head
+    const bool lane_pairs = view.dtype != CKV_F32 && rotary >= 16 && rotary <= 128
+        && (rotary & (rotary - 1)) == 0;
     if (pool->fusable && lane_pairs && decode_fast_applies(view, (uint32_t)q_heads, queries, output)
         && aligned(keys) && aligned(values) && (!gate || aligned(gate))) {
         split_scratch split {};
@@ -1957,8 +1959,8 @@ int ckv_append_decode_noalloc(ckv_pool* pool, size_t layer, const void* keys, co
     const pool_view view = view_of(pool);
     if (!decode_fast_applies(view, (uint32_t)q_heads, queries, output))
         return fail_fixed(ctx, CKV_E_INVALID_ARGUMENT,
-                          "no-allocation decode: needs a bf16/fp16 pool with head_dim 128, "
-                          "16-token pages, 1, 2, 4 or 8 q heads per kv head and 16-byte "
+                          "no-allocation decode: needs head_dim 128, 16-token pages, 1, 2, 4 "
+                          "or 8 q heads per kv head (1, 2 or 4 for f32 pools) and 16-byte "
                           "aligned pools, queries and output");
     // a batch of multi-row query tiles is refused whatever ran on it before
     // (a decode launch or ckv_decode_plan would have derived its plan)

@@ -1,22 +1,21 @@
-// Paged GQA decode attention: split-KV partials + merge.
+// Paged GQA decode attention.
 //
-// Work decomposition (built on the host at upload, reused by every layer):
-// each row's logical range 0..position is cut into chunks of m.chunk tokens
-// (a multiple of 16); one wave64 owns one (chunk, kv_head) and serves all
-// q heads of that KV head's GQA group, so every K/V byte is read once.
-// A row with a single chunk writes its output directly; otherwise each wave
-// writes (max, denominator, accumulator) and merge_kernel combines them with
-// weights 2^(m_c - M), the reduction of paged_attention_reduce_f32
+// Fast path (head_dim 128, 16-token pages, 1/2/4/8 q heads per KV head; f32
+// pages up to 4): one workgroup per (plan workgroup, kv_head) serves every q
+// head of the KV head's GQA group, so each K/V byte is read once. A wave reads
+// four token rows per load instruction, 16 lanes per row, so lane l holds
+// features 8*(l%16)..8*(l%16)+7 of token 4j + l/16 (16 bytes of a bf16/fp16
+// row, 32 of an f32 row). A score is a dot chain over the lane's 8 features
+// (v_dot2 for 16-bit pairs) followed by a 16-lane DPP all-reduce (4 VALU ops).
+// Each 16-lane row group keeps its own online-softmax state over its tokens;
+// the four states are merged once per segment. Scores are kept in the log2
+// domain (scale * log2(e)) so every exponential is one v_exp_f32. Rows the
+// batch plan cuts are merged in the same launch with weights 2^(m_c - M), the
+// reduction of paged_attention_reduce_f32
 // (src/metal/kernels/attention.metal:567-615).
 //
-// Fast path (16-bit K/V, head_dim 128, block_size % 4 == 0): the wave reads
-// four token rows per load instruction, 16 lanes x 16 bytes per 256-byte
-// row, so lane l holds features 8*(l%16).. of token 4j + l/16. A score is a
-// bf16/fp16 dot2 chain over the lane's 8 features followed by a 16-lane DPP
-// all-reduce (4 VALU ops). Each 16-lane row group keeps its own online-softmax
-// state over its tokens; the four states are merged once per chunk. Scores
-// are kept in the log2 domain (scale * log2(e)) so every exponential is one
-// v_exp_f32.
+// Generic path (any head_dim <= 1024, any page size): split-KV over token
+// chunks, one wave per (chunk, kv_head), and a merge launch.
 #include "ckv_internal.h"
 
 #include <algorithm>
@@ -40,6 +39,44 @@ __device__ __forceinline__ uint4 load_stream(const void* p)
 {
     const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
     return make_uint4(t.x, t.y, t.z, t.w);
+}
+
+// The eight consecutive elements of one K, V or query row a lane of the fast
+// decode holds: one 16-byte word for 16-bit pools, two for f32 (the
+// reference's storage, src/metal/metal_kv_cache.cc:57-69).
+template <int DT>
+struct lane8 {
+    static constexpr uint32_t words = DT == CKV_F32 ? 2 : 1;
+    static constexpr uint32_t elem = DT == CKV_F32 ? 4 : 2; // bytes per element
+    uint4 w[words];
+};
+
+template <int DT>
+__device__ __forceinline__ lane8<DT> load8_stream(const char* p)
+{
+    lane8<DT> x;
+#pragma unroll
+    for (uint32_t i = 0; i < lane8<DT>::words; ++i)
+        x.w[i] = load_stream(p + 16 * i);
+    return x;
+}
+
+template <int DT>
+__device__ __forceinline__ lane8<DT> load8(const char* p)
+{
+    lane8<DT> x;
+#pragma unroll
+    for (uint32_t i = 0; i < lane8<DT>::words; ++i)
+        x.w[i] = *reinterpret_cast<const uint4*>(p + 16 * i);
+    return x;
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(char* p, const lane8<DT>& x)
+{
+#pragma unroll
+    for (uint32_t i = 0; i < lane8<DT>::words; ++i)
+        *reinterpret_cast<uint4*>(p + 16 * i) = x.w[i];
 }
 
 __device__ __forceinline__ float fast_exp2(float x)
@@ -186,6 +223,88 @@ __host__ __device__ constexpr uint32_t record_floats(uint32_t head_dim)
     return head_dim + 4;
 }
 
+// Workgroups whose lanes need more than 128 registers (more than two q heads
+// per KV head, or f32 pages, whose double-buffered K/V words alone take 128)
+// run at most 8 waves, two per SIMD, with up to 256 registers a lane.
+__host__ __device__ constexpr bool wide_lanes(uint32_t group, int dtype)
+{
+    return group > 2 || dtype == CKV_F32;
+}
+
+// Eight q heads of f32 pages do not fit 256 registers a lane (the kernel
+// would spill): such pools take the generic kernel.
+__host__ __device__ constexpr bool fast_fits(uint32_t group, int dtype)
+{
+    return !(group == 8 && dtype == CKV_F32);
+}
+
+// q . k over a lane's eight elements (16-bit pairs by v_dot2 with fp32
+// accumulation; f32 by fused multiply-adds), and a V row widened to floats.
+template <int DT>
+__device__ __forceinline__ float dot8(const lane8<DT>& q, const lane8<DT>& k)
+{
+    if constexpr (DT == CKV_F32) {
+        float d = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < 2; ++i) {
+            d = __builtin_fmaf(__builtin_bit_cast(float, q.w[i].x), __builtin_bit_cast(float, k.w[i].x), d);
+            d = __builtin_fmaf(__builtin_bit_cast(float, q.w[i].y), __builtin_bit_cast(float, k.w[i].y), d);
+            d = __builtin_fmaf(__builtin_bit_cast(float, q.w[i].z), __builtin_bit_cast(float, k.w[i].z), d);
+            d = __builtin_fmaf(__builtin_bit_cast(float, q.w[i].w), __builtin_bit_cast(float, k.w[i].w), d);
+        }
+        return d;
+    } else {
+        using ops = half2_ops<DT == CKV_F16>;
+        float d = ops::dot2(q.w[0].x, k.w[0].x, 0.0f);
+        d = ops::dot2(q.w[0].y, k.w[0].y, d);
+        d = ops::dot2(q.w[0].z, k.w[0].z, d);
+        return ops::dot2(q.w[0].w, k.w[0].w, d);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void widen8(const lane8<DT>& v, float (&f)[8])
+{
+    if constexpr (DT == CKV_F32) {
+#pragma unroll
+        for (uint32_t i = 0; i < 2; ++i) {
+            f[4 * i + 0] = __builtin_bit_cast(float, v.w[i].x);
+            f[4 * i + 1] = __builtin_bit_cast(float, v.w[i].y);
+            f[4 * i + 2] = __builtin_bit_cast(float, v.w[i].z);
+            f[4 * i + 3] = __builtin_bit_cast(float, v.w[i].w);
+        }
+    } else {
+        using ops = half2_ops<DT == CKV_F16>;
+        const uint4 w = v.w[0];
+        f[0] = ops::lo(w.x); f[1] = ops::hi(w.x); f[2] = ops::lo(w.y); f[3] = ops::hi(w.y);
+        f[4] = ops::lo(w.z); f[5] = ops::hi(w.z); f[6] = ops::lo(w.w); f[7] = ops::hi(w.w);
+    }
+}
+
+// One element of a pool-dtype row (gate, output, generic-path operands) as
+// float, and back (one rounding, to nearest even).
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* base, uint64_t i)
+{
+    if constexpr (DT == CKV_F32)
+        return static_cast<const float*>(base)[i];
+    else if constexpr (DT == CKV_BF16)
+        return __builtin_bit_cast(float, (uint32_t)static_cast<const uint16_t*>(base)[i] << 16);
+    else
+        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(base)[i]));
+}
+
+template <int DT>
+__device__ __forceinline__ void store_elem(void* base, uint64_t i, float x)
+{
+    if constexpr (DT == CKV_F32)
+        static_cast<float*>(base)[i] = x;
+    else if constexpr (DT == CKV_BF16)
+        static_cast<uint16_t*>(base)[i] = static_cast<uint16_t>(bf16_bits(x));
+    else
+        static_cast<uint16_t*>(base)[i] = static_cast<uint16_t>(f16_bits(x));
+}
+
 // Fast path, one workgroup per (plan workgroup, kv_head), W waves. A
 // workgroup runs its plan segments one after another: each a row, or a piece
 // (a run of pages) of a row that the plan cuts (the split-K of
@@ -213,14 +332,18 @@ __host__ __device__ constexpr uint32_t record_floats(uint32_t head_dim)
 // (src/metal/kernels/tensor_ops.metal:158-195) would: feature f < rotary/2
 // pairs with f + rotary/2, which sits in the lane part ^ (rotary/16) of the
 // same 16-lane group, so one lane exchange per register rotates a head.
-template <int G, bool F16, bool FUSED, bool GATED, bool ROPE>
-__global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg_kernel(
-    pool_view p, meta_view m, uint32_t layer, const uint16_t* __restrict__ q, uint32_t q_heads,
-    float scale_log2, uint16_t* __restrict__ out, const char* __restrict__ k_in,
-    const char* __restrict__ v_in, const uint16_t* __restrict__ gate, rope_table64 freq,
+template <int G, int DT, bool FUSED, bool GATED, bool ROPE>
+__global__ __launch_bounds__(wide_lanes(G, DT) ? 512 : 1024, wide_lanes(G, DT) ? 2 : 4) void decode_wg_kernel(
+    pool_view p, meta_view m, uint32_t layer, const char* __restrict__ q, uint32_t q_heads,
+    float scale_log2, void* __restrict__ out, const char* __restrict__ k_in,
+    const char* __restrict__ v_in, const void* __restrict__ gate, rope_table64 freq,
     uint32_t rotary, split_scratch split)
 {
+    static_assert(!(ROPE && DT == CKV_F32), "the fused rotation works on 16-bit pairs");
+    constexpr bool F16 = DT == CKV_F16;
     using ops = half2_ops<F16>;
+    using row8 = lane8<DT>;
+    constexpr uint32_t ES = row8::elem;
     constexpr uint32_t D = 128;
     constexpr uint32_t BS = 16;
     extern __shared__ float lds[];
@@ -228,10 +351,10 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // a scalar
     const uint32_t H = p.kv_heads;
     const uint32_t kv_head = blockIdx.x % H;
-    const uint32_t row_bytes = p.features * 2u;
+    const uint32_t row_bytes = p.features * ES;
     const uint64_t page_bytes = (uint64_t)BS * row_bytes;
-    const char* kl = static_cast<const char*>(p.keys) + (uint64_t)layer * p.layer_elems * 2u;
-    const char* vl = static_cast<const char*>(p.values) + (uint64_t)layer * p.layer_elems * 2u;
+    const char* kl = static_cast<const char*>(p.keys) + (uint64_t)layer * p.layer_elems * ES;
+    const char* vl = static_cast<const char*>(p.values) + (uint64_t)layer * p.layer_elems * ES;
     // the layer's bases and the table are known from the arguments alone: load
     // them now, beside the plan entry, not after it
     asm volatile("" ::"s"(kl), "s"(vl), "s"(m.table), "s"(row_bytes), "s"(q));
@@ -247,7 +370,7 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
         const uint32_t tid = wave * 64 + lane;
         const uint32_t group = lane >> 4;
         const uint32_t part = lane & 15;
-        const uint32_t head_off = kv_head * (D * 2u) + part * 16u;
+        const uint32_t head_off = kv_head * (D * ES) + part * 8u * ES;
         const uint32_t row = e0.x;
         const uint32_t chunk = e0.y;
         const uint32_t position = e0.z;
@@ -256,18 +379,17 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
         const uint32_t pg_first = e1.x;
         const uint32_t pg_end = e1.y;
         const uint32_t n_chunks = e1.z;
-        uint32_t gate_early = 0; // the first epilogue iteration's gate value (one register)
+        float gate_early = 0.0f; // the first epilogue iteration's gate value (one register)
         if constexpr (GATED) {
             if (tid < G * D)
-                gate_early = gate[((uint64_t)row * q_heads + kv_head * G) * D + tid];
+                gate_early = load_elem<DT>(gate, ((uint64_t)row * q_heads + kv_head * G) * D + tid);
         }
         const uint32_t* tbl = m.table + (e0.w - pg_first); // the row's table
 
-        uint4 qv[G];
+        row8 qv[G];
 #pragma unroll
         for (int g = 0; g < G; ++g)
-            qv[g] = *reinterpret_cast<const uint4*>(
-                q + ((uint64_t)row * q_heads + kv_head * G + g) * D + part * 8);
+            qv[g] = load8<DT>(q + (((uint64_t)row * q_heads + kv_head * G + g) * D + part * 8) * ES);
 
         // ROPE: this lane's 8 features (pairs j0 .. j0 + 7) and their rotation;
         // every lane of the wave takes part in the exchanges. The queries and the
@@ -318,7 +440,7 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
         const uint64_t in_row = (uint64_t)row * row_bytes + head_off;
         uint4 k_new = make_uint4(0, 0, 0, 0); // ROPE: the new token's key, rotated once loaded
         if constexpr (ROPE)
-            k_new = *reinterpret_cast<const uint4*>(k_in + in_row);
+            k_new = load8<DT>(k_in + in_row).w[0];
 
         float mx[G], den[G], acc[G][8];
 #pragma unroll
@@ -331,7 +453,7 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
         }
 
         // rows past the row's last token re-read that token (in bounds, written)
-        auto load_page = [&](uint32_t pg, uint4* k, uint4* v) {
+        auto load_page = [&](uint32_t pg, row8* k, row8* v) {
             const uint64_t base = (uint64_t)tbl[pg] * page_bytes;
             const char* kb = kl + base;
             const char* vb = vl + base;
@@ -343,19 +465,19 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
                 const uint32_t off = r * row_bytes + head_off;
                 const bool fresh = FUSED && last_page && r == last_in_page;
                 // ROPE: the new token's slot is read too and replaced in process
-                k[j] = load_stream(fresh && !ROPE ? k_in + in_row : kb + off);
-                v[j] = load_stream(fresh ? v_in + in_row : vb + off);
+                k[j] = load8_stream<DT>(fresh && !ROPE ? k_in + in_row : kb + off);
+                v[j] = load8_stream<DT>(fresh ? v_in + in_row : vb + off);
             }
         };
 
-        auto process = [&](uint4* k, const uint4* v, uint32_t pg) {
+        auto process = [&](row8* k, const row8* v, uint32_t pg) {
             const uint32_t valid = pg == n_pages - 1 ? last_in_page + 1 : BS;
             if (FUSED && pg == n_pages - 1) {
                 if constexpr (ROPE) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         if (4u * j + group == last_in_page)
-                            k[j] = k_new;
+                            k[j].w[0] = k_new;
                 }
                 // append: the lanes holding the new token write it into its slot
                 const uint64_t base = (uint64_t)tbl[pg] * page_bytes;
@@ -363,8 +485,8 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     if (4u * j + group == last_in_page) {
-                        *reinterpret_cast<uint4*>(const_cast<char*>(kl) + base + off) = k[j];
-                        *reinterpret_cast<uint4*>(const_cast<char*>(vl) + base + off) = v[j];
+                        store8<DT>(const_cast<char*>(kl) + base + off, k[j]);
+                        store8<DT>(const_cast<char*>(vl) + base + off, v[j]);
                     }
                 }
             }
@@ -378,11 +500,7 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
                 float s[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    float d = ops::dot2(qv[g].x, k[j].x, 0.0f);
-                    d = ops::dot2(qv[g].y, k[j].y, d);
-                    d = ops::dot2(qv[g].z, k[j].z, d);
-                    d = ops::dot2(qv[g].w, k[j].w, d);
-                    const float r = row16_sum(d) * scale_log2;
+                    const float r = row16_sum(dot8<DT>(qv[g], k[j])) * scale_log2;
                     s[j] = ok[j] ? r : -INFINITY;
                 }
                 const float nm = fmaxf(mx[g], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
@@ -403,9 +521,8 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
             // token by token: widen the V row once, accumulate it into every q head
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float vf[8] = { ops::lo(v[j].x), ops::hi(v[j].x), ops::lo(v[j].y),
-                                      ops::hi(v[j].y), ops::lo(v[j].z), ops::hi(v[j].z),
-                                      ops::lo(v[j].w), ops::hi(v[j].w) };
+                float vf[8];
+                widen8<DT>(v[j], vf);
 #pragma unroll
                 for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -414,7 +531,7 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
             }
         };
 
-        uint4 ka[4], va[4], kb[4], vb[4];
+        row8 ka[4], va[4], kb[4], vb[4];
         uint32_t pg = pg_first + wave;
         if (pg < pg_end)
             load_page(pg, ka, va);
@@ -424,7 +541,7 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
             angles(rc, rs);
 #pragma unroll
             for (int g = 0; g < G; ++g)
-                qv[g] = rotate(qv[g], rc, rs);
+                qv[g].w[0] = rotate(qv[g].w[0], rc, rs);
             k_new = rotate(k_new, rc, rs);
         }
         // Issue arbitration favours older waves: with a fixed priority the
@@ -520,11 +637,9 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
         };
         auto emit = [&](uint32_t g, uint32_t f, uint32_t it, float o) {
             const uint64_t at = ((uint64_t)row * q_heads + kv_head * G + g) * D + f;
-            if constexpr (GATED) {
-                const uint16_t gb = it == 0 ? (uint16_t)gate_early : gate[at];
-                o *= sigmoid(half_value<F16>(gb));
-            }
-            out[at] = static_cast<uint16_t>(F16 ? f16_bits(o) : bf16_bits(o));
+            if constexpr (GATED)
+                o *= sigmoid(it == 0 ? gate_early : load_elem<DT>(gate, at));
+            store_elem<DT>(out, at, o);
         };
         if (n_chunks == 1) {
             uint32_t it = 0;
@@ -655,28 +770,6 @@ __global__ __launch_bounds__(G <= 2 ? 1024 : 512, G <= 2 ? 4 : 2) void decode_wg
 }
 
 // ---- generic path: any head_dim <= 1024, f32 / bf16 / fp16 ---------------------
-
-template <int DT>
-__device__ __forceinline__ float load_elem(const void* base, uint64_t i)
-{
-    if constexpr (DT == CKV_F32)
-        return static_cast<const float*>(base)[i];
-    else if constexpr (DT == CKV_BF16)
-        return __builtin_bit_cast(float, (uint32_t)static_cast<const uint16_t*>(base)[i] << 16);
-    else
-        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(base)[i]));
-}
-
-template <int DT>
-__device__ __forceinline__ void store_elem(void* base, uint64_t i, float x)
-{
-    if constexpr (DT == CKV_F32)
-        static_cast<float*>(base)[i] = x;
-    else if constexpr (DT == CKV_BF16)
-        static_cast<uint16_t*>(base)[i] = static_cast<uint16_t>(bf16_bits(x));
-    else
-        static_cast<uint16_t*>(base)[i] = static_cast<uint16_t>(f16_bits(x));
-}
 
 __device__ __forceinline__ float wave_sum(float v)
 {
@@ -861,13 +954,13 @@ bool aligned16(const void* ptr)
 // layer): with 6-16 units per CU, 8 waves is 0.6-9.5 % faster for mean rows
 // of 50-160 pages, the two tie at 256 pages and 10 is 2.7 % faster at 288
 // (config 3); with 1-2 units per CU, 8 waves is 7-16 % slower. A smaller
-// batch takes the maximum (16, or 8 for larger groups) so each row streams
+// batch takes the maximum (16, or 8 for wide lanes) so each row streams
 // as fast as one CU allows. Chunks of cut rows take split_waves (a chunk is
 // short, and several of them share a CU). CKV_DECODE_WAVES overrides.
-uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count, uint32_t mean_pages,
-                    uint32_t split_pages)
+uint32_t fast_waves(uint32_t group, int dtype, uint32_t units, int cu_count,
+                    uint32_t mean_pages, uint32_t split_pages)
 {
-    const uint32_t limit = group <= 2 ? 16u : 8u;
+    const uint32_t limit = wide_lanes(group, dtype) ? 8u : 16u;
     if (const char* forced = std::getenv("CKV_DECODE_WAVES")) {
         const long v = std::strtol(forced, nullptr, 10);
         if (v >= 1 && v <= (long)limit)
@@ -875,14 +968,14 @@ uint32_t fast_waves(uint32_t group, uint32_t units, int cu_count, uint32_t mean_
     }
     if (split_pages)
         return std::min(limit, split_waves);
-    if (group <= 2 && cu_count > 0 && units >= (uint32_t)cu_count)
+    if (limit > 10 && cu_count > 0 && units >= (uint32_t)cu_count)
         return units / (uint32_t)cu_count >= 6 && mean_pages < 256 ? 8 : 10;
     return limit;
 }
 
 template <int G>
 hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
-                       const void* q, uint32_t q_heads, float scale_log2, void* out, bool f16,
+                       const void* q, uint32_t q_heads, float scale_log2, void* out, int dt,
                        const void* k_in, const void* v_in, const void* gate, int cu_count,
                        split_scratch split, const rope_table* rope = nullptr,
                        uint32_t rotary = 0)
@@ -890,39 +983,45 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
     if (!m.plan || (m.n_cut && (!split.records || !split.arrivals)))
         return hipErrorInvalidValue;
     const uint32_t units = m.n_plan * p.kv_heads;
-    const uint32_t waves = fast_waves(G, units, cu_count, m.mean_pages, m.split_pages);
+    const uint32_t waves = fast_waves(G, dt, units, cu_count, m.mean_pages, m.split_pages);
     const dim3 grid(units), block(64 * waves);
     // the merge's (acc, max, denominator) per wave, then the rope angle table
     const size_t lds = ((size_t)waves * G * (128 + 2) + (rope ? 2 * 64 : 0)) * sizeof(float);
-    const auto qq = static_cast<const uint16_t*>(q);
-    const auto oo = static_cast<uint16_t*>(out);
+    const auto qq = static_cast<const char*>(q);
     const auto ki = static_cast<const char*>(k_in);
     const auto vi = static_cast<const char*>(v_in);
-    const auto gg = static_cast<const uint16_t*>(gate);
     rope_table64 f64 = {};
     if (rope)
         for (uint32_t j = 0; j < rotary / 2; ++j)
             f64.inv_freq[j] = rope->inv_freq[j];
     // one instantiation per (dtype, fused, gated, rope); rope only when fused
-    const int variant = (rope ? 8 : 0) | (f16 ? 4 : 0) | (k_in ? 2 : 0) | (gate ? 1 : 0);
+    // and on 16-bit pages
+    const int variant = (rope ? 16 : 0) | (dt << 2) | (k_in ? 2 : 0) | (gate ? 1 : 0);
     switch (variant) {
-#define CKV_FAST_CASE(V, F16_, FUSED_, GATED_, ROPE_)                                          \
-    case V:                                                                                    \
-        decode_wg_kernel<G, F16_, FUSED_, GATED_, ROPE_><<<grid, block, lds, s>>>(            \
-            p, m, layer, qq, q_heads, scale_log2, oo, ki, vi, gg, f64, rotary, split);         \
+#define CKV_FAST_CASE(DT_, FUSED_, GATED_, ROPE_)                                              \
+    case (ROPE_ ? 16 : 0) | (DT_ << 2) | (FUSED_ ? 2 : 0) | (GATED_ ? 1 : 0):                  \
+        if constexpr (fast_fits(G, DT_))                                                       \
+            decode_wg_kernel<G, DT_, FUSED_, GATED_, ROPE_><<<grid, block, lds, s>>>(          \
+                p, m, layer, qq, q_heads, scale_log2, out, ki, vi, gate, f64, rotary, split);  \
+        else                                                                                   \
+            return hipErrorInvalidValue;                                                       \
         break;
-        CKV_FAST_CASE(0, false, false, false, false)
-        CKV_FAST_CASE(1, false, false, true, false)
-        CKV_FAST_CASE(2, false, true, false, false)
-        CKV_FAST_CASE(3, false, true, true, false)
-        CKV_FAST_CASE(4, true, false, false, false)
-        CKV_FAST_CASE(5, true, false, true, false)
-        CKV_FAST_CASE(6, true, true, false, false)
-        CKV_FAST_CASE(7, true, true, true, false)
-        CKV_FAST_CASE(10, false, true, false, true)
-        CKV_FAST_CASE(11, false, true, true, true)
-        CKV_FAST_CASE(14, true, true, false, true)
-        CKV_FAST_CASE(15, true, true, true, true)
+        CKV_FAST_CASE(CKV_F32, false, false, false)
+        CKV_FAST_CASE(CKV_F32, false, true, false)
+        CKV_FAST_CASE(CKV_F32, true, false, false)
+        CKV_FAST_CASE(CKV_F32, true, true, false)
+        CKV_FAST_CASE(CKV_BF16, false, false, false)
+        CKV_FAST_CASE(CKV_BF16, false, true, false)
+        CKV_FAST_CASE(CKV_BF16, true, false, false)
+        CKV_FAST_CASE(CKV_BF16, true, true, false)
+        CKV_FAST_CASE(CKV_F16, false, false, false)
+        CKV_FAST_CASE(CKV_F16, false, true, false)
+        CKV_FAST_CASE(CKV_F16, true, false, false)
+        CKV_FAST_CASE(CKV_F16, true, true, false)
+        CKV_FAST_CASE(CKV_BF16, true, false, true)
+        CKV_FAST_CASE(CKV_BF16, true, true, true)
+        CKV_FAST_CASE(CKV_F16, true, false, true)
+        CKV_FAST_CASE(CKV_F16, true, true, true)
 #undef CKV_FAST_CASE
     default:
         return hipErrorInvalidValue;
@@ -1240,8 +1339,9 @@ void write_decode_plan(const std::vector<uint32_t>& positions,
 bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads)
 {
     const uint32_t G = q_heads / p.kv_heads;
-    return p.dtype != CKV_F32 && p.head_dim == 128 && p.block_size == 16
-        && (G == 1 || G == 2 || G == 4 || G == 8) && aligned16(p.keys) && aligned16(p.values);
+    return p.head_dim == 128 && p.block_size == 16
+        && (G == 1 || G == 2 || G == 4 || G == 8) && fast_fits(G, p.dtype) && aligned16(p.keys)
+        && aligned16(p.values);
 }
 
 bool decode_fast_applies(const pool_view& p, uint32_t q_heads, const void* q, const void* out)
@@ -1257,19 +1357,19 @@ hipError_t launch_decode(hipStream_t s, const pool_view& p, const meta_view& m, 
         return hipSuccess;
     const float scale_log2 = scale * log2e;
     if (decode_fast_applies(p, q_heads, q, out)) {
-        const bool f16 = p.dtype == CKV_F16;
+        const int dt = p.dtype;
         switch (q_heads / p.kv_heads) {
         case 1:
-            return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
+            return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, dt, nullptr,
                                   nullptr, gate, cu_count, split);
         case 2:
-            return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
+            return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, dt, nullptr,
                                   nullptr, gate, cu_count, split);
         case 4:
-            return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
+            return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, dt, nullptr,
                                   nullptr, gate, cu_count, split);
         default:
-            return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, nullptr,
+            return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, dt, nullptr,
                                   nullptr, gate, cu_count, split);
         }
     }
@@ -1304,19 +1404,19 @@ hipError_t launch_append_decode(hipStream_t s, const pool_view& p, const meta_vi
     if (rope && (rotary < 16 || rotary > 128 || (rotary & (rotary - 1)) != 0))
         return hipErrorInvalidValue;
     const float scale_log2 = scale * log2e;
-    const bool f16 = p.dtype == CKV_F16;
+    const int dt = p.dtype;
     switch (q_heads / p.kv_heads) {
     case 1:
-        return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
+        return launch_fast<1>(s, p, m, layer, q, q_heads, scale_log2, out, dt, k_in, v_in, gate,
                               cu_count, split, rope, rotary);
     case 2:
-        return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
+        return launch_fast<2>(s, p, m, layer, q, q_heads, scale_log2, out, dt, k_in, v_in, gate,
                               cu_count, split, rope, rotary);
     case 4:
-        return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
+        return launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, dt, k_in, v_in, gate,
                               cu_count, split, rope, rotary);
     default:
-        return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, f16, k_in, v_in, gate,
+        return launch_fast<8>(s, p, m, layer, q, q_heads, scale_log2, out, dt, k_in, v_in, gate,
                               cu_count, split, rope, rotary);
     }
 }

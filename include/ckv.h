@@ -276,8 +276,9 @@ int ckv_gather(ckv_pool* pool, size_t layer, size_t table_offset, size_t table_l
  * to logical positions 0..positions[r] through their table range:
  * out = softmax(q . k * scale) . v with fp32 accumulation. queries and
  * output are device [rows, q_heads*head_dim] of the pool dtype.
- * Decode form: the q heads of a GQA group share every K/V read. 16-bit pools
- * with head_dim 128 and 16-token pages take one workgroup per (row, kv_head),
+ * Decode form: the q heads of a GQA group share every K/V read. Pools with
+ * head_dim 128, 16-token pages and 1, 2, 4 or 8 q heads per kv head (1, 2 or
+ * 4 for f32 pools) take one workgroup per (row, kv_head),
  * or per page chunk of rows the batch plan cuts (ckv_decode_plan), the chunks
  * merged by the last to finish; other geometries take split-KV over token
  * chunks and a merge launch. Both are the split-K of
@@ -323,8 +324,8 @@ int ckv_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_he
  * the rest the records. It needs what the allocating calls already set up:
  * a batch of single-row query tiles uploaded with ckv_tables_upload or
  * ckv_batch_upload (its plan goes up with it), and the fast decode's geometry
- * (bf16/fp16, head_dim 128, 16-token pages, 1, 2, 4 or 8 q heads per kv head,
- * 16-byte aligned pools, queries and output); a batch with a multi-row query
+ * (head_dim 128, 16-token pages, 1, 2, 4 or 8 q heads per kv head, 1, 2 or 4
+ * for f32 pools, 16-byte aligned pools, queries and output); a batch with a multi-row query
  * tile is refused whatever ran on it before. Otherwise, and when the batch's
  * records exceed the array (n_records * q_heads * 528 bytes > 16 MiB - 256 KiB
  * or n_records * kv_heads * 4 bytes > 256 KiB, see ckv_decode_plan), it
@@ -384,7 +385,8 @@ int ckv_rope_append(ckv_pool* pool, size_t layer, const void* keys, const void* 
  * queries and of the new keys, store_kv, paged_attention (and, with a gate,
  * sigmoid_mul) — src/qwen/qwen_layer.cc:20-30, :43-49 (Qwen3) and :183-206
  * (Qwen3.5 full attention) — in one launch where ckv_append_decode's fused
- * kernel applies and rotary_dim (0 = head_dim) is 16, 32, 64 or 128; otherwise
+ * kernel applies, the pool is bf16 or fp16 and rotary_dim (0 = head_dim) is
+ * 16, 32, 64 or 128; otherwise
  * as ckv_rope into a pool-owned buffer, ckv_rope_append and the attention.
  * keys/values: [rows, kv_heads*head_dim]; queries: [rows, q_heads*head_dim];
  * queries and keys are read unrotated and not modified; gate may be NULL (no

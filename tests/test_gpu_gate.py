@@ -17,7 +17,7 @@ import torch
 from chibillm_amd import ckv
 from oracle import oracle as orc
 from tests.gpu_util import (assert_close, force_plan, new_context, new_pool, to_dev, to_f32,
-                            to_host)
+                            to_host, torch_dtype)
 
 pytestmark = pytest.mark.gpu
 
@@ -95,11 +95,24 @@ def decode_case(seed, batch=24):
     return rng, lengths, tables, blocks
 
 
+def shifted(t, aligned):
+    """t itself, or a copy one element past a 16-byte boundary."""
+    if aligned:
+        return t
+    base = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
+    view = base[1:1 + t.numel()].view(t.shape)
+    view.copy_(t)
+    assert view.data_ptr() % 16 != 0
+    return view
+
+
+@pytest.mark.parametrize("aligned", [True, False])
 @pytest.mark.parametrize("code", [orc.BF16, orc.F16, orc.F32])
-def test_gated_decode_matches_oracle_and_unfused(ctx, code):
-    """bf16/f16 take the fused decode kernel; f32 the generic split-K path
-    with the merge (the gate in both of its epilogues)."""
-    print(f"gated decode dtype {code}", flush=True)
+def test_gated_decode_matches_oracle_and_unfused(ctx, code, aligned):
+    """Every pool dtype through the fast decode kernel's gated epilogue, and
+    through the generic split-K path with the merge (misaligned queries and
+    output: the gate in both of its epilogues)."""
+    print(f"gated decode dtype {code} aligned {aligned}", flush=True)
     rng, lengths, tables, blocks = decode_case(11 + code)
     H, Hq = 8, 16
     F = H * D
@@ -117,10 +130,10 @@ def test_gated_decode_matches_oracle_and_unfused(ctx, code):
     kd.copy_(to_dev(kc, code))
     vd.copy_(to_dev(vc, code))
     pool.upload(flat, offsets, [len(t) for t in tables], positions)
-    qd, gd = to_dev(q, code), to_dev(gate, code)
-    gated = torch.full_like(qd, float("nan"))
+    qd, gd = shifted(to_dev(q, code), aligned), shifted(to_dev(gate, code), aligned)
+    gated = shifted(torch.full_like(qd, float("nan")), aligned)
     pool.attention_gated(0, qd, Hq, scale, gd, gated)
-    plain = torch.full_like(qd, float("nan"))
+    plain = shifted(torch.full_like(qd, float("nan")), aligned)
     pool.attention(0, qd, Hq, scale, plain)
     unfused = torch.empty_like(plain)
     ctx.sigmoid_mul(gd, plain, unfused)
@@ -179,14 +192,16 @@ def test_gated_prefill_tiles(ctx, group):
     pool.close()
 
 
+@pytest.mark.parametrize("code", [orc.BF16, orc.F32])
 @pytest.mark.parametrize("split", [None, "3", "b5"])
-def test_append_decode_gated_equals_fused_pair(ctx, split, monkeypatch):
-    """The decode step's fused append + attention with the gate: pages bit-exact
-    with ckv_append_decode, output within tolerance of the oracle; also with
-    every row cut into chunks of 3 pages and with the batch dealt out 5 pages
-    to a workgroup (the gate applied by the chunk that merges)."""
+def test_append_decode_gated_equals_fused_pair(ctx, split, code, monkeypatch):
+    """The decode step's fused append + attention with the gate, bf16 and f32
+    pages: pages bit-exact with ckv_append_decode, output within tolerance of
+    the oracle; also with every row cut into chunks of 3 pages and with the
+    batch dealt out 5 pages to a workgroup (the gate applied by the chunk that
+    merges)."""
+    print(f"append_decode_gated dtype {code} split {split}", flush=True)
     force_plan(monkeypatch, split)
-    code = orc.BF16
     rng, lengths, tables, blocks = decode_case(5, batch=16)
     H, Hq = 8, 16
     F = H * D
@@ -209,7 +224,7 @@ def test_append_decode_gated_equals_fused_pair(ctx, split, monkeypatch):
         kd.copy_(to_dev(kc, code))
         vd.copy_(to_dev(vc, code))
         pool.upload(flat, offsets, [len(t) for t in tables], positions, slots)
-        out = torch.full((rows, Hq * D), float("nan"), dtype=torch.bfloat16, device="cuda")
+        out = torch.full((rows, Hq * D), float("nan"), dtype=torch_dtype(code), device="cuda")
         if gated:
             pool.append_decode_gated(0, to_dev(k_new, code), to_dev(v_new, code),
                                      to_dev(q, code), Hq, scale, to_dev(gate, code), out)

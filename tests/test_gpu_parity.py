@@ -266,7 +266,7 @@ def compact_oracle(geom_h_d, lengths, tables, ks, vs, q, q_heads, positions=None
     H, D = geom_h_d
     F = H * D
     n_pages = sum(len(t) for t in tables)
-    kc = np.zeros(n_pages * 16 * F, np.uint16)
+    kc = np.zeros(n_pages * 16 * F, np.float32 if code == orc.F32 else np.uint16)
     vc = np.zeros_like(kc)
     flat, offsets, at = [], [], 0
     for n, t, k, v in zip(lengths, tables, ks, vs):
@@ -507,6 +507,77 @@ def test_edge_positions_and_gqa_groups(ctx):
         assert_close(to_f32(out), expected, what=f"group {group}")
         pool.close()
     ctx.sync()
+
+
+# ---- f32 pools (the reference's storage dtype) through the fast decode ------------------------
+
+@pytest.mark.parametrize("split", [None, "0", "3"])
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_f32_decode_append_decode_and_noalloc(ctx, group, split, monkeypatch):
+    """f32 pages through the fast decode kernel (1, 2 or 4 q heads per kv head;
+    8 take the generic split-KV kernel): rows of 1 to 1,025 tokens ending on and
+    past page boundaries, under the default plan, with no cut and with chunks
+    of 3 pages. ckv_append_decode (fused) and ckv_append then
+    ckv_decode_attention leave the same pages and outputs bit for bit; the
+    no-allocation entry point matches them where the fast kernel applies and
+    refuses the pool where it does not; outputs within 1e-5 abs + 1e-4 rel of
+    the oracle (f32 storage and f32 arithmetic on both sides)."""
+    print(f"f32 decode group {group} split {split}", flush=True)
+    force_plan(monkeypatch, split)
+    rng = orc.Mt64(40 + group)
+    lengths = [1, 16, 17, 32, 33, 257, 1024, 1025]
+    B = sum(-(-n // 16) for n in lengths) + 3
+    perm = rng.permutation(B)
+    tables, at = [], 0
+    for n in lengths:
+        tables.append(perm[at:at + -(-n // 16)])
+        at += len(tables[-1])
+    H = 16 // group if group < 8 else 2
+    q_heads = H * group
+    F = H * 128
+    ks = [rng.normal(n * F, orc.F32).reshape(n, F) for n in lengths]
+    vs = [rng.normal(n * F, orc.F32).reshape(n, F) for n in lengths]
+    q = rng.normal(len(lengths) * q_heads * 128, orc.F32).reshape(len(lengths), -1)
+    flat = np.concatenate(tables)
+    offsets = np.cumsum([0] + [len(t) for t in tables[:-1]])
+    positions = [n - 1 for n in lengths]
+    slots = [orc.slot(t, p, 16) for t, p in zip(tables, positions)]
+    k_new = to_dev(np.stack([k[-1] for k in ks]), orc.F32)
+    v_new = to_dev(np.stack([v[-1] for v in vs]), orc.F32)
+    qd = to_dev(q, orc.F32)
+    scale = float(np.float32(1 / math.sqrt(128)))
+    outs, caches = [], []
+    for how in ("fused", "pair", "noalloc"):
+        pool, kd, vd = new_pool(ctx, (1, B, 16, H, 128), orc.F32, fill=float("nan"))
+        cached = [(n - 1, t, k[:-1], v[:-1]) for n, t, k, v in zip(lengths, tables, ks, vs) if n > 1]
+        fill_by_append(pool, *zip(*cached), code=orc.F32)
+        pool.upload(flat, offsets, [len(t) for t in tables], positions, slots)
+        out = torch.full((len(lengths), q_heads * 128), float("nan"), device="cuda")
+        if how == "fused":
+            pool.append_decode(0, k_new, v_new, qd, q_heads, scale, out)
+        elif how == "pair":
+            pool.append(0, k_new, v_new)
+            pool.decode(0, qd, q_heads, scale, out)
+        elif group == 8:
+            with pytest.raises(ckv.CkvError) as e:
+                pool.append_decode_noalloc(0, k_new, v_new, qd, q_heads, scale, out)
+            assert e.value.name == "ckv.invalid_argument"
+            pool.close()
+            continue
+        else:
+            pool.append_decode_noalloc(0, k_new, v_new, qd, q_heads, scale, out)
+        ctx.sync()
+        outs.append(out)
+        caches.append((kd.clone(), vd.clone()))
+        pool.close()
+    for other, cache in zip(outs[1:], caches[1:]):
+        assert torch.equal(outs[0], other)
+        # bit patterns: pages never written hold the NaN fill
+        for a, b in zip(caches[0], cache):
+            assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    expected = compact_oracle((H, 128), lengths, tables, ks, vs, q, q_heads, code=orc.F32)
+    assert_close(to_f32(outs[0]), expected, atol=1e-5, rtol=1e-4,
+                 what=f"f32 group {group} split {split}")
 
 
 # ---- pages: copies, checkpoints, table patches ----------------------------------------------

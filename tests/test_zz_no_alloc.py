@@ -178,8 +178,9 @@ def test_noalloc_refuses_a_tiled_batch_whatever_ran_before(ctx):
 
 def test_noalloc_refuses_instead_of_allocating(ctx, monkeypatch):
     """A batch of multi-row query tiles (no decode plan uploaded), an f32 pool
-    and a plan whose records exceed the 16 MiB array are refused with
-    invalid_argument; nothing is launched."""
+    with 8 q heads per kv head (the generic kernel's geometry) and a plan whose
+    records exceed the 16 MiB array are refused with invalid_argument; nothing
+    is launched."""
     q = torch.zeros(4, 2048, dtype=torch.bfloat16, device="cuda")
     kv = torch.zeros(4, 1024, dtype=torch.bfloat16, device="cuda")
     out = torch.empty_like(q)
@@ -203,10 +204,10 @@ def test_noalloc_refuses_instead_of_allocating(ctx, monkeypatch):
     pool.close()
     f32, _, _ = new_pool(ctx, (1, 4, 16, 8, 128), orc.F32)
     f32.upload([0, 1, 2, 3], [0, 1, 2, 3], [1] * 4, [0] * 4, slots=[0, 16, 32, 48])
-    qf = torch.zeros(4, 2048, device="cuda")
+    qf = torch.zeros(4, 64 * 128, device="cuda")
     kf = torch.zeros(4, 1024, device="cuda")
     with pytest.raises(ckv.CkvError) as e:
-        f32.append_decode_noalloc(0, kf, kf, qf, 16, SCALE, torch.empty_like(qf))
-    assert e.value.name == "ckv.invalid_argument"
+        f32.append_decode_noalloc(0, kf, kf, qf, 64, SCALE, torch.empty_like(qf))
+    assert e.value.name == "ckv.invalid_argument" and "f32" in str(e.value)
     ctx.sync()
     f32.close()

@@ -324,13 +324,17 @@ bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads);
 // Floats per (work item, q head) partial record: [max, denominator, 0, 0, acc[head_dim]].
 uint32_t partial_record_floats(uint32_t head_dim);
 
-// ---- launchers (kernels_prefill.hip) ------------------------------------------
-// MFMA prefill: 16-bit K/V, head_dim 128, 16-token pages, GQA group 1/2/4/8,
-// 16-byte aligned pools, queries and output.
+// ---- launchers (kernels_prefill.hip, kernels_prefill_f32.hip) -----------------
+// MFMA prefill: head_dim 128, 16-token pages, GQA group 1/2/4/8, 16-byte
+// aligned pools, queries and output; bf16/fp16 products on
+// v_mfma_f32_32x32x16, f32 ones on v_mfma_f32_32x32x2_f32.
 bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, const void* out);
 hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                           const void* q, uint32_t q_heads, float scale, void* out,
                           const void* gate = nullptr);
+hipError_t launch_prefill_f32(hipStream_t s, const pool_view& p, const meta_view& m,
+                              uint32_t layer, const void* q, uint32_t q_heads, float scale,
+                              void* out, const void* gate);
 
 // ---- launchers (kernels_rope.hip) --------------------------------------------------
 // theta^(-2j/rotary) in float for j < rotary/2 (src/metal/metal_kernels.mm:186-191)

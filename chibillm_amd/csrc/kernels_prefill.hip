@@ -616,7 +616,7 @@ bool aligned16(const void* ptr)
 
 bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, const void* out)
 {
-    if (p.dtype == CKV_F32 || p.head_dim != dim || p.block_size != page_tokens)
+    if (p.head_dim != dim || p.block_size != page_tokens)
         return false;
     if (!p.kv_heads || q_heads % p.kv_heads)
         return false;
@@ -630,6 +630,8 @@ hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m,
                           const void* q, uint32_t q_heads, float scale, void* out,
                           const void* gate)
 {
+    if (p.dtype == CKV_F32)
+        return launch_prefill_f32(s, p, m, layer, q, q_heads, scale, out, gate);
     const uint32_t group = q_heads / p.kv_heads;
     const uint64_t grid = (uint64_t)m.n_tiles * group * p.kv_heads;
     if (!grid)

@@ -146,11 +146,11 @@ def test_gated_decode_matches_oracle_and_unfused(ctx, code, aligned):
     pool.close()
 
 
-@pytest.mark.parametrize("group", [2, 8])
-def test_gated_prefill_tiles(ctx, group):
-    """Ragged tiles through the MFMA prefill kernel's gated epilogue."""
-    print(f"gated prefill group {group}", flush=True)
-    code = orc.BF16
+@pytest.mark.parametrize("group,code", [(2, orc.BF16), (8, orc.BF16), (2, orc.F32), (8, orc.F32)])
+def test_gated_prefill_tiles(ctx, group, code):
+    """Ragged tiles through the MFMA prefill kernels' gated epilogues (bf16
+    and f32 pages)."""
+    print(f"gated prefill group {group} dtype {code}", flush=True)
     rng = orc.Mt64(40 + group)
     H = 2
     Hq = H * group

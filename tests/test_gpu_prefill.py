@@ -111,9 +111,13 @@ def test_shared_prefix_chunks_with_copy_on_write_tail(ctx, prefix):
 RAGGED = [(0, 1), (0, 40), (5, 300), (100, 33), (16, 257), (1000, 64), (700, 1), (63, 2)]
 
 
-@pytest.mark.parametrize("code", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16, orc.F32])
 @pytest.mark.parametrize("group", [1, 2, 4, 8])
 def test_ragged_tiles_every_group_size(ctx, group, code):
+    """Every route (auto, prefill, decode form) against the oracle; f32 pages
+    (the reference's storage dtype, fp32 products on the matrix cores) within
+    1e-5 abs + 1e-4 rel, and their prefill takes the MFMA kernel (one
+    paged_attention_prefill launch)."""
     print(f"ragged tiles group {group} dtype {code}", flush=True)
     H = 2
     Hq = H * group
@@ -148,11 +152,18 @@ def test_ragged_tiles_every_group_size(ctx, group, code):
     expected = orc.Attention(geom, kc, vc, code, q, code, positions, flat, offsets, lengths, Hq,
                              1, scale()).online_threads(8)
     qd = to_dev(q, code)
+    tol = dict(atol=1e-5, rtol=1e-4) if code == orc.F32 else {}
     for name in ("attention", "prefill", "decode"):
         out = torch.full_like(qd, float("nan"))
+        ctx.sync()
+        ctx.profile(True)
+        ctx.profile_reset()
         getattr(pool, name)(1, qd, Hq, scale(), out)
         ctx.sync()
-        assert_close(to_f32(out), expected, what=f"{name}, group {group}")
+        launches = ctx.profile_query("paged_attention_prefill")[1]
+        ctx.profile(False)
+        assert launches == (0 if name == "decode" else 1), (name, launches)
+        assert_close(to_f32(out), expected, what=f"{name}, group {group}", **tol)
     pool.close()
 
 

@@ -47,6 +47,29 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+# pool element types bench.py measures: bf16 (the BASELINE configs) and f32
+# (the reference's own storage type)
+ELEM_BYTES = {"bf16": 2, "f32": 4}
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}  # MI355X dense matrix peaks
+
+
+def pool_types(dtype):
+    """(torch dtype, ckv code, oracle code) of a pool of element type `dtype`."""
+    import torch
+
+    from chibillm_amd import ckv
+    from oracle import oracle as orc
+
+    if dtype == "f32":
+        return torch.float32, ckv.F32, orc.F32
+    return torch.bfloat16, ckv.BF16, orc.BF16
+
+
+def host_values(orc, a, code):
+    """float32 samples as the oracle's host array of element type `code`."""
+    return np.asarray(a, np.float32) if code == orc.F32 else orc.from_f32(a, code)
+
+
 def traffic_bytes(workload, kernel):
     """Measured HBM bytes per launch of `kernel` if a counter summary exists."""
     try:
@@ -96,25 +119,27 @@ def median_seconds(fn, runs):
     return statistics.median(times)
 
 
-def host_decode_batch(lengths, seed):
-    """One layer of bf16 K/V on the host for rows of `lengths` tokens on permuted
-    pages, and bf16 queries: the oracle's attention over them. The pages hold a
-    tiled block of N(0,1) values (the timing does not depend on the values)."""
+def host_decode_batch(lengths, seed, dtype="bf16"):
+    """One layer of K/V of element type `dtype` on the host for rows of
+    `lengths` tokens on permuted pages, and queries of that type: the oracle's
+    attention over them. The pages hold a tiled block of N(0,1) values (the
+    timing does not depend on the values)."""
     from oracle import oracle as orc
 
+    code = orc.F32 if dtype == "f32" else orc.BF16
     gen = np.random.default_rng(seed)
     F = KV_HEADS * HEAD_DIM
     pages = [math.ceil(n / BLOCK) for n in lengths]
     n_pages = sum(pages)
-    block = orc.from_f32(gen.standard_normal(1 << 22, np.float32), orc.BF16)
+    block = host_values(orc, gen.standard_normal(1 << 22, np.float32), code)
     reps = -(-(n_pages * BLOCK * F) // block.size)
     kc = np.tile(block, reps)[:n_pages * BLOCK * F]
     vc = np.roll(kc, 12345)
-    q = orc.from_f32(gen.standard_normal((len(lengths), Q_HEADS * HEAD_DIM), np.float32),
-                     orc.BF16)
+    q = host_values(orc, gen.standard_normal((len(lengths), Q_HEADS * HEAD_DIM), np.float32),
+                    code)
     perm = gen.permutation(n_pages).astype(np.uint32)
     offsets = np.cumsum([0] + pages[:-1])
-    return orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, orc.BF16, q, orc.BF16,
+    return orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, code, q, code,
                          [n - 1 for n in lengths], perm, offsets, pages, Q_HEADS, 0,
                          1 / math.sqrt(HEAD_DIM))
 
@@ -122,7 +147,7 @@ def host_decode_batch(lengths, seed):
 _CPU_DECODE_CACHE = {}
 
 
-def cpu_decode_baseline(lengths, threads, runs, with_step=False):
+def cpu_decode_baseline(lengths, threads, runs, with_step=False, dtype="bf16"):
     """The CPU path of one decode step at these lengths, timed on this host
     (median of `runs` each): decode attention over one layer on `threads`
     threads and on one thread (oracle/oracle.c, the restated
@@ -131,18 +156,19 @@ def cpu_decode_baseline(lengths, threads, runs, with_step=False):
     step, block_manager reservations plus prepare_paged_batch. A run that asks
     twice for the same inputs (the default run's config-3 line and its config-5
     leg) times them once."""
-    key = (tuple(lengths), threads, runs, with_step)
+    key = (tuple(lengths), threads, runs, with_step, dtype)
     if key not in _CPU_DECODE_CACHE:
-        _CPU_DECODE_CACHE[key] = _cpu_decode_baseline(lengths, threads, runs, with_step)
+        _CPU_DECODE_CACHE[key] = _cpu_decode_baseline(lengths, threads, runs, with_step, dtype)
     return dict(_CPU_DECODE_CACHE[key], legs_ms=dict(_CPU_DECODE_CACHE[key]["legs_ms"]))
 
 
-def _cpu_decode_baseline(lengths, threads, runs, with_step):
+def _cpu_decode_baseline(lengths, threads, runs, with_step, dtype):
     from oracle import oracle as orc
 
     F = KV_HEADS * HEAD_DIM
-    layer_bytes = sum(lengths) * F * 2 * 2
-    att = host_decode_batch(lengths, 1)
+    code = orc.F32 if dtype == "f32" else orc.BF16
+    layer_bytes = sum(lengths) * F * 2 * ELEM_BYTES[dtype]
+    att = host_decode_batch(lengths, 1, dtype)
     all_s = median_seconds(lambda: att.online_threads(threads), runs)
     single_s = median_seconds(lambda: att.online_threads(1), runs)
     out = {
@@ -162,9 +188,9 @@ def _cpu_decode_baseline(lengths, threads, runs, with_step):
     if with_step:
         rows = len(lengths)
         gen = np.random.default_rng(2)
-        k = orc.from_f32(gen.standard_normal((rows, F), np.float32), orc.BF16)
+        k = host_values(orc, gen.standard_normal((rows, F), np.float32), code)
         pages = sum(math.ceil((n + 1) / BLOCK) for n in lengths) + 1
-        kc = np.zeros(pages * BLOCK * F, np.uint16)
+        kc = np.zeros(pages * BLOCK * F, k.dtype)
         vc = np.zeros_like(kc)
         slots = gen.permutation(pages * BLOCK)[:rows].astype(np.uint32)
         reps = 100
@@ -228,17 +254,18 @@ def bench_config2(args, long_row=False):
     flat = perm[:sum(pages)]
     offsets = np.cumsum([0] + pages[:-1])
     F = KV_HEADS * HEAD_DIM
+    tdt, code, _ = pool_types(args.dtype)
+    es = ELEM_BYTES[args.dtype]
     ctx = ckv.Context(0, stream=torch.cuda.current_stream())
     if args.calibrate_copy:
         calibration_copy(ctx)
     tgen = torch.Generator(device=device)
     tgen.manual_seed(args.seed)
     elems = CONFIG2_POOL * BLOCK * F
-    keys = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=tgen)
-    values = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=tgen)
-    pool = ckv.Pool(ctx, 1, CONFIG2_POOL, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16, keys, values)
-    q = torch.randn(batch, Q_HEADS * HEAD_DIM, generator=tgen, device=device).to(
-        torch.bfloat16)
+    keys = torch.empty(elems, dtype=tdt, device=device).normal_(generator=tgen)
+    values = torch.empty(elems, dtype=tdt, device=device).normal_(generator=tgen)
+    pool = ckv.Pool(ctx, 1, CONFIG2_POOL, BLOCK, KV_HEADS, HEAD_DIM, code, keys, values)
+    q = torch.randn(batch, Q_HEADS * HEAD_DIM, generator=tgen, device=device).to(tdt)
     out = torch.empty_like(q)
     scale = 1.0 / math.sqrt(HEAD_DIM)
     pool.upload(flat, offsets, pages, [n - 1 for n in lengths])
@@ -258,8 +285,8 @@ def bench_config2(args, long_row=False):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     launch_ms = start.elapsed_time(end) / steps
-    kv_bytes = sum(lengths) * F * 2 * 2
-    per_launch = kv_bytes + 2 * batch * Q_HEADS * HEAD_DIM * 2 + 4 * sum(pages)
+    kv_bytes = sum(lengths) * F * 2 * es
+    per_launch = kv_bytes + 2 * batch * Q_HEADS * HEAD_DIM * es + 4 * sum(pages)
     achieved = per_launch / (launch_ms / 1e3) / 1e9
     if long_row:
         metric = ("paged decode KV-read GB/s (% HBM peak), Qwen3-0.6B KV, one layer, one row of "
@@ -271,6 +298,9 @@ def bench_config2(args, long_row=False):
         metric = "paged decode KV-read GB/s (% HBM peak), Qwen3-0.6B KV, one layer, batch 32"
         workload = ("config2: single-layer paged GQA decode attention, batch 32, context "
                     "U[256,4096], pages from a seeded permutation of a 65,536-page pool")
+    if args.dtype != "bf16":
+        metric += f", {args.dtype} pages"
+        workload += f"; {args.dtype} pages (BASELINE's config is bf16)"
     result = {
         "metric": metric,
         "value": round(kv_bytes / (launch_ms / 1e3) / 1e9, 2),
@@ -283,7 +313,7 @@ def bench_config2(args, long_row=False):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": args.dtype,
         "data": "synthetic N(0,1) K/V/Q, seeded lengths and page permutation",
         "config": {
             "workload": workload,
@@ -300,7 +330,8 @@ def bench_config2(args, long_row=False):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None if long_row else traffic_bytes("config2", "decode"),
+            "traffic": (None if long_row or args.dtype != "bf16"
+                        else traffic_bytes("config2", "decode")),
             "avg_launch_us": round(launch_ms * 1e3, 3),
             "algorithmic_bytes_per_launch": int(per_launch),
         },
@@ -312,10 +343,11 @@ def bench_config2(args, long_row=False):
     if not args.no_cpu_baseline:
         threads = baseline_threads(args)
         log(f"CPU baseline on {threads} threads")
-        base = cpu_decode_baseline(lengths, threads, runs=5)
+        base = cpu_decode_baseline(lengths, threads, runs=5, dtype=args.dtype)
         base["sample"] = (f"the whole workload: oracle/oracle.c decode attention (restated "
                           f"paged_attention_f32, fp32 accumulate) over the same {batch} "
-                          f"rows ({sum(lengths)} tokens, {kv_bytes / 1e9:.3f} GB of bf16 K/V), "
+                          f"rows ({sum(lengths)} tokens, {kv_bytes / 1e9:.3f} GB of "
+                          f"{args.dtype} K/V), "
                           f"median of 5 runs on {threads} threads and 5 on one")
         result["cpu_baseline"] = base
     return result
@@ -356,15 +388,17 @@ def bench_config3(args):
     for s in range(BATCH):
         ensure_pages(s, int(lengths[s]))
 
-    kv_gb = LAYERS * n_pool * BLOCK * F * 2 * 2 / 1e9
+    tdt, code, _ = pool_types(args.dtype)
+    es = ELEM_BYTES[args.dtype]
+    kv_gb = LAYERS * n_pool * BLOCK * F * 2 * es / 1e9
     log(f"pool {n_pool} pages x {LAYERS} layers = {kv_gb:.1f} GB K+V; "
         f"context tokens {int(lengths.sum())}")
     ctx = ckv.Context(0, stream=torch.cuda.current_stream())
     if args.calibrate_copy:
         calibration_copy(ctx)
     elems = LAYERS * n_pool * BLOCK * F
-    keys = torch.empty(elems, dtype=torch.bfloat16, device=device)
-    values = torch.empty(elems, dtype=torch.bfloat16, device=device)
+    keys = torch.empty(elems, dtype=tdt, device=device)
+    values = torch.empty(elems, dtype=tdt, device=device)
     tgen = torch.Generator(device=device)
     tgen.manual_seed(args.seed)
     t0 = time.perf_counter()
@@ -374,14 +408,14 @@ def bench_config3(args):
             buf[i:i + step].normal_(generator=tgen)
     torch.cuda.synchronize()
     log(f"filled K/V with N(0,1) in {time.perf_counter() - t0:.1f} s")
-    pool = ckv.Pool(ctx, LAYERS, n_pool, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16, keys, values)
+    pool = ckv.Pool(ctx, LAYERS, n_pool, BLOCK, KV_HEADS, HEAD_DIM, code, keys, values)
 
-    q = torch.randn(LAYERS, BATCH, Q_HEADS * HEAD_DIM, generator=tgen, device=device).to(torch.bfloat16)
-    k_new = torch.randn(LAYERS, BATCH, F, generator=tgen, device=device).to(torch.bfloat16)
-    v_new = torch.randn(LAYERS, BATCH, F, generator=tgen, device=device).to(torch.bfloat16)
-    out = torch.empty(LAYERS, BATCH, Q_HEADS * HEAD_DIM, dtype=torch.bfloat16, device=device)
+    q = torch.randn(LAYERS, BATCH, Q_HEADS * HEAD_DIM, generator=tgen, device=device).to(tdt)
+    k_new = torch.randn(LAYERS, BATCH, F, generator=tgen, device=device).to(tdt)
+    v_new = torch.randn(LAYERS, BATCH, F, generator=tgen, device=device).to(tdt)
+    out = torch.empty(LAYERS, BATCH, Q_HEADS * HEAD_DIM, dtype=tdt, device=device)
     gate = (torch.randn(LAYERS, BATCH, Q_HEADS * HEAD_DIM, generator=tgen, device=device)
-            .to(torch.bfloat16) if args.gate else None)
+            .to(tdt) if args.gate else None)
     scale = 1.0 / math.sqrt(HEAD_DIM)
     offsets = np.arange(BATCH, dtype=np.uint32) * max_pages
 
@@ -446,7 +480,7 @@ def bench_config3(args):
                for name in (dominant, "paged_attention_merge", "store_kv")}
     ctx.profile(False)
 
-    kv_row_bytes = F * 2 * 2  # K + V, bf16, all KV heads
+    kv_row_bytes = F * 2 * es  # K + V, all KV heads
     kv_bytes = LAYERS * tokens_attended * kv_row_bytes
     value = kv_bytes / elapsed / 1e9
     ms_per_step = elapsed * 1e3 / args.steps
@@ -455,12 +489,13 @@ def bench_config3(args):
     appended = 0 if args.no_fuse else BATCH * kv_row_bytes
     qo_rows = 3 if args.gate else 2  # Q and O, and the gate when it is read
     per_launch = (tokens_attended * kv_row_bytes + pages_read * 4
-                  + args.steps * (qo_rows * BATCH * Q_HEADS * HEAD_DIM * 2 + appended)) / args.steps
+                  + args.steps * (qo_rows * BATCH * Q_HEADS * HEAD_DIM * es + appended)) / args.steps
     launches = LAYERS * args.steps * (2 if args.no_fuse else 1)
     avg_launch_s = launches_ms / launches / 1e3
     achieved = per_launch / (launches_ms / (LAYERS * args.steps) / 1e3) / 1e9
     result = {
-        "metric": "paged decode KV-read GB/s (% HBM peak) + tokens/s, Qwen3-0.6B KV, batch 128",
+        "metric": "paged decode KV-read GB/s (% HBM peak) + tokens/s, Qwen3-0.6B KV, batch 128"
+                  + ("" if args.dtype == "bf16" else f", {args.dtype} pages"),
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -470,7 +505,7 @@ def bench_config3(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": args.dtype,
         "data": "synthetic N(0,1) K/V/Q, seeded lengths and page order",
         "config": {
             "workload": "config3: 28-layer decode step (append 1 token/seq/layer + paged GQA "
@@ -498,13 +533,15 @@ def bench_config3(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_bytes("config3", dominant),
+            "traffic": traffic_bytes("config3", dominant) if args.dtype == "bf16" else None,
             "avg_launch_us": round(avg_launch_s * 1e6, 2),
             "algorithmic_bytes_per_launch": int(per_launch),
             "timing": "one event pair per step around its 28 launches, launch gaps included",
         },
         "cpu_baseline": None,
     }
+    if args.dtype != "bf16":
+        result["config"]["workload"] += f"; {args.dtype} pages (BASELINE's config is bf16)"
     pool.close()
     del keys, values
     torch.cuda.empty_cache()
@@ -513,7 +550,8 @@ def bench_config3(args):
         log(f"CPU baseline on {threads} threads")
         base_lengths = [int(x) for x in np.random.default_rng(args.seed).integers(
             CTX_LO, CTX_HI + 1, BATCH)]
-        base = cpu_decode_baseline(base_lengths, threads, runs=5, with_step=True)
+        base = cpu_decode_baseline(base_lengths, threads, runs=5, with_step=True,
+                                   dtype=args.dtype)
         legs = base["legs_ms"]
         step_ms = (LAYERS * (legs["decode_attention_per_layer"]
                              + legs["append_store_kv_per_layer"])
@@ -523,14 +561,14 @@ def bench_config3(args):
         base["sample"] = (f"one layer of the workload, scaled by {LAYERS}: oracle/oracle.c decode "
                           f"attention (restated paged_attention_f32, fp32 accumulate) over the "
                           f"{BATCH} rows ({sum(base_lengths)} tokens, "
-                          f"{sum(base_lengths) * F * 4 / 1e9:.2f} GB of bf16 K/V per layer), "
+                          f"{sum(base_lengths) * F * 2 * es / 1e9:.2f} GB of {args.dtype} K/V per "
+                          f"layer), "
                           f"store_kv of the {BATCH} new rows, and the step's block_manager + "
                           f"prepare_paged_batch; median of 5 runs each, on {threads} threads "
                           f"and on one")
         result["cpu_baseline"] = base
     return result
 
-MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 ROPE_THETA = 1e6  # Qwen3-0.6B rope_theta
 PREFILL_SEQS, PREFILL_CHUNK = 64, 512
 
@@ -542,27 +580,29 @@ def prefill_flops(prefix, chunk, seqs):
     return 4 * HEAD_DIM * Q_HEADS * seqs * keys
 
 
-def prefill_cpu_baseline(threads, prefix, runs=5):
+def prefill_cpu_baseline(threads, prefix, runs=5, dtype="bf16"):
     """Oracle causal attention (restated paged_flash_attention_prefill_f32
     maths, fp32) on bounded samples of one layer: 4 sequences x 256 chunk rows
     on `threads` threads and 1 sequence x 128 rows on one thread, median of
     `runs` each."""
     from oracle import oracle as orc
 
+    code = orc.F32 if dtype == "f32" else orc.BF16
+
     def sample(seqs, rows, seed):
         gen = np.random.default_rng(seed)
         F = KV_HEADS * HEAD_DIM
         pages = math.ceil((prefix + rows) / BLOCK)
         n_pages = pages * seqs
-        kc = orc.from_f32(gen.standard_normal(n_pages * BLOCK * F, np.float32), orc.BF16)
-        vc = orc.from_f32(gen.standard_normal(n_pages * BLOCK * F, np.float32), orc.BF16)
-        q = orc.from_f32(gen.standard_normal((seqs * rows, Q_HEADS * HEAD_DIM), np.float32),
-                         orc.BF16)
+        kc = host_values(orc, gen.standard_normal(n_pages * BLOCK * F, np.float32), code)
+        vc = host_values(orc, gen.standard_normal(n_pages * BLOCK * F, np.float32), code)
+        q = host_values(orc, gen.standard_normal((seqs * rows, Q_HEADS * HEAD_DIM), np.float32),
+                        code)
         table = gen.permutation(n_pages).astype(np.uint32)
         positions = [prefix + i for _ in range(seqs) for i in range(rows)]
         offsets = [s * pages for s in range(seqs) for _ in range(rows)]
-        return orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, orc.BF16, q,
-                             orc.BF16, positions, table, offsets, [pages] * len(positions),
+        return orc.Attention((1, n_pages, BLOCK, KV_HEADS, HEAD_DIM), kc, vc, code, q,
+                             code, positions, table, offsets, [pages] * len(positions),
                              Q_HEADS, 0, 1 / math.sqrt(HEAD_DIM))
 
     big, small = sample(4, 256, 2), sample(1, 128, 3)
@@ -579,7 +619,7 @@ def prefill_cpu_baseline(threads, prefix, runs=5):
         "cpu_model": cpu_model(),
         "median_of": runs,
         "single_thread": {"value": round(flops1 / single_s / 1e9, 3), "unit": "GFLOP/s"},
-        "sample": (f"oracle/oracle.c causal attention over paged bf16 K/V, fp32 accumulate, one "
+        "sample": (f"oracle/oracle.c causal attention over paged {dtype} K/V, fp32 accumulate, one "
                    f"layer: 4 sequences x 256 rows at positions {prefix}..{prefix + 255} "
                    f"({flops / 1e9:.1f} GFLOP) on {threads} threads, and 1 x 128 rows "
                    f"({flops1 / 1e9:.1f} GFLOP) on one; median of {runs} runs each"),
@@ -618,17 +658,19 @@ def bench_config4(args):
     cow_dst = [int(t[full]) for t in tables] if partial else []
 
     ctx = ckv.Context(0, stream=torch.cuda.current_stream())
+    tdt, code, _ = pool_types(args.dtype)
+    es = ELEM_BYTES[args.dtype]
     elems = LAYERS * n_pool * BLOCK * F
     gen = torch.Generator(device=device)
     gen.manual_seed(args.seed)
-    keys = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=gen)
-    values = torch.empty(elems, dtype=torch.bfloat16, device=device).normal_(generator=gen)
-    pool = ckv.Pool(ctx, LAYERS, n_pool, BLOCK, KV_HEADS, HEAD_DIM, ckv.BF16, keys, values)
+    keys = torch.empty(elems, dtype=tdt, device=device).normal_(generator=gen)
+    values = torch.empty(elems, dtype=tdt, device=device).normal_(generator=gen)
+    pool = ckv.Pool(ctx, LAYERS, n_pool, BLOCK, KV_HEADS, HEAD_DIM, code, keys, values)
     rows = S * C
-    q = torch.randn(LAYERS, rows, Q_HEADS * HEAD_DIM, generator=gen, device=device).to(torch.bfloat16)
-    k_new = torch.randn(LAYERS, rows, F, generator=gen, device=device).to(torch.bfloat16)
-    v_new = torch.randn(LAYERS, rows, F, generator=gen, device=device).to(torch.bfloat16)
-    out = torch.empty(LAYERS, rows, Q_HEADS * HEAD_DIM, dtype=torch.bfloat16, device=device)
+    q = torch.randn(LAYERS, rows, Q_HEADS * HEAD_DIM, generator=gen, device=device).to(tdt)
+    k_new = torch.randn(LAYERS, rows, F, generator=gen, device=device).to(tdt)
+    v_new = torch.randn(LAYERS, rows, F, generator=gen, device=device).to(tdt)
+    out = torch.empty(LAYERS, rows, Q_HEADS * HEAD_DIM, dtype=tdt, device=device)
     scale = 1.0 / math.sqrt(HEAD_DIM)
     log(f"config4: prefix {prefix} ({prefix_pages} shared pages, tail copy: {partial}), "
         f"{S} x {C}-row chunks, pool {n_pool} pages x {LAYERS} layers")
@@ -666,9 +708,11 @@ def bench_config4(args):
     flops = prefill_flops(prefix, C, S)
     achieved = flops / avg_s / 1e12
     ms_per_step = elapsed * 1e3 / args.steps
+    peak = MFMA_PEAK_TFLOPS[args.dtype]
     result = {
         "metric": "chunked-prefill attention TFLOP/s (MFMA) + tokens/s, Qwen3-0.6B KV, "
-                  "64 sequences x 512-token chunks over a shared prefix",
+                  "64 sequences x 512-token chunks over a shared prefix"
+                  + ("" if args.dtype == "bf16" else f", {args.dtype} pages"),
         "value": round(LAYERS * flops * args.steps / elapsed / 1e12, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -678,7 +722,7 @@ def bench_config4(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": args.dtype,
         "data": "synthetic N(0,1) K/V/Q, seeded page order",
         "config": {
             "workload": f"config4: {S} sequences share a {prefix}-token prefix (refcounted "
@@ -694,26 +738,28 @@ def bench_config4(args):
             "kernel": "paged_attention_prefill",
             "bound": "mfma",
             "achieved": round(achieved, 2),
-            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+            "frac": round(achieved / peak, 4),
             "traffic": None,
             "avg_launch_us": round(avg_s * 1e6, 2),
             "algorithmic_flops_per_launch": flops,
         },
         "cpu_baseline": None,
     }
+    if args.dtype != "bf16":
+        result["config"]["workload"] += f"; {args.dtype} pages (BASELINE's config is bf16)"
     if args.rope:
         # the fused append's algorithmic bytes: key and value rows read, page
         # rows written, positions and slots
         ms, n = kernels["rope_append"]
-        per = rows * (4 * F * 2 + 8)
+        per = rows * (4 * F * es + 8)
         result["rope_append"] = {"avg_launch_us": round(ms / n * 1e3, 2),
                                  "bytes_per_launch": per,
                                  "achieved_gbs": round(per / (ms / n / 1e3) / 1e9, 2)}
         # the queries' rotation in place: query rows read and written, positions
         ms, n = kernels["rope"]
-        per = rows * (2 * Q_HEADS * HEAD_DIM * 2 + 4)
+        per = rows * (2 * Q_HEADS * HEAD_DIM * es + 4)
         result["rope"] = {"avg_launch_us": round(ms / n * 1e3, 2), "bytes_per_launch": per,
                           "achieved_gbs": round(per / (ms / n / 1e3) / 1e9, 2)}
         result["config"]["workload"] += "; keys rotated inside the append, queries by ckv_rope"
@@ -723,7 +769,7 @@ def bench_config4(args):
     if not args.no_cpu_baseline:
         threads = baseline_threads(args)
         log(f"CPU baseline on {threads} threads")
-        result["cpu_baseline"] = prefill_cpu_baseline(threads, prefix)
+        result["cpu_baseline"] = prefill_cpu_baseline(threads, prefix, dtype=args.dtype)
     return result
 
 
@@ -1108,6 +1154,10 @@ def main():
                     help="config4 shared prefix tokens (2008 leaves a partial tail page, "
                          "so every sequence copies it on write; 2000 does not); spill: the "
                          "prefix moved")
+    ap.add_argument("--dtype", choices=["bf16", "f32"], default="bf16",
+                    help="config2, config3, config4: the pools' element type (bf16, the "
+                         "BASELINE configs; f32, the reference's storage type); an f32 run "
+                         "appends no legs")
     ap.add_argument("--no-legs", action="store_true",
                     help="config3: skip the bounded config 2, 4 and 5 legs the default run "
                          "appends to its line")
@@ -1117,6 +1167,9 @@ def main():
               "(run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
+    if args.dtype != "bf16" and args.workload not in ("config2", "config3", "config4"):
+        print(f"--dtype {args.dtype}: config2, config3 and config4 only", file=sys.stderr)
+        sys.exit(2)
     if args.workload == "config2":
         result = bench_config2(args)
     elif args.workload == "longrow":
@@ -1131,7 +1184,7 @@ def main():
         result = bench_ceiling(args)
     else:
         result = bench_config3(args)
-        if not args.no_legs:
+        if not args.no_legs and args.dtype == "bf16":
             result["legs"] = run_legs(args)
     print(json.dumps(result), flush=True)
 

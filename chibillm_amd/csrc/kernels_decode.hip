@@ -956,7 +956,12 @@ bool aligned16(const void* ptr)
 // (config 3); with 1-2 units per CU, 8 waves is 7-16 % slower. A smaller
 // batch takes the maximum (16, or 8 for wide lanes) so each row streams
 // as fast as one CU allows. Chunks of cut rows take split_waves (a chunk is
-// short, and several of them share a CU). CKV_DECODE_WAVES overrides.
+// short, and several of them share a CU). f32 pages take 4 waves, two
+// workgroups per CU at their two waves per SIMD: on config 2's shape 4, 6 and
+// 8 waves measured 110.3, 120.4 and 117.3 us per launch, on config 3's 839,
+// 872 and 851 us (one box; 2, 3 and 5 waves on another: 115.6, 111.8, 120.2
+// and 958, 863, 858 us).
+// CKV_DECODE_WAVES overrides.
 uint32_t fast_waves(uint32_t group, int dtype, uint32_t units, int cu_count,
                     uint32_t mean_pages, uint32_t split_pages)
 {
@@ -966,6 +971,8 @@ uint32_t fast_waves(uint32_t group, int dtype, uint32_t units, int cu_count,
         if (v >= 1 && v <= (long)limit)
             return (uint32_t)v;
     }
+    if (dtype == CKV_F32)
+        return 4;
     if (split_pages)
         return std::min(limit, split_waves);
     if (limit > 10 && cu_count > 0 && units >= (uint32_t)cu_count)

@@ -167,16 +167,19 @@ def test_ragged_tiles_every_group_size(ctx, group, code):
     pool.close()
 
 
-def test_layer_beyond_4_gib_takes_64_bit_page_addresses(ctx):
-    """A pool whose layer spans more than 4 GiB per tensor (140,000 pages of
-    32 KiB) makes the prefill kernel address pages with 64-bit arithmetic; two
-    sequences whose pages lie above the 4 GiB line (one of them interleaved
-    with pages below it) attend over 1,000 tokens with 200-row chunks, checked
-    against the oracle over a compact copy of the pages used."""
+@pytest.mark.parametrize("code", [orc.BF16, orc.F32])
+def test_layer_beyond_4_gib_takes_64_bit_page_addresses(ctx, code):
+    """A pool whose layer spans more than 4 GiB per tensor (140,000 bf16 or
+    70,000 f32 pages of 32 or 64 KiB) makes the kernels address pages with
+    64-bit arithmetic; two sequences whose pages lie above the 4 GiB line (one
+    of them interleaved with pages below it) attend over 1,000 tokens with
+    200-row chunks through the prefill and decode forms, checked against the
+    oracle over a compact copy of the pages used."""
     H, Hq, n, chunk = 8, 16, 1000, 200
     F = H * D
-    blocks = 140_000
-    assert blocks * 16 * F * 2 > 1 << 32
+    es = 4 if code == orc.F32 else 2
+    blocks = 140_000 * 2 // es
+    assert blocks * 16 * F * es > 1 << 32
     rng = orc.Mt64(77)
     n_pages = pages_for(n)
     high = np.arange(blocks - n_pages, blocks, dtype=np.uint32)  # byte offsets past 4 GiB
@@ -185,37 +188,38 @@ def test_layer_beyond_4_gib_takes_64_bit_page_addresses(ctx):
     mixed[1::2] = np.arange(blocks - 3 * n_pages, blocks - 3 * n_pages + len(mixed[1::2]),
                             dtype=np.uint32)
     tables = [high, mixed]
-    ks = [rng.normal(n * F, orc.BF16).reshape(n, F) for _ in tables]
-    vs = [rng.normal(n * F, orc.BF16).reshape(n, F) for _ in tables]
-    print(f"prefill over a {blocks}-page layer ({blocks * 16 * F * 2 / 2**30:.2f} GiB per tensor)",
-          flush=True)
-    pool, _, _ = new_pool(ctx, (1, blocks, 16, H, D), orc.BF16)
+    ks = [rng.normal(n * F, code).reshape(n, F) for _ in tables]
+    vs = [rng.normal(n * F, code).reshape(n, F) for _ in tables]
+    print(f"prefill over a {blocks}-page layer ({blocks * 16 * F * es / 2**30:.2f} GiB per "
+          f"tensor), dtype {code}", flush=True)
+    pool, _, _ = new_pool(ctx, (1, blocks, 16, H, D), code)
     for t, k, v in zip(tables, ks, vs):
         slots = [orc.slot(t, p, 16) for p in range(n)]
         pool.upload(t, [0] * n, [len(t)] * n, list(range(n)), slots)
-        pool.append(0, to_dev(k, orc.BF16), to_dev(v, orc.BF16))
+        pool.append(0, to_dev(k, code), to_dev(v, code))
     positions = list(range(n - chunk, n)) * 2
     offsets = [0] * chunk + [n_pages] * chunk
     lengths = [n_pages] * (2 * chunk)
     rows = len(positions)
-    q = rng.normal(rows * Hq * D, orc.BF16).reshape(rows, Hq * D)
+    q = rng.normal(rows * Hq * D, code).reshape(rows, Hq * D)
     pool.upload(np.concatenate(tables), offsets, lengths, positions)
     # the oracle over a compact pool: page j of sequence s renumbered s * n_pages + j
-    kc = np.zeros(2 * n_pages * 16 * F, np.uint16)
+    kc = np.zeros(2 * n_pages * 16 * F, ks[0].dtype)
     vc = np.zeros_like(kc)
     for s_i, (k, v) in enumerate(zip(ks, vs)):
         compact = np.arange(s_i * n_pages, (s_i + 1) * n_pages, dtype=np.uint32)
         slots = [orc.slot(compact, p, 16) for p in range(n)]
         orc.store_kv(kc, vc, k, v, slots, 0, 2 * n_pages * 16)
     flat_c = np.arange(2 * n_pages, dtype=np.uint32)
-    expected = orc.Attention((1, 2 * n_pages, 16, H, D), kc, vc, orc.BF16, q, orc.BF16, positions,
+    expected = orc.Attention((1, 2 * n_pages, 16, H, D), kc, vc, code, q, code, positions,
                              flat_c, offsets, lengths, Hq, 0, scale()).online_threads(8)
-    qd = to_dev(q, orc.BF16)
-    for name in ("prefill", "attention"):
+    qd = to_dev(q, code)
+    tol = dict(atol=1e-5, rtol=1e-4) if code == orc.F32 else {}
+    for name in ("prefill", "attention", "decode"):
         out = torch.full_like(qd, float("nan"))
         getattr(pool, name)(0, qd, Hq, scale(), out)
         ctx.sync()
-        assert_close(to_f32(out), expected, what=f"{name} over a 4.6 GB layer")
+        assert_close(to_f32(out), expected, what=f"{name} over a {blocks}-page layer", **tol)
     pool.close()
     del pool
     torch.cuda.empty_cache()

@@ -3,9 +3,10 @@
 // Fast path (head_dim 128, 16-token pages, 1/2/4/8 q heads per KV head; f32
 // pages up to 4): one workgroup per (plan workgroup, kv_head) serves every q
 // head of the KV head's GQA group, so each K/V byte is read once. A wave reads
-// four token rows per load instruction, 16 lanes per row, so lane l holds
-// features 8*(l%16)..8*(l%16)+7 of token 4j + l/16 (16 bytes of a bf16/fp16
-// row, 32 of an f32 row). A score is a dot chain over the lane's 8 features
+// four token rows per load instruction, 16 lanes per row, so lane l holds 8
+// features of token 4j + l/16: 8*(l%16).. of a bf16/fp16 row (16 bytes), or
+// 4*(l%16).. and 64 + 4*(l%16).. of an f32 row (two 16-byte words, each
+// instruction reading 256 contiguous bytes). A score is a dot chain over the lane's 8 features
 // (v_dot2 for 16-bit pairs) followed by a 16-lane DPP all-reduce (4 VALU ops).
 // Each 16-lane row group keeps its own online-softmax state over its tokens;
 // the four states are merged once per segment. Scores are kept in the log2
@@ -41,14 +42,23 @@ __device__ __forceinline__ uint4 load_stream(const void* p)
     return make_uint4(t.x, t.y, t.z, t.w);
 }
 
-// The eight consecutive elements of one K, V or query row a lane of the fast
-// decode holds: one 16-byte word for 16-bit pools, two for f32 (the
-// reference's storage, src/metal/metal_kv_cache.cc:57-69).
+// The eight elements of one K, V or query head row a lane of the fast decode
+// holds: lane part p (of 16) takes the 16 bytes at 16p, features 8p..8p+7 of
+// a 16-bit row; of an f32 row (the reference's storage,
+// src/metal/metal_kv_cache.cc:57-69) also the 16 bytes at 256 + 16p, so its
+// features are 4p..4p+3 and 64+4p..64+4p+3. Either way each 16-byte load
+// instruction of 16 lanes reads 256 contiguous bytes of the row.
 template <int DT>
 struct lane8 {
     static constexpr uint32_t words = DT == CKV_F32 ? 2 : 1;
     static constexpr uint32_t elem = DT == CKV_F32 ? 4 : 2; // bytes per element
+    static constexpr uint32_t stride = 256;                 // bytes between the words
     uint4 w[words];
+    // the head feature of the lane's element i (of 8), for lane part p
+    static __device__ __forceinline__ uint32_t feature(uint32_t p, uint32_t i)
+    {
+        return DT == CKV_F32 ? (i < 4 ? 4 * p + i : 64 + 4 * p + (i - 4)) : 8 * p + i;
+    }
 };
 
 template <int DT>
@@ -57,7 +67,7 @@ __device__ __forceinline__ lane8<DT> load8_stream(const char* p)
     lane8<DT> x;
 #pragma unroll
     for (uint32_t i = 0; i < lane8<DT>::words; ++i)
-        x.w[i] = load_stream(p + 16 * i);
+        x.w[i] = load_stream(p + lane8<DT>::stride * i);
     return x;
 }
 
@@ -67,7 +77,7 @@ __device__ __forceinline__ lane8<DT> load8(const char* p)
     lane8<DT> x;
 #pragma unroll
     for (uint32_t i = 0; i < lane8<DT>::words; ++i)
-        x.w[i] = *reinterpret_cast<const uint4*>(p + 16 * i);
+        x.w[i] = *reinterpret_cast<const uint4*>(p + lane8<DT>::stride * i);
     return x;
 }
 
@@ -76,7 +86,7 @@ __device__ __forceinline__ void store8(char* p, const lane8<DT>& x)
 {
 #pragma unroll
     for (uint32_t i = 0; i < lane8<DT>::words; ++i)
-        *reinterpret_cast<uint4*>(p + 16 * i) = x.w[i];
+        *reinterpret_cast<uint4*>(p + lane8<DT>::stride * i) = x.w[i];
 }
 
 __device__ __forceinline__ float fast_exp2(float x)
@@ -370,7 +380,7 @@ __global__ __launch_bounds__(wide_lanes(G, DT) ? 512 : 1024, wide_lanes(G, DT) ?
         const uint32_t tid = wave * 64 + lane;
         const uint32_t group = lane >> 4;
         const uint32_t part = lane & 15;
-        const uint32_t head_off = kv_head * (D * ES) + part * 8u * ES;
+        const uint32_t head_off = kv_head * (D * ES) + part * 16u; // the lane's first word
         const uint32_t row = e0.x;
         const uint32_t chunk = e0.y;
         const uint32_t position = e0.z;
@@ -389,7 +399,7 @@ __global__ __launch_bounds__(wide_lanes(G, DT) ? 512 : 1024, wide_lanes(G, DT) ?
         row8 qv[G];
 #pragma unroll
         for (int g = 0; g < G; ++g)
-            qv[g] = load8<DT>(q + (((uint64_t)row * q_heads + kv_head * G + g) * D + part * 8) * ES);
+            qv[g] = load8<DT>(q + ((uint64_t)row * q_heads + kv_head * G + g) * D * ES + part * 16);
 
         // ROPE: this lane's 8 features (pairs j0 .. j0 + 7) and their rotation;
         // every lane of the wave takes part in the exchanges. The queries and the
@@ -611,9 +621,11 @@ __global__ __launch_bounds__(wide_lanes(G, DT) ? 512 : 1024, wide_lanes(G, DT) ?
         if (group == 0) {
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                float4* dst = reinterpret_cast<float4*>(lds_acc + (wave * G + g) * D + part * 8);
-                dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-                dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+                float* dst = lds_acc + (wave * G + g) * D;
+                *reinterpret_cast<float4*>(dst + row8::feature(part, 0)) =
+                    make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+                *reinterpret_cast<float4*>(dst + row8::feature(part, 4)) =
+                    make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
                 if (part == 0) {
                     lds_ml[(wave * G + g) * 2] = mx[g];
                     lds_ml[(wave * G + g) * 2 + 1] = den[g];

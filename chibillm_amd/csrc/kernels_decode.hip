@@ -970,9 +970,8 @@ bool aligned16(const void* ptr)
 // as fast as one CU allows. Chunks of cut rows take split_waves (a chunk is
 // short, and several of them share a CU). f32 pages take 4 waves, two
 // workgroups per CU at their two waves per SIMD: on config 2's shape 4, 6 and
-// 8 waves measured 110.3, 120.4 and 117.3 us per launch, on config 3's 839,
-// 872 and 851 us (one box; 2, 3 and 5 waves on another: 115.6, 111.8, 120.2
-// and 958, 863, 858 us).
+// 8 waves measured 90.9, 97.9 and 96.6 us per launch, on config 3's 770, 768
+// and 779 us (one box).
 // CKV_DECODE_WAVES overrides.
 uint32_t fast_waves(uint32_t group, int dtype, uint32_t units, int cu_count,
                     uint32_t mean_pages, uint32_t split_pages)

@@ -10,6 +10,11 @@
       scaled by what the same counter reads for the calibration copy that
       `bench.py --calibrate-copy` runs first: ckv_copy_blocks of 1024 pages of
       32 KiB for keys and values, 64 MiB read and 64 MiB written.
+
+  python -m measure.rocprof_summary counters <prefix>_counter_collection.csv \
+          --kernel <symbol substring>
+      every counter of a --pmc pass, mean per dispatch of one kernel (as the
+      counters report it: summed over the XCDs), as a markdown table
 """
 from __future__ import annotations
 
@@ -105,12 +110,30 @@ def traffic(fetch_csv: str, write_csv: str, kernel: str) -> dict:
     }
 
 
+def counters_markdown(path: str, kernel: str) -> str:
+    names = []
+    with open(path, newline="") as fh:
+        for r in csv.DictReader(fh):
+            if r["Counter_Name"] not in names:
+                names.append(r["Counter_Name"])
+    out = ["| counter | per dispatch |", "|---|---:|"]
+    symbol, dispatches = None, 0
+    for name in names:
+        symbol, dispatches, mean = pick(counter_means(path, name), kernel)
+        out.append(f"| {name} | {mean:,.0f} |")
+    out.insert(0, f"`{short_name(symbol)}`, mean over {dispatches} dispatches\n")
+    return "\n".join(out)
+
+
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
     s = sub.add_parser("stats")
     s.add_argument("csv")
     s.add_argument("--top", type=int, default=8)
+    c = sub.add_parser("counters")
+    c.add_argument("csv")
+    c.add_argument("--kernel", required=True, help="substring of the kernel symbol")
     t = sub.add_parser("traffic")
     t.add_argument("--fetch", required=True)
     t.add_argument("--write", required=True)
@@ -122,6 +145,9 @@ def main(argv=None) -> None:
     args = ap.parse_args(argv)
     if args.cmd == "stats":
         print(stats_markdown(kernel_stats(args.csv), args.top))
+        return
+    if args.cmd == "counters":
+        print(counters_markdown(args.csv, args.kernel))
         return
     entry = traffic(args.fetch, args.write, args.kernel)
     doc = {"kernels": {args.name: entry}, "commands": args.command}

@@ -300,9 +300,11 @@ int ckv_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void
                       const void* queries, size_t q_heads, float scale, void* output, size_t rows);
 /* Prefill form (paged_flash_attention_prefill_f32,
  * src/metal/kernels/attention.metal:246-444): query tiles of consecutive
- * positions of one sequence share every K/V tile; QK^T and PV run on MFMA
- * for 16-bit pools and scale > 0 (other scales take the decode form row by
- * row, with the same results). Same arguments and checks as
+ * positions of one sequence share every K/V tile; QK^T and PV run on the
+ * matrix cores for head_dim 128, 16-token pages, 1, 2, 4 or 8 q heads per kv
+ * head and scale > 0 (bf16/fp16 products for 16-bit pools, exact fp32
+ * products for f32 pools); other geometries and scales take the decode form
+ * row by row, with the same results. Same arguments and checks as
  * ckv_decode_attention. */
 int ckv_prefill_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_heads,
                           float scale, void* output, size_t rows);

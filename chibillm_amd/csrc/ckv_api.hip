@@ -1792,7 +1792,7 @@ int prefill_impl(ckv_pool* pool, size_t layer, const void* queries, size_t q_hea
     ckv_context* ctx = pool->ctx;
     return run_kernel(ctx, "paged_attention_prefill", [&] {
         return launch_prefill(ctx->stream, view, pool->meta, (uint32_t)layer, queries,
-                              (uint32_t)q_heads, scale, output, gate);
+                              (uint32_t)q_heads, scale, output, gate, ctx->cu_count);
     });
 }
 

@@ -331,7 +331,7 @@ uint32_t partial_record_floats(uint32_t head_dim);
 bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, const void* out);
 hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                           const void* q, uint32_t q_heads, float scale, void* out,
-                          const void* gate = nullptr);
+                          const void* gate, int cu_count);
 hipError_t launch_prefill_f32(hipStream_t s, const pool_view& p, const meta_view& m,
                               uint32_t layer, const void* q, uint32_t q_heads, float scale,
                               void* out, const void* gate);

@@ -12,6 +12,9 @@
 // heads of that head's GQA group: 256 query vectors, one q-block of 32 per
 // wave (wave w: head w % G, rows 32*(w / G)..). Every K/V byte of a key block
 // is staged once per workgroup in LDS and used by all 256 query vectors.
+// Launches too small to give every compute unit such a workgroup take four
+// waves per workgroup instead (128/G rows, GQA groups up to 4), two to a
+// compute unit.
 //
 // Per 32-key block (two pages) and wave:
 //   S^T[key][query] = K . Q^T    8 x v_mfma_f32_32x32x16 (A = K rows from
@@ -40,6 +43,7 @@
 // carry finite zeros into P.V.
 #include "ckv_internal.h"
 
+#include <cstdlib>
 #include <type_traits>
 
 namespace ckv {
@@ -58,7 +62,6 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 constexpr uint32_t dim = 128;
 constexpr uint32_t page_tokens = 16;
 constexpr uint32_t block_keys = 32;
-constexpr uint32_t waves = 8;
 
 // K stage: already in the A-operand order of S^T = K.Q^T. Region ks (1 KiB)
 // holds, at 16-byte slot l, what lane l = 32g + n reads for step ks:
@@ -74,7 +77,6 @@ constexpr uint32_t k_stage_bytes = 8 * 1024;
 constexpr uint32_t vg_bytes = 1024 + 64;
 constexpr uint32_t v_stage_bytes = 8 * vg_bytes;
 constexpr uint32_t stage_bytes = k_stage_bytes + v_stage_bytes;
-constexpr uint32_t n_stages = 8; // block kb in stage kb % 8
 
 // The source of masked (past the tile's last position) K and V rows: zeros,
 // so that their zero probabilities multiply finite values.
@@ -95,7 +97,7 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds)
                  "global_load_lds_dwordx4 %1, off\n\t"
                  "s_mov_b32 m0, %0"
                  : "=&s"(saved)
-                 : "v"(src), "s"(lds));
+                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)));
 }
 
 // The same with a scalar 64-bit base and a per-lane 32-bit byte offset: no
@@ -109,7 +111,7 @@ __device__ __forceinline__ void dma16_s(const void* base, uint32_t voff, uint32_
                  "global_load_lds_dwordx4 %1, %2\n\t"
                  "s_mov_b32 m0, %0"
                  : "=&s"(saved)
-                 : "v"(voff), "s"(base), "s"(lds));
+                 : "v"(voff), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds)));
 }
 
 // The K and V DMAs of one block, each with a scalar 64-bit base and a per-lane
@@ -127,14 +129,18 @@ __device__ __forceinline__ void dma16_pair(const void* kb, uint32_t koff, uint32
                  "global_load_lds_dwordx4 %4, %5\n\t"
                  "s_mov_b32 m0, %0"
                  : "=&s"(saved)
-                 : "v"(koff), "s"(kb), "s"(klds), "v"(voff), "s"(vb), "s"(vlds));
+                 : "v"(koff), "s"(kb), "s"(__builtin_amdgcn_readfirstlane(klds)), "v"(voff), "s"(vb),
+                   "s"(__builtin_amdgcn_readfirstlane(vlds)));
 }
 
 // vmcnt wait (the other counters left alone) that lets `outstanding` of this
-// wave's newest DMA loads (two per block: K and V) stay in flight.
+// wave's newest DMA loads (a K and a V load per region it stages per block)
+// stay in flight.
 __device__ __forceinline__ void wait_dma(uint32_t outstanding)
 {
-    if (outstanding >= 4)
+    if (outstanding >= 8)
+        __builtin_amdgcn_s_waitcnt(0x0F78); // vmcnt(8)
+    else if (outstanding >= 4)
         __builtin_amdgcn_s_waitcnt(0x0F74); // vmcnt(4)
     else if (outstanding >= 2)
         __builtin_amdgcn_s_waitcnt(0x0F72); // vmcnt(2)
@@ -238,19 +244,34 @@ __device__ __forceinline__ void exponentiate(f32x16_t& s, float m, float& l, flo
     l += sum;
 }
 
-template <int G, bool F16, bool WIDE>
-__global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
+// W waves per workgroup: 8 (two per SIMD, eight LDS stages), or 4 for
+// launches that would leave compute units idle (one per SIMD, four stages,
+// so two workgroups share a compute unit and twice as many run at once).
+template <int W>
+struct prefill_shape {
+    static constexpr uint32_t stages = W == 8 ? 8 : 4;   // block kb in stage kb % stages
+    static constexpr uint32_t regions = 8 / W;           // K regions and V groups a wave stages
+    static constexpr uint32_t dmas = 2 * regions;        // DMA loads per block and wave
+};
+
+template <int G, bool F16, bool WIDE, int W>
+__global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
     pool_view p, meta_view md, uint32_t layer, const uint16_t* __restrict__ q,
     uint16_t* __restrict__ out, uint32_t q_heads, float c, const uint16_t* __restrict__ gate)
 {
+    static_assert(W == 8 || (W == 4 && G <= 4), "a workgroup covers every q head of its group");
+    using shape = prefill_shape<W>;
+    constexpr uint32_t n_stages = shape::stages;
+    constexpr uint32_t R = shape::regions;
     __shared__ __attribute__((aligned(16))) uint8_t lds[n_stages * stage_bytes];
-    constexpr uint32_t tile_rows = 256 / G;
+    constexpr uint32_t tile_rows = 32 * W / G;
+    constexpr uint32_t subs = 256 / tile_rows; // workgroups per (tile, kv head)
 
     const uint32_t kv_heads = p.kv_heads;
     const uint32_t kvh = blockIdx.x % kv_heads; // consecutive workgroups: different heads/XCDs
     const uint32_t rest = blockIdx.x / kv_heads;
-    const uint32_t sub = rest % G;
-    const uint32_t tile = rest / G;
+    const uint32_t sub = rest % subs;
+    const uint32_t tile = rest / subs;
     // one scalar load gives the tile: first row, rows, first position, table offset
     const uint4 te = *reinterpret_cast<const uint4*>(md.tiles + tile_entry_words * tile);
     const uint32_t count = te.y;
@@ -290,14 +311,20 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
 
     const uint16_t* kbase = static_cast<const uint16_t*>(p.keys) + layer * p.layer_elems + kvh * dim;
     const uint16_t* vbase = static_cast<const uint16_t*>(p.values) + layer * p.layer_elems + kvh * dim;
-    // K DMA: this lane's key (LDS row lane % 32) and features in its wave's region
+    // K DMA: this lane's key (LDS row lane % 32) and features in the wave's
+    // regions wave, wave + W, ...
     const uint32_t k_key = key_row(lane & 31);
-    const uint32_t k_feat = 16 * wave + 8 * (lane >> 5);
-    const uint32_t k_off = ((k_key & 15) * F + k_feat) * 2; // bytes into the key's page
-    const bool k_hi = (lane & 31) >= 16;                    // the key is in the block's second page
-    // V DMA: this lane's key of its wave's group and its LDS read offset
-    const uint32_t vd_key = 16 * (wave >> 2) + 4 * (lane >> 4) + (wave & 3);
-    const uint32_t v_off = ((vd_key & 15) * F + (lane & 15) * 8) * 2;
+    const bool k_hi = (lane & 31) >= 16; // the key is in the block's second page
+    uint32_t k_feat[R], k_off[R], vd_key[R], v_off[R];
+#pragma unroll
+    for (uint32_t r = 0; r < R; ++r) {
+        const uint32_t region = wave + r * W;
+        k_feat[r] = 16 * region + 8 * (lane >> 5);
+        k_off[r] = ((k_key & 15) * F + k_feat[r]) * 2; // bytes into the key's page
+        // V DMA: this lane's key of the wave's group `region`
+        vd_key[r] = 16 * (region >> 2) + 4 * (lane >> 4) + (region & 3);
+        v_off[r] = ((vd_key[r] & 15) * F + (lane & 15) * 8) * 2;
+    }
     const uint32_t vr_off = ((lane & 15) >> 2) * vg_bytes + (lane >> 5) * 512
         + ((lane >> 4) & 1) * 32 + (lane & 3) * 8;
     // DMA operands that do not change from block to block
@@ -331,17 +358,21 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
     // spanning at most 4 GiB takes 32-bit page offsets from its base (two
     // scalar multiplies); a WIDE one 64-bit page addresses.
     auto load_full = [&](uint32_t pg0, uint32_t pg1, uint32_t st) {
-        if constexpr (WIDE) {
-            const uint8_t* k0 = kbytes + pg0 * page_bytes;
-            const uint8_t* k1 = kbytes + pg1 * page_bytes;
-            const uint8_t* vp = vbytes + (wave_u >= 4 ? pg1 : pg0) * page_bytes;
-            dma16((k_hi ? k1 : k0) + k_off, st + wave_u * 1024);
-            dma16_s(vp, v_off, st + k_stage_bytes + wave_u * vg_bytes);
-        } else {
-            const uint32_t off0 = pg0 * page_bytes32, off1 = pg1 * page_bytes32;
-            dma16_pair(kbytes, (k_hi ? off1 : off0) + k_off, st + wave_u * 1024, vbytes,
-                       (wave_u >= 4 ? off1 : off0) + v_off,
-                       st + k_stage_bytes + wave_u * vg_bytes);
+#pragma unroll
+        for (uint32_t r = 0; r < R; ++r) {
+            const uint32_t region = wave_u + r * W;
+            if constexpr (WIDE) {
+                const uint8_t* k0 = kbytes + pg0 * page_bytes;
+                const uint8_t* k1 = kbytes + pg1 * page_bytes;
+                const uint8_t* vp = vbytes + (region >= 4 ? pg1 : pg0) * page_bytes;
+                dma16((k_hi ? k1 : k0) + k_off[r], st + region * 1024);
+                dma16_s(vp, v_off[r], st + k_stage_bytes + region * vg_bytes);
+            } else {
+                const uint32_t off0 = pg0 * page_bytes32, off1 = pg1 * page_bytes32;
+                dma16_pair(kbytes, (k_hi ? off1 : off0) + k_off[r], st + region * 1024, vbytes,
+                           (region >= 4 ? off1 : off0) + v_off[r],
+                           st + k_stage_bytes + region * vg_bytes);
+            }
         }
     };
     // load_block for a block whose keys are all in the tile and whose
@@ -363,11 +394,17 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
         } else {
             const uint8_t* k0 = kbytes + pg0 * page_bytes;
             const uint8_t* k1 = kbytes + pg1 * page_bytes;
-            const uint8_t* vp = vbytes + (wave_u >= 4 ? pg1 : pg0) * page_bytes;
-            const uint8_t* ksrc = key0 + k_key <= pos_last ? (k_hi ? k1 : k0) + k_off : zbytes + k_feat * 2;
-            dma16(ksrc, st + wave_u * 1024);
-            const uint8_t* vsrc = key0 + vd_key <= pos_last ? vp + v_off : zbytes + (lane & 15) * 16;
-            dma16(vsrc, st + k_stage_bytes + wave_u * vg_bytes);
+#pragma unroll
+            for (uint32_t r = 0; r < R; ++r) {
+                const uint32_t region = wave_u + r * W;
+                const uint8_t* vp = vbytes + (region >= 4 ? pg1 : pg0) * page_bytes;
+                const uint8_t* ksrc = key0 + k_key <= pos_last ? (k_hi ? k1 : k0) + k_off[r]
+                                                               : zbytes + k_feat[r] * 2;
+                dma16(ksrc, st + region * 1024);
+                const uint8_t* vsrc = key0 + vd_key[r] <= pos_last ? vp + v_off[r]
+                                                                   : zbytes + (lane & 15) * 16;
+                dma16(vsrc, st + k_stage_bytes + region * vg_bytes);
+            }
         }
     };
 
@@ -469,8 +506,9 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
     // This wave's loads newer than block b once it has issued block `last`.
     auto newer = [&](uint32_t b, uint32_t last) {
         const uint32_t top = min(last, n_blocks - 1);
-        return top > b ? 2 * (top - b) : 0u;
+        return top > b ? shape::dmas * (top - b) : 0u;
     };
+    if constexpr (W == 8) {
     // Blocks are loaded four ahead and published two at a time: the barrier
     // after an odd iteration kb waits for blocks kb + 1 and kb + 2, which the
     // next two iterations read. Block b is loaded in iteration b - 4 into the
@@ -547,6 +585,45 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
     }
     for (; kb < n_blocks; ++kb)
         iteration(kb, no {}, no {});
+    } else {
+        // Four stages, loads two blocks ahead, a barrier after every block:
+        // block b is loaded in iteration b - 2 into the stage of block b - 4,
+        // whose last read (V, iteration b - 3) precedes the barrier after
+        // iteration b - 3; the barrier after iteration kb waits for block
+        // kb + 1, the next iteration's K.
+        fetch_pages(0);
+        load_block(0);
+        if (1 < n_blocks)
+            load_block(1);
+        wait_dma(0);
+        __syncthreads();
+        {
+            if (2 < n_blocks)
+                load_block(2);
+            uint4 ka[8];
+            read_k(0, ka);
+            qk(ka);
+            stats(0, false);
+            rescale();
+        }
+        for (uint32_t kb = 1; kb < n_blocks; ++kb) {
+            if (kb + 2 < n_blocks)
+                load_block(kb + 2);
+            uint4 ka[8], va[4][2];
+            uint4 pt[2];
+            read_k(kb, ka);
+            __builtin_amdgcn_sched_barrier(0);
+            probabilities(pt); // vector: block kb - 1
+            qk(ka);            // matrix: block kb
+            read_v(kb - 1, va);
+            pv(va, pt); // matrix: block kb - 1
+            const bool grew = stats(kb, false);
+            wait_dma(newer(kb + 1, kb + 2));
+            __syncthreads();
+            if (grew)
+                rescale();
+        }
+    }
     // the last block's probabilities and product
     {
         uint4 va[4][2];
@@ -580,31 +657,54 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_kernel(
         }
 }
 
-template <int G>
-hipError_t launch_g(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
-                    const void* q, uint32_t q_heads, float c, void* out, uint32_t grid,
-                    const void* gate)
+template <int G, int W>
+hipError_t launch_gw(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
+                     const void* q, uint32_t q_heads, float c, void* out, const void* gate)
 {
+    const uint64_t grid = (uint64_t)m.n_tiles * (256 / (32 * W / G)) * p.kv_heads;
+    if (!grid)
+        return hipSuccess;
+    if (grid > 0x7FFFFFFFull)
+        return hipErrorInvalidValue;
     const auto* qq = static_cast<const uint16_t*>(q);
     auto* oo = static_cast<uint16_t*>(out);
     const auto* gg = static_cast<const uint16_t*>(gate);
     // a layer's K (or V) span beyond 4 GiB needs 64-bit page addresses
     const bool wide = p.layer_elems * 2 > 0xFFFFFFFFull;
     const bool f16 = p.dtype == CKV_F16;
-    const dim3 g(grid), b(64 * waves);
+    const dim3 g((uint32_t)grid), b(64 * W);
     if (f16 && wide)
-        hipLaunchKernelGGL((prefill_kernel<G, true, true>), g, b, 0, s, p, m, layer, qq, oo,
+        hipLaunchKernelGGL((prefill_kernel<G, true, true, W>), g, b, 0, s, p, m, layer, qq, oo,
                            q_heads, c, gg);
     else if (f16)
-        hipLaunchKernelGGL((prefill_kernel<G, true, false>), g, b, 0, s, p, m, layer, qq, oo,
+        hipLaunchKernelGGL((prefill_kernel<G, true, false, W>), g, b, 0, s, p, m, layer, qq, oo,
                            q_heads, c, gg);
     else if (wide)
-        hipLaunchKernelGGL((prefill_kernel<G, false, true>), g, b, 0, s, p, m, layer, qq, oo,
+        hipLaunchKernelGGL((prefill_kernel<G, false, true, W>), g, b, 0, s, p, m, layer, qq, oo,
                            q_heads, c, gg);
     else
-        hipLaunchKernelGGL((prefill_kernel<G, false, false>), g, b, 0, s, p, m, layer, qq, oo,
+        hipLaunchKernelGGL((prefill_kernel<G, false, false, W>), g, b, 0, s, p, m, layer, qq, oo,
                            q_heads, c, gg);
     return hipGetLastError();
+}
+
+// A launch of 8-wave workgroups (one per compute unit: their LDS stages take
+// 135 KB) that would not give every compute unit one takes 4-wave workgroups
+// instead: twice as many, two to a compute unit (GQA groups up to 4).
+// CKV_PREFILL_WAVES (4 or 8) overrides.
+template <int G>
+hipError_t launch_g(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
+                    const void* q, uint32_t q_heads, float c, void* out, const void* gate,
+                    int cu_count)
+{
+    bool small = cu_count > 0 && (uint64_t)m.n_tiles * G * p.kv_heads < (uint64_t)cu_count;
+    if (const char* forced = std::getenv("CKV_PREFILL_WAVES"))
+        small = std::strtol(forced, nullptr, 10) == 4;
+    if constexpr (G <= 4) {
+        if (small)
+            return launch_gw<G, 4>(s, p, m, layer, q, q_heads, c, out, gate);
+    }
+    return launch_gw<G, 8>(s, p, m, layer, q, q_heads, c, out, gate);
 }
 
 bool aligned16(const void* ptr)
@@ -628,26 +728,20 @@ bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, cons
 
 hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                           const void* q, uint32_t q_heads, float scale, void* out,
-                          const void* gate)
+                          const void* gate, int cu_count)
 {
     if (p.dtype == CKV_F32)
         return launch_prefill_f32(s, p, m, layer, q, q_heads, scale, out, gate);
-    const uint32_t group = q_heads / p.kv_heads;
-    const uint64_t grid = (uint64_t)m.n_tiles * group * p.kv_heads;
-    if (!grid)
-        return hipSuccess;
-    if (grid > 0x7FFFFFFFull)
-        return hipErrorInvalidValue;
     const float c = scale * log2e;
-    switch (group) {
+    switch (q_heads / p.kv_heads) {
     case 1:
-        return launch_g<1>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
+        return launch_g<1>(s, p, m, layer, q, q_heads, c, out, gate, cu_count);
     case 2:
-        return launch_g<2>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
+        return launch_g<2>(s, p, m, layer, q, q_heads, c, out, gate, cu_count);
     case 4:
-        return launch_g<4>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
+        return launch_g<4>(s, p, m, layer, q, q_heads, c, out, gate, cu_count);
     case 8:
-        return launch_g<8>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
+        return launch_g<8>(s, p, m, layer, q, q_heads, c, out, gate, cu_count);
     default:
         return hipErrorInvalidValue;
     }

@@ -111,14 +111,19 @@ def test_shared_prefix_chunks_with_copy_on_write_tail(ctx, prefix):
 RAGGED = [(0, 1), (0, 40), (5, 300), (100, 33), (16, 257), (1000, 64), (700, 1), (63, 2)]
 
 
+@pytest.mark.parametrize("waves", [None, "8"])
 @pytest.mark.parametrize("code", [orc.BF16, orc.F16, orc.F32])
 @pytest.mark.parametrize("group", [1, 2, 4, 8])
-def test_ragged_tiles_every_group_size(ctx, group, code):
+def test_ragged_tiles_every_group_size(ctx, group, code, waves, monkeypatch):
     """Every route (auto, prefill, decode form) against the oracle; f32 pages
     (the reference's storage dtype, fp32 products on the matrix cores) within
     1e-5 abs + 1e-4 rel, and their prefill takes the MFMA kernel (one
-    paged_attention_prefill launch)."""
-    print(f"ragged tiles group {group} dtype {code}", flush=True)
+    paged_attention_prefill launch). This batch is too small to give every
+    compute unit an 8-wave workgroup, so 16-bit pools with GQA groups up to 4
+    take 4-wave workgroups by default; waves "8" forces the 8-wave kernel."""
+    if waves:
+        monkeypatch.setenv("CKV_PREFILL_WAVES", waves)
+    print(f"ragged tiles group {group} dtype {code} waves {waves}", flush=True)
     H = 2
     Hq = H * group
     F = H * D

@@ -1066,6 +1066,10 @@ int ckv_pool_destroy(ckv_pool* pool)
         (void)dev_free(ctx, pool->d_partials);
     if (pool->d_arrivals)
         (void)dev_free(ctx, pool->d_arrivals);
+    if (pool->d_pre_records)
+        (void)dev_free(ctx, pool->d_pre_records);
+    if (pool->d_pre_arrivals)
+        (void)dev_free(ctx, pool->d_pre_arrivals);
     if (pool->d_pairs)
         (void)dev_free(ctx, pool->d_pairs);
     if (pool->d_seq)
@@ -1790,9 +1794,36 @@ int prefill_impl(ckv_pool* pool, size_t layer, const void* queries, size_t q_hea
         || !(scale > 0.0f))
         return run_decode(pool, layer, queries, q_heads, scale, output, gate);
     ckv_context* ctx = pool->ctx;
+    const prefill_shape_info plan = prefill_plan(view, pool->meta, (uint32_t)q_heads, ctx->cu_count);
+    prefill_split split { nullptr, nullptr, plan.n_split };
+    if (plan.n_split > 1) {
+        int status = ensure_device(ctx, &pool->d_pre_records, &pool->d_pre_records_floats,
+                                   (size_t)plan.records_floats, "prefill split records");
+        if (status)
+            return status;
+        if (plan.counters > pool->d_pre_arrivals_words) {
+            status = ensure_device(ctx, &pool->d_pre_arrivals, &pool->d_pre_arrivals_words,
+                                   (size_t)plan.counters, "prefill split counters");
+            if (status)
+                return status;
+            status = run_kernel(ctx, "fill", [&] {
+                return launch_fill(ctx->stream, pool->d_pre_arrivals, 0,
+                                   (uint32_t)pool->d_pre_arrivals_words);
+            });
+            if (status) {
+                // not known to be zero: allocate and clear again next time
+                (void)dev_free(ctx, pool->d_pre_arrivals);
+                pool->d_pre_arrivals = nullptr;
+                pool->d_pre_arrivals_words = 0;
+                return status;
+            }
+        }
+        split.records = pool->d_pre_records;
+        split.arrivals = pool->d_pre_arrivals;
+    }
     return run_kernel(ctx, "paged_attention_prefill", [&] {
         return launch_prefill(ctx->stream, view, pool->meta, (uint32_t)layer, queries,
-                              (uint32_t)q_heads, scale, output, gate, ctx->cu_count);
+                              (uint32_t)q_heads, scale, output, gate, plan, split);
     });
 }
 

@@ -76,6 +76,19 @@ struct split_scratch {
 
 constexpr size_t tile_entry_words = 4;
 
+// Device scratch of a prefill launch whose tiles' key blocks are split
+// between workgroups: a record [max, denominator, 0, 0, acc[128]] per (share,
+// query vector), and an arrival counter per (tile, workgroup row range, kv
+// head), zero before a launch and left zero by it. n_split = 1: no split.
+struct prefill_split {
+    float* records;
+    uint32_t* arrivals;
+    uint32_t n_split;
+};
+constexpr uint32_t prefill_record_floats = 128 + 4;
+constexpr uint32_t split_min_blocks = 4; // 32-key blocks a share attends at least
+constexpr uint32_t split_max = 8;        // shares a tile's keys are split into at most
+
 // Largest query tile, in rows (positions): the prefill kernel covers a tile
 // with G workgroups of 256/G rows for GQA group size G.
 constexpr uint32_t prefill_tile_rows = 256;
@@ -229,6 +242,10 @@ struct ckv_pool {
     size_t d_partials_bytes = 0;
     uint32_t* d_arrivals = nullptr; // the fast decode's arrival counters (zero between launches)
     size_t d_arrivals_words = 0;
+    float* d_pre_records = nullptr; // the split prefill's records
+    size_t d_pre_records_floats = 0;
+    uint32_t* d_pre_arrivals = nullptr; // its arrival counters (zero between launches)
+    size_t d_pre_arrivals_words = 0;
     uint32_t* d_pairs = nullptr; // block-id pairs / patch pairs
     size_t d_pairs_words = 0;
     char* d_spill = nullptr; // staging of checkpoint export/import
@@ -329,9 +346,21 @@ uint32_t partial_record_floats(uint32_t head_dim);
 // aligned pools, queries and output; bf16/fp16 products on
 // v_mfma_f32_32x32x16, f32 ones on v_mfma_f32_32x32x2_f32.
 bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, const void* out);
+// How a 16-bit prefill launch runs: workgroup waves (8, or 4 when 8-wave
+// workgroups would not give every compute unit one) and the key split of the
+// 4-wave form (1: none), with the records and counters that split needs.
+struct prefill_shape_info {
+    uint32_t waves;
+    uint32_t n_split;
+    uint64_t records_floats;
+    uint64_t counters;
+};
+prefill_shape_info prefill_plan(const pool_view& p, const meta_view& m, uint32_t q_heads,
+                                int cu_count);
 hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                           const void* q, uint32_t q_heads, float scale, void* out,
-                          const void* gate, int cu_count);
+                          const void* gate, const prefill_shape_info& plan,
+                          prefill_split split);
 hipError_t launch_prefill_f32(hipStream_t s, const pool_view& p, const meta_view& m,
                               uint32_t layer, const void* q, uint32_t q_heads, float scale,
                               void* out, const void* gate);

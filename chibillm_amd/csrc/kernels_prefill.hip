@@ -43,6 +43,7 @@
 // carry finite zeros into P.V.
 #include "ckv_internal.h"
 
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -148,6 +149,46 @@ __device__ __forceinline__ void wait_dma(uint32_t outstanding)
         __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
 }
 
+// The split tiles' records pass between workgroups as the decode's split-K
+// partial records do (kernels_decode.hip), at 16 bytes per access: buffer
+// stores and loads with the sc1 cache policy, the same instructions at the
+// same policy that LLVM emits for relaxed agent-scope atomic stores and loads
+// on gfx950 (global/buffer_store/load sc1: the store writes through, the
+// load misses any L2 line that could be stale, so every XCD sees the data in
+// memory without an L2 writeback); a wait for the stores' completion before
+// one thread's relaxed agent-scope fetch-add counts the share in; the loads
+// of the share that arrives last are issued after that fetch-add returns.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "kernels_prefill.hip's split-key handoff relies on gfx950's memory system; build for gfx950"
+#endif
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int cache_sc1 = 16; // the buffer builtins' cache-policy operand: sc1
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t record_rsrc(float* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void agent_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, float a,
+                                             float b, float c, float d)
+{
+    const u32x4_t v = { __float_as_uint(a), __float_as_uint(b), __float_as_uint(c),
+                        __float_as_uint(d) };
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, cache_sc1);
+}
+
+__device__ __forceinline__ u32x4_t agent_load4(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, cache_sc1);
+}
+
+// Waits until every vector memory access this wave issued (stores included)
+// has completed; a compiler barrier too.
+__device__ __forceinline__ void wait_vector_memory()
+{
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 __device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* ptr)
 {
     const uint64_t v = (uint64_t)(uintptr_t)ptr;
@@ -231,9 +272,12 @@ __device__ __forceinline__ float block_max(const f32x16_t& s)
 // Probabilities of one q-block against the running maximum m (raw q.k
 // units; c = scale * log2(e) so every exponential is one exp2), added to
 // this lane's share of the denominator.
+template <bool GUARD>
 __device__ __forceinline__ void exponentiate(f32x16_t& s, float m, float& l, float c)
 {
-    const float mc = m * c;
+    // GUARD: a workgroup that attends only part of the keys may have seen no
+    // unmasked key of a query yet (m = -inf); its probabilities are then 0
+    const float mc = GUARD && m == -__builtin_inff() ? 0.0f : m * c;
     s[0] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[0], c, -mc));
     float sum = s[0]; // an exponential is never -0, so this is 0 + s[0] exactly
 #pragma unroll
@@ -257,9 +301,12 @@ struct prefill_shape {
 template <int G, bool F16, bool WIDE, int W>
 __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
     pool_view p, meta_view md, uint32_t layer, const uint16_t* __restrict__ q,
-    uint16_t* __restrict__ out, uint32_t q_heads, float c, const uint16_t* __restrict__ gate)
+    uint16_t* __restrict__ out, uint32_t q_heads, float c, const uint16_t* __restrict__ gate,
+    prefill_split split_scratch)
 {
     static_assert(W == 8 || (W == 4 && G <= 4), "a workgroup covers every q head of its group");
+    // 4-wave workgroups may split a tile's key blocks between workgroups
+    constexpr bool SPLIT = W == 4;
     using shape = prefill_shape<W>;
     constexpr uint32_t n_stages = shape::stages;
     constexpr uint32_t R = shape::regions;
@@ -269,7 +316,9 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
 
     const uint32_t kv_heads = p.kv_heads;
     const uint32_t kvh = blockIdx.x % kv_heads; // consecutive workgroups: different heads/XCDs
-    const uint32_t rest = blockIdx.x / kv_heads;
+    const uint32_t n_split = SPLIT ? split_scratch.n_split : 1;
+    const uint32_t rest = blockIdx.x / kv_heads / n_split;
+    const uint32_t part = blockIdx.x / kv_heads % n_split; // this workgroup's share of the keys
     const uint32_t sub = rest % subs;
     const uint32_t tile = rest / subs;
     // one scalar load gives the tile: first row, rows, first position, table offset
@@ -284,6 +333,19 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
     const uint32_t pos_last = pos0 + nrows - 1;
     const uint32_t* table = md.table + te.w;
     const uint32_t n_blocks = pos_last / block_keys + 1;
+    // Key blocks [kb_begin, kb_end) of this workgroup: the tile's blocks cut
+    // into n_parts ranges of at least split_min_blocks (uniform over the tile's
+    // workgroups), range `part`.
+    uint32_t n_parts = 1, kb_begin = 0, kb_end = n_blocks;
+    if constexpr (SPLIT) {
+        n_parts = min(n_split, max(1u, n_blocks / split_min_blocks));
+        if (part >= n_parts)
+            return;
+        kb_begin = part * n_blocks / n_parts;
+        kb_end = (part + 1) * n_blocks / n_parts;
+    } else {
+        (void)part;
+    }
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63, wave = tid >> 6;
@@ -460,7 +522,7 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
             }
     };
     auto probabilities = [&](uint4 (&pt)[2]) {
-        exponentiate(sp, m, l, c);
+        exponentiate<SPLIT>(sp, m, l, c);
 #pragma unroll
         for (int h = 0; h < 2; ++h)
             pt[h] = make_uint4(pack2<F16>(sp[8 * h + 0], sp[8 * h + 1]),
@@ -494,7 +556,9 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
     };
     auto rescale = [&]() {
         const float m_new = fmaxf(m, mx);
-        const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c); // 0 at the start
+        float alpha = __builtin_amdgcn_exp2f((m - m_new) * c); // 0 at the start
+        if constexpr (SPLIT)
+            alpha = m_new == -__builtin_inff() ? 1.0f : alpha; // nothing attended yet
         l *= alpha;
         m = m_new;
         m_limit = m_new + rescale_raw;
@@ -505,7 +569,7 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
 
     // This wave's loads newer than block b once it has issued block `last`.
     auto newer = [&](uint32_t b, uint32_t last) {
-        const uint32_t top = min(last, n_blocks - 1);
+        const uint32_t top = min(last, kb_end - 1);
         return top > b ? shape::dmas * (top - b) : 0u;
     };
     if constexpr (W == 8) {
@@ -591,23 +655,23 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
         // whose last read (V, iteration b - 3) precedes the barrier after
         // iteration b - 3; the barrier after iteration kb waits for block
         // kb + 1, the next iteration's K.
-        fetch_pages(0);
-        load_block(0);
-        if (1 < n_blocks)
-            load_block(1);
+        fetch_pages(kb_begin);
+        load_block(kb_begin);
+        if (kb_begin + 1 < kb_end)
+            load_block(kb_begin + 1);
         wait_dma(0);
         __syncthreads();
         {
-            if (2 < n_blocks)
-                load_block(2);
+            if (kb_begin + 2 < kb_end)
+                load_block(kb_begin + 2);
             uint4 ka[8];
-            read_k(0, ka);
+            read_k(kb_begin, ka);
             qk(ka);
-            stats(0, false);
+            stats(kb_begin, false);
             rescale();
         }
-        for (uint32_t kb = 1; kb < n_blocks; ++kb) {
-            if (kb + 2 < n_blocks)
+        for (uint32_t kb = kb_begin + 1; kb < kb_end; ++kb) {
+            if (kb + 2 < kb_end)
                 load_block(kb + 2);
             uint4 ka[8], va[4][2];
             uint4 pt[2];
@@ -629,13 +693,94 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
         uint4 va[4][2];
         uint4 pt[2];
         probabilities(pt);
-        read_v(n_blocks - 1, va);
+        read_v(kb_end - 1, va);
         pv(va, pt);
+    }
+
+    float lt = l + __shfl_xor(l, 32); // the query's denominator (both lane halves)
+    if (SPLIT && n_parts > 1) {
+        // A share of a split tile: its record is 33 chunks of 4 floats per
+        // query vector, chunk 0 = [max, denominator, 0, 0] and chunk 1 + j =
+        // acc[4j .. 4j + 3], chunk-major with the workgroup's 128 query vectors
+        // consecutive, so the 32 lanes of a wave half fill 512 contiguous
+        // bytes per access. The share that arrives last folds every share's
+        // record, its own included, in share order (the result does not
+        // depend on the order of arrival), with weights 2^(m_s - M).
+        const uint32_t pair = (tile * subs + sub) * kv_heads + kvh;
+        const uint32_t qv = wave * 32 + n; // this lane's query vector in the workgroup
+        constexpr uint32_t QV = 32 * W, chunks = prefill_record_floats / 4;
+        const __amdgpu_buffer_rsrc_t rs = record_rsrc(
+            split_scratch.records + (uint64_t)pair * n_split * (chunks * QV * 4),
+            n_split * chunks * QV * 16);
+        auto off = [&](uint32_t share, uint32_t chunk) {
+            return ((share * chunks + chunk) * QV + qv) * 16u;
+        };
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int quad = 0; quad < 4; ++quad) {
+                const f32x16_t& acc = o[mt];
+                agent_store4(rs, off(part, 1 + 8 * mt + 2 * quad + g), acc[4 * quad],
+                             acc[4 * quad + 1], acc[4 * quad + 2], acc[4 * quad + 3]);
+            }
+        if (g == 0)
+            agent_store4(rs, off(part, 0), m, lt, 0.0f, 0.0f);
+        wait_vector_memory();
+        __syncthreads(); // also: every wave is past its LDS reads
+        uint32_t* const last_flag = reinterpret_cast<uint32_t*>(lds);
+        if (tid == 0) {
+            const uint32_t before = __hip_atomic_fetch_add(split_scratch.arrivals + pair, 1u,
+                                                           __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t last = before == n_parts - 1;
+            if (last)
+                __hip_atomic_store(split_scratch.arrivals + pair, 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            *last_flag = last;
+        }
+        __syncthreads();
+        if (!*last_flag)
+            return;
+        float M = -__builtin_inff();
+#pragma unroll
+        for (uint32_t s = 0; s < split_max; ++s) // every share's head in one round trip
+            M = fmaxf(M, __uint_as_float(agent_load4(rs, off(min(s, n_parts - 1), 0))[0]));
+        // M is finite for a valid row: the tile's first share attends key 0
+        auto weight = [&](float ms) {
+            return ms == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f((ms - M) * c);
+        };
+        lt = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+            o[mt] = f32x16_t {};
+        for (uint32_t s = 0; s < n_parts; s += 2) { // two shares per round trip
+            const uint32_t s1 = min(s + 1, n_parts - 1);
+            u32x4_t ha = agent_load4(rs, off(s, 0)), hb = agent_load4(rs, off(s1, 0));
+            u32x4_t va[16], vb[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                va[j] = agent_load4(rs, off(s, 1 + 2 * j + g));
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                vb[j] = agent_load4(rs, off(s1, 1 + 2 * j + g));
+            const float wa = weight(__uint_as_float(ha[0]));
+            const float wb = s + 1 < n_parts ? weight(__uint_as_float(hb[0])) : 0.0f;
+            lt += __uint_as_float(ha[1]) * wa;
+            lt += __uint_as_float(hb[1]) * wb;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) // chunk 1 + 2j + g = features 32mt + 8quad + 4g + e
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float acc = o[j / 4][4 * (j % 4) + e];
+                    acc += __uint_as_float(va[j][e]) * wa;
+                    o[j / 4][4 * (j % 4) + e] = acc + __uint_as_float(vb[j][e]) * wb;
+                }
+        }
     }
 
     if (!active || !valid)
         return;
-    const float inv = 1.0f / (l + __shfl_xor(l, 32));
+    const float inv = 1.0f / lt;
     uint16_t* dst = out + qoff;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
@@ -659,9 +804,11 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
 
 template <int G, int W>
 hipError_t launch_gw(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
-                     const void* q, uint32_t q_heads, float c, void* out, const void* gate)
+                     const void* q, uint32_t q_heads, float c, void* out, const void* gate,
+                     prefill_split split)
 {
-    const uint64_t grid = (uint64_t)m.n_tiles * (256 / (32 * W / G)) * p.kv_heads;
+    const uint64_t grid = (uint64_t)m.n_tiles * (256 / (32 * W / G)) * p.kv_heads
+        * (W == 4 ? split.n_split : 1);
     if (!grid)
         return hipSuccess;
     if (grid > 0x7FFFFFFFull)
@@ -675,36 +822,30 @@ hipError_t launch_gw(hipStream_t s, const pool_view& p, const meta_view& m, uint
     const dim3 g((uint32_t)grid), b(64 * W);
     if (f16 && wide)
         hipLaunchKernelGGL((prefill_kernel<G, true, true, W>), g, b, 0, s, p, m, layer, qq, oo,
-                           q_heads, c, gg);
+                           q_heads, c, gg, split);
     else if (f16)
         hipLaunchKernelGGL((prefill_kernel<G, true, false, W>), g, b, 0, s, p, m, layer, qq, oo,
-                           q_heads, c, gg);
+                           q_heads, c, gg, split);
     else if (wide)
         hipLaunchKernelGGL((prefill_kernel<G, false, true, W>), g, b, 0, s, p, m, layer, qq, oo,
-                           q_heads, c, gg);
+                           q_heads, c, gg, split);
     else
         hipLaunchKernelGGL((prefill_kernel<G, false, false, W>), g, b, 0, s, p, m, layer, qq, oo,
-                           q_heads, c, gg);
+                           q_heads, c, gg, split);
     return hipGetLastError();
 }
 
-// A launch of 8-wave workgroups (one per compute unit: their LDS stages take
-// 135 KB) that would not give every compute unit one takes 4-wave workgroups
-// instead: twice as many, two to a compute unit (GQA groups up to 4).
-// CKV_PREFILL_WAVES (4 or 8) overrides.
 template <int G>
 hipError_t launch_g(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                     const void* q, uint32_t q_heads, float c, void* out, const void* gate,
-                    int cu_count)
+                    const prefill_shape_info& plan, prefill_split split)
 {
-    bool small = cu_count > 0 && (uint64_t)m.n_tiles * G * p.kv_heads < (uint64_t)cu_count;
-    if (const char* forced = std::getenv("CKV_PREFILL_WAVES"))
-        small = std::strtol(forced, nullptr, 10) == 4;
     if constexpr (G <= 4) {
-        if (small)
-            return launch_gw<G, 4>(s, p, m, layer, q, q_heads, c, out, gate);
+        if (plan.waves == 4)
+            return launch_gw<G, 4>(s, p, m, layer, q, q_heads, c, out, gate, split);
     }
-    return launch_gw<G, 8>(s, p, m, layer, q, q_heads, c, out, gate);
+    split.n_split = 1;
+    return launch_gw<G, 8>(s, p, m, layer, q, q_heads, c, out, gate, split);
 }
 
 bool aligned16(const void* ptr)
@@ -726,22 +867,59 @@ bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, cons
     return aligned16(p.keys) && aligned16(p.values) && aligned16(q) && aligned16(out);
 }
 
+// A launch of 8-wave workgroups (one per compute unit: their LDS stages take
+// 135 KB) that would not give every compute unit one takes 4-wave workgroups
+// instead, two to a compute unit (GQA groups up to 4); if those still leave
+// compute units idle, each tile's key blocks are split between as many
+// workgroups as fill them (at most split_max, each attending at least
+// split_min_blocks blocks; the kernel takes fewer for short tiles).
+// CKV_PREFILL_WAVES (4 or 8) and CKV_PREFILL_SPLIT override.
+prefill_shape_info prefill_plan(const pool_view& p, const meta_view& m, uint32_t q_heads,
+                                int cu_count)
+{
+    prefill_shape_info plan { 8, 1, 0, 0 };
+    const uint32_t group = p.kv_heads ? q_heads / p.kv_heads : 0;
+    if (p.dtype == CKV_F32 || group == 0 || group > 4)
+        return plan;
+    const uint64_t grid8 = (uint64_t)m.n_tiles * group * p.kv_heads;
+    bool small = cu_count > 0 && grid8 < (uint64_t)cu_count;
+    if (const char* forced = std::getenv("CKV_PREFILL_WAVES"))
+        small = std::strtol(forced, nullptr, 10) == 4;
+    if (!small)
+        return plan;
+    plan.waves = 4;
+    const uint64_t pairs = grid8 * 2; // 4-wave workgroups
+    uint64_t split = pairs && cu_count > 0 ? 2 * (uint64_t)cu_count / pairs : 1;
+    if (const char* forced = std::getenv("CKV_PREFILL_SPLIT"))
+        split = (uint64_t)std::max(1L, std::strtol(forced, nullptr, 10));
+    plan.n_split = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(split, 1), split_max);
+    if (plan.n_split > 1) {
+        plan.records_floats = pairs * plan.n_split * 128 * prefill_record_floats;
+        plan.counters = pairs;
+    }
+    return plan;
+}
+
 hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                           const void* q, uint32_t q_heads, float scale, void* out,
-                          const void* gate, int cu_count)
+                          const void* gate, const prefill_shape_info& plan,
+                          prefill_split split)
 {
     if (p.dtype == CKV_F32)
         return launch_prefill_f32(s, p, m, layer, q, q_heads, scale, out, gate);
+    if (plan.n_split > 1 && (!split.records || !split.arrivals))
+        return hipErrorInvalidValue;
+    split.n_split = plan.n_split;
     const float c = scale * log2e;
     switch (q_heads / p.kv_heads) {
     case 1:
-        return launch_g<1>(s, p, m, layer, q, q_heads, c, out, gate, cu_count);
+        return launch_g<1>(s, p, m, layer, q, q_heads, c, out, gate, plan, split);
     case 2:
-        return launch_g<2>(s, p, m, layer, q, q_heads, c, out, gate, cu_count);
+        return launch_g<2>(s, p, m, layer, q, q_heads, c, out, gate, plan, split);
     case 4:
-        return launch_g<4>(s, p, m, layer, q, q_heads, c, out, gate, cu_count);
+        return launch_g<4>(s, p, m, layer, q, q_heads, c, out, gate, plan, split);
     case 8:
-        return launch_g<8>(s, p, m, layer, q, q_heads, c, out, gate, cu_count);
+        return launch_g<8>(s, p, m, layer, q, q_heads, c, out, gate, plan, split);
     default:
         return hipErrorInvalidValue;
     }

@@ -7,7 +7,8 @@
 // decode: rows (default 128) of U[lo, hi] tokens (default config 3's
 // [1024, 8192]), or lognormal lengths with LOGNORMAL=median:sigma:max, on
 // permuted pages, through ckv_append_decode; prefill: config 4's 64 x 512 rows
-// over a 2,000-token prefix through ckv_prefill_attention. Prints each
+// over a 2,000-token prefix (PREFILL_SHAPE=seqs:chunk:prefix for another)
+// through ckv_prefill_attention. Prints each
 // library's time per launch and how many outputs differ.
 #include <hip/hip_runtime.h>
 #include <dlfcn.h>
@@ -132,8 +133,12 @@ int main(int argc, char** argv)
         }
         for (auto n : len) kv_bytes += (double)n * F * 2 * 2;
     } else {
-        // config 4: 64 sequences x 512 rows at positions 2000..2511 over a shared 125-page prefix
-        const uint32_t seqs = 64, chunk = 512, prefix = 2000, pp = prefix / BS, cp = chunk / BS;
+        // config 4: 64 sequences x 512 rows at positions 2000..2511 over a shared 125-page prefix;
+        // PREFILL_SHAPE=seqs:chunk:prefix (multiples of 16) for another shape
+        uint32_t seqs = 64, chunk = 512, prefix = 2000;
+        if (const char* shape = getenv("PREFILL_SHAPE"))
+            sscanf(shape, "%u:%u:%u", &seqs, &chunk, &prefix);
+        const uint32_t pp = prefix / BS, cp = chunk / BS;
         blocks = pp + (size_t)seqs * cp;
         std::vector<uint32_t> seq_table(seqs * (pp + cp));
         for (uint32_t q = 0; q < seqs; ++q)

@@ -172,6 +172,80 @@ def test_ragged_tiles_every_group_size(ctx, group, code, waves, monkeypatch):
     pool.close()
 
 
+# a long chunk over a long prefix (three tiles, the last of one row), a short
+# sequence beside it, and a chunk that starts at position 0
+LONG = [(3000, 513), (40, 200), (0, 130)]
+_long_expected = {}
+
+
+@pytest.mark.parametrize("split", [None, "1", "3", "8"])
+@pytest.mark.parametrize("code", [orc.BF16, orc.F16])
+@pytest.mark.parametrize("group", [1, 4])
+def test_key_split_of_small_launches(ctx, group, code, split, monkeypatch):
+    """A launch too small to fill the GPU splits each tile's key blocks
+    between up to 8 workgroups, and the last of them to finish folds the
+    others' (max, denominator, accumulator) records into its own; the result
+    matches the oracle for every split (None: the launch's own choice, "1":
+    no split, "3": ranges of uneven length), is the same bit for bit on a
+    second call (the arrival counters are left at zero), and is one
+    paged_attention_prefill launch. Shares whose keys all lie after some of
+    their rows' positions carry a -inf maximum and weigh nothing."""
+    if split:
+        monkeypatch.setenv("CKV_PREFILL_SPLIT", split)
+    print(f"key split group {group} dtype {code} split {split}", flush=True)
+    H = 2
+    Hq = H * group
+    F = H * D
+    rng = orc.Mt64(11 * group + code)
+    lengths_tok = [start + n for start, n in LONG]
+    total_pages = sum(pages_for(n) for n in lengths_tok)
+    blocks = total_pages + 3
+    perm = rng.permutation(blocks)
+    geom = (1, blocks, 16, H, D)
+    slot_count = blocks * 16
+    kc = rng.normal(slot_count * F, code)
+    vc = rng.normal(slot_count * F, code)
+    tables, at = [], 0
+    for n in lengths_tok:
+        tables.append(perm[at:at + pages_for(n)])
+        at += pages_for(n)
+    flat = np.concatenate(tables)
+    positions, offsets, lengths = [], [], []
+    at = 0
+    for (start, n), t in zip(LONG, tables):
+        positions += list(range(start, start + n))
+        offsets += [at] * n
+        lengths += [len(t)] * n
+        at += len(t)
+    rows = len(positions)
+    q = rng.normal(rows * Hq * D, code).reshape(rows, Hq * D)
+    pool, kd, vd = new_pool(ctx, geom, code)
+    kd.copy_(to_dev(kc, code))
+    vd.copy_(to_dev(vc, code))
+    pool.upload(flat, offsets, lengths, positions)
+    key = (group, code)
+    if key not in _long_expected:
+        _long_expected[key] = orc.Attention(geom, kc, vc, code, q, code, positions, flat, offsets,
+                                            lengths, Hq, 0, scale()).online_threads(8)
+    expected = _long_expected[key]
+    qd = to_dev(q, code)
+    outs = []
+    for _ in range(2):
+        out = torch.full_like(qd, float("nan"))
+        ctx.sync()
+        ctx.profile(True)
+        ctx.profile_reset()
+        pool.prefill(0, qd, Hq, scale(), out)
+        ctx.sync()
+        launches = ctx.profile_query("paged_attention_prefill")[1]
+        ctx.profile(False)
+        assert launches == 1, launches
+        assert_close(to_f32(out), expected, what=f"split {split}, group {group}")
+        outs.append(out)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    pool.close()
+
+
 @pytest.mark.parametrize("code", [orc.BF16, orc.F32])
 def test_layer_beyond_4_gib_takes_64_bit_page_addresses(ctx, code):
     """A pool whose layer spans more than 4 GiB per tensor (140,000 bf16 or

@@ -1795,7 +1795,7 @@ int prefill_impl(ckv_pool* pool, size_t layer, const void* queries, size_t q_hea
         return run_decode(pool, layer, queries, q_heads, scale, output, gate);
     ckv_context* ctx = pool->ctx;
     const prefill_shape_info plan = prefill_plan(view, pool->meta, (uint32_t)q_heads, ctx->cu_count);
-    prefill_split split { nullptr, nullptr, plan.n_split };
+    prefill_split split { nullptr, nullptr, plan.n_split, plan.min_blocks };
     if (plan.n_split > 1) {
         int status = ensure_device(ctx, &pool->d_pre_records, &pool->d_pre_records_floats,
                                    (size_t)plan.records_floats, "prefill split records");

@@ -79,14 +79,17 @@ constexpr size_t tile_entry_words = 4;
 // Device scratch of a prefill launch whose tiles' key blocks are split
 // between workgroups: a record [max, denominator, 0, 0, acc[128]] per (share,
 // query vector), and an arrival counter per (tile, workgroup row range, kv
-// head), zero before a launch and left zero by it. n_split = 1: no split.
+// head), zero before a launch and left zero by it. n_split = 1: no split;
+// a tile's keys are cut into at most n_split ranges of at least min_blocks
+// 32-key blocks.
 struct prefill_split {
     float* records;
     uint32_t* arrivals;
     uint32_t n_split;
+    uint32_t min_blocks;
 };
 constexpr uint32_t prefill_record_floats = 128 + 4;
-constexpr uint32_t split_min_blocks = 4; // 32-key blocks a share attends at least
+constexpr uint32_t split_min_blocks = 8; // default of prefill_split::min_blocks
 constexpr uint32_t split_max = 8;        // shares a tile's keys are split into at most
 
 // Largest query tile, in rows (positions): the prefill kernel covers a tile
@@ -352,6 +355,7 @@ bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, cons
 struct prefill_shape_info {
     uint32_t waves;
     uint32_t n_split;
+    uint32_t min_blocks;
     uint64_t records_floats;
     uint64_t counters;
 };

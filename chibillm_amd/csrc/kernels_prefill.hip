@@ -316,9 +316,13 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
 
     const uint32_t kv_heads = p.kv_heads;
     const uint32_t kvh = blockIdx.x % kv_heads; // consecutive workgroups: different heads/XCDs
+    // key ranges vary slowest: every tile's first range is dispatched before
+    // any second one (ranges interleaved with the rows placed the ranges that
+    // find no keys, and the long ones, unevenly: +5 to +29 % launch time)
     const uint32_t n_split = SPLIT ? split_scratch.n_split : 1;
-    const uint32_t rest = blockIdx.x / kv_heads / n_split;
-    const uint32_t part = blockIdx.x / kv_heads % n_split; // this workgroup's share of the keys
+    const uint32_t n_rest = md.n_tiles * subs;
+    const uint32_t rest = blockIdx.x / kv_heads % n_rest;
+    const uint32_t part = blockIdx.x / kv_heads / n_rest; // this workgroup's range of the keys
     const uint32_t sub = rest % subs;
     const uint32_t tile = rest / subs;
     // one scalar load gives the tile: first row, rows, first position, table offset
@@ -334,11 +338,14 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
     const uint32_t* table = md.table + te.w;
     const uint32_t n_blocks = pos_last / block_keys + 1;
     // Key blocks [kb_begin, kb_end) of this workgroup: the tile's blocks cut
-    // into n_parts ranges of at least split_min_blocks (uniform over the tile's
+    // into n_parts ranges of at least min_blocks (uniform over the tile's
     // workgroups), range `part`.
     uint32_t n_parts = 1, kb_begin = 0, kb_end = n_blocks;
     if constexpr (SPLIT) {
-        n_parts = min(n_split, max(1u, n_blocks / split_min_blocks));
+        // a tile shorter than 3 ranges' worth is not split: the handoff's round
+        // trips would cost more than the blocks it takes off the longest range
+        const uint32_t mb = split_scratch.min_blocks;
+        n_parts = n_blocks >= 3 * mb ? min(n_split, n_blocks / mb) : 1;
         if (part >= n_parts)
             return;
         kb_begin = part * n_blocks / n_parts;
@@ -741,19 +748,17 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
         __syncthreads();
         if (!*last_flag)
             return;
+        // online over the shares, two per round trip: the running state
+        // (M, lt, o) is rescaled by 2^(M - M') when a share raises the maximum
         float M = -__builtin_inff();
-#pragma unroll
-        for (uint32_t s = 0; s < split_max; ++s) // every share's head in one round trip
-            M = fmaxf(M, __uint_as_float(agent_load4(rs, off(min(s, n_parts - 1), 0))[0]));
-        // M is finite for a valid row: the tile's first share attends key 0
-        auto weight = [&](float ms) {
-            return ms == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f((ms - M) * c);
+        auto weight = [&](float ms, float to) { // 0 for a share that attended nothing
+            return ms == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f((ms - to) * c);
         };
         lt = 0.0f;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
             o[mt] = f32x16_t {};
-        for (uint32_t s = 0; s < n_parts; s += 2) { // two shares per round trip
+        for (uint32_t s = 0; s < n_parts; s += 2) {
             const uint32_t s1 = min(s + 1, n_parts - 1);
             u32x4_t ha = agent_load4(rs, off(s, 0)), hb = agent_load4(rs, off(s1, 0));
             u32x4_t va[16], vb[16];
@@ -763,19 +768,23 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
 #pragma unroll
             for (int j = 0; j < 16; ++j)
                 vb[j] = agent_load4(rs, off(s1, 1 + 2 * j + g));
-            const float wa = weight(__uint_as_float(ha[0]));
-            const float wb = s + 1 < n_parts ? weight(__uint_as_float(hb[0])) : 0.0f;
-            lt += __uint_as_float(ha[1]) * wa;
+            const float ma = __uint_as_float(ha[0]);
+            const float mb = s + 1 < n_parts ? __uint_as_float(hb[0]) : -__builtin_inff();
+            const float m_new = fmaxf(M, fmaxf(ma, mb));
+            const float keep = weight(M, m_new), wa = weight(ma, m_new), wb = weight(mb, m_new);
+            M = m_new;
+            lt = lt * keep + __uint_as_float(ha[1]) * wa;
             lt += __uint_as_float(hb[1]) * wb;
 #pragma unroll
             for (int j = 0; j < 16; ++j) // chunk 1 + 2j + g = features 32mt + 8quad + 4g + e
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float acc = o[j / 4][4 * (j % 4) + e];
+                    float acc = o[j / 4][4 * (j % 4) + e] * keep;
                     acc += __uint_as_float(va[j][e]) * wa;
                     o[j / 4][4 * (j % 4) + e] = acc + __uint_as_float(vb[j][e]) * wb;
                 }
         }
+        // lt > 0 for a valid row: the tile's first share attends key 0
     }
 
     if (!active || !valid)
@@ -873,11 +882,11 @@ bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, cons
 // compute units idle, each tile's key blocks are split between as many
 // workgroups as fill them (at most split_max, each attending at least
 // split_min_blocks blocks; the kernel takes fewer for short tiles).
-// CKV_PREFILL_WAVES (4 or 8) and CKV_PREFILL_SPLIT override.
+// CKV_PREFILL_WAVES (4 or 8), CKV_PREFILL_SPLIT and CKV_PREFILL_SPLIT_MIN (blocks) override.
 prefill_shape_info prefill_plan(const pool_view& p, const meta_view& m, uint32_t q_heads,
                                 int cu_count)
 {
-    prefill_shape_info plan { 8, 1, 0, 0 };
+    prefill_shape_info plan { 8, 1, split_min_blocks, 0, 0 };
     const uint32_t group = p.kv_heads ? q_heads / p.kv_heads : 0;
     if (p.dtype == CKV_F32 || group == 0 || group > 4)
         return plan;
@@ -893,6 +902,8 @@ prefill_shape_info prefill_plan(const pool_view& p, const meta_view& m, uint32_t
     if (const char* forced = std::getenv("CKV_PREFILL_SPLIT"))
         split = (uint64_t)std::max(1L, std::strtol(forced, nullptr, 10));
     plan.n_split = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(split, 1), split_max);
+    if (const char* forced = std::getenv("CKV_PREFILL_SPLIT_MIN"))
+        plan.min_blocks = (uint32_t)std::max(1L, std::strtol(forced, nullptr, 10));
     if (plan.n_split > 1) {
         plan.records_floats = pairs * plan.n_split * 128 * prefill_record_floats;
         plan.counters = pairs;
@@ -910,6 +921,7 @@ hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m,
     if (plan.n_split > 1 && (!split.records || !split.arrivals))
         return hipErrorInvalidValue;
     split.n_split = plan.n_split;
+    split.min_blocks = plan.min_blocks;
     const float c = scale * log2e;
     switch (q_heads / p.kv_heads) {
     case 1:

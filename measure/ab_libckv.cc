@@ -8,7 +8,8 @@
 // [1024, 8192]), or lognormal lengths with LOGNORMAL=median:sigma:max, on
 // permuted pages, through ckv_append_decode; prefill: config 4's 64 x 512 rows
 // over a 2,000-token prefix (PREFILL_SHAPE=seqs:chunk:prefix for another)
-// through ckv_prefill_attention. Prints each
+// through ckv_prefill_attention. AB_ENV_A/AB_ENV_B set environment settings
+// for one side's launches only. Prints each
 // library's time per launch and how many outputs differ.
 #include <hip/hip_runtime.h>
 #include <dlfcn.h>
@@ -19,6 +20,7 @@
 #include <vector>
 #include <algorithm>
 #include <cmath>
+#include <string>
 
 #define CHECK(x) do { hipError_t e = (x); if (e != hipSuccess) { printf("hip error %s at %d\n", hipGetErrorString(e), __LINE__); exit(1); } } while (0)
 
@@ -183,6 +185,34 @@ int main(int argc, char** argv)
         }
     }
     const float scale = 0.08838834764831845f;
+    // AB_ENV_A / AB_ENV_B = "NAME=value,NAME=value": set before that library's
+    // launches and cleared before the other's (the libraries read such
+    // settings at each launch), so one library can be compared with itself
+    // under two settings
+    auto apply_env = [&](int i) {
+        for (int pass = 0; pass < 2; ++pass) { // clear the other side's names, then set ours
+            const char* spec = getenv(pass ? (i ? "AB_ENV_B" : "AB_ENV_A") : (i ? "AB_ENV_A" : "AB_ENV_B"));
+            if (!spec)
+                continue;
+            std::string all(spec);
+            size_t at = 0;
+            while (at < all.size()) {
+                size_t end = all.find(',', at);
+                if (end == std::string::npos)
+                    end = all.size();
+                const std::string item = all.substr(at, end - at);
+                const size_t eq = item.find('=');
+                if (eq != std::string::npos) {
+                    const std::string name = item.substr(0, eq);
+                    if (pass)
+                        setenv(name.c_str(), item.substr(eq + 1).c_str(), 1);
+                    else
+                        unsetenv(name.c_str());
+                }
+                at = end + 1;
+            }
+        }
+    };
     hipEvent_t e0, e1;
     CHECK(hipEventCreate(&e0));
     CHECK(hipEventCreate(&e1));
@@ -190,6 +220,7 @@ int main(int argc, char** argv)
     for (int r = -1; r < rounds; ++r) {
         for (int k = 0; k < 2; ++k) {
             const int i = (r & 1) ? 1 - k : k; // alternate which goes first
+            apply_env(i);
             CHECK(hipEventRecord(e0, st));
             for (int j = 0; j < launches; ++j)
                 if (pre ? libs[i].prefill(libs[i].pool, j % L, q, Hq, scale, outs[i], B)

@@ -178,20 +178,24 @@ LONG = [(3000, 513), (40, 200), (0, 130)]
 _long_expected = {}
 
 
-@pytest.mark.parametrize("split", [None, "1", "3", "8"])
+@pytest.mark.parametrize("split", [None, "1", "3", "8", "8/1"])
 @pytest.mark.parametrize("code", [orc.BF16, orc.F16])
 @pytest.mark.parametrize("group", [1, 4])
 def test_key_split_of_small_launches(ctx, group, code, split, monkeypatch):
-    """A launch too small to fill the GPU splits each tile's key blocks
-    between up to 8 workgroups, and the last of them to finish folds the
-    others' (max, denominator, accumulator) records into its own; the result
-    matches the oracle for every split (None: the launch's own choice, "1":
-    no split, "3": ranges of uneven length), is the same bit for bit on a
+    """A launch too small to fill the GPU splits each long tile's key blocks
+    between up to 8 workgroups, and the last of them to finish folds every
+    range's (max, denominator, accumulator) record; the result matches the
+    oracle for every split (None: the launch's own choice, "1": no split,
+    "3": ranges of uneven length, "8/1": ranges down to one 32-key block, so
+    that some ranges lie wholly after some of their rows' positions and carry
+    a -inf maximum that must weigh nothing), is the same bit for bit on a
     second call (the arrival counters are left at zero), and is one
-    paged_attention_prefill launch. Shares whose keys all lie after some of
-    their rows' positions carry a -inf maximum and weigh nothing."""
+    paged_attention_prefill launch."""
     if split:
-        monkeypatch.setenv("CKV_PREFILL_SPLIT", split)
+        n, _, least = split.partition("/")
+        monkeypatch.setenv("CKV_PREFILL_SPLIT", n)
+        if least:
+            monkeypatch.setenv("CKV_PREFILL_SPLIT_MIN", least)
     print(f"key split group {group} dtype {code} split {split}", flush=True)
     H = 2
     Hq = H * group

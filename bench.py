@@ -636,7 +636,7 @@ def bench_config4(args):
     from chibillm_amd import ckv
 
     device = torch.device("cuda:0")
-    prefix, S, C = args.prefix, PREFILL_SEQS, PREFILL_CHUNK
+    prefix, S, C = args.prefix, args.sequences, PREFILL_CHUNK
     F = KV_HEADS * HEAD_DIM
     full = prefix // BLOCK
     partial = prefix % BLOCK != 0
@@ -711,7 +711,7 @@ def bench_config4(args):
     peak = MFMA_PEAK_TFLOPS[args.dtype]
     result = {
         "metric": "chunked-prefill attention TFLOP/s (MFMA) + tokens/s, Qwen3-0.6B KV, "
-                  "64 sequences x 512-token chunks over a shared prefix"
+                  f"{S} sequences x {C}-token chunks over a shared prefix"
                   + ("" if args.dtype == "bf16" else f", {args.dtype} pages"),
         "value": round(LAYERS * flops * args.steps / elapsed / 1e12, 2),
         "unit": "TFLOP/s",
@@ -1089,7 +1089,7 @@ def bench_ceiling(args):
 LEGS = (
     ("config2", {"steps": 2000, "warmup": 3},
      "one decode launch over config 2's batch per step, 2,000 timed steps"),
-    ("config4", {"steps": 5, "warmup": 1, "prefix": 2008},
+    ("config4", {"steps": 5, "warmup": 1, "prefix": 2008, "sequences": PREFILL_SEQS},
      "5 timed steps of config 4 at the 2,008-token prefix (copy-on-write tail)"),
     ("config5", {"steps": 1000},
      "the first 1,000 steps of config 5's churn trace (ramp-up to the live cap included)"),
@@ -1154,6 +1154,10 @@ def main():
                     help="config4 shared prefix tokens (2008 leaves a partial tail page, "
                          "so every sequence copies it on write; 2000 does not); spill: the "
                          "prefix moved")
+    ap.add_argument("--sequences", type=int, default=PREFILL_SEQS,
+                    help="config4 sequences (default 64, BASELINE's config); fewer make a "
+                         "launch too small to fill the GPU, which splits each tile's keys "
+                         "between workgroups (e.g. --sequences 1 --prefix 8000)")
     ap.add_argument("--dtype", choices=["bf16", "f32"], default="bf16",
                     help="config2, config3, config4: the pools' element type (bf16, the "
                          "BASELINE configs; f32, the reference's storage type); an f32 run "
@@ -1167,6 +1171,9 @@ def main():
               "(run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
+    if args.sequences < 1:
+        print("--sequences must be at least 1", file=sys.stderr)
+        sys.exit(2)
     if args.dtype != "bf16" and args.workload not in ("config2", "config3", "config4"):
         print(f"--dtype {args.dtype}: config2, config3 and config4 only", file=sys.stderr)
         sys.exit(2)

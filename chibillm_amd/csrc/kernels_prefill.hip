@@ -249,24 +249,38 @@ __device__ __forceinline__ float sigmoid(float g)
 // 32-query block sees a new maximum in most key blocks.
 constexpr float rescale_log2 = 8.0f;
 
-// Row maximum of the 16 scores a lane holds and its partner lane's 16.
-// The partner (lane l ^ 32) is read with v_permlane32_swap, which exchanges
-// the two 32-lane halves inside the VALU: of its two results, lanes 0-31 find
-// the upper half's value in the second and lanes 32-63 the lower half's in
-// the first, while the other result holds the lane's own value, so the
-// maximum of all three is the pair's. A ds_bpermute would put an LDS round
-// trip on the chain from the scores to the next block's exponentials (1 %
-// of config 4's prefill time; outputs bit-identical).
-__device__ __forceinline__ float block_max(const f32x16_t& s)
+// Maxima by v_maximum3_f32 (IEEE 754-2019 maximum: a NaN propagates, so the
+// scores the matrix core writes need no quieting first, which fmaxf's maxNum
+// would make the compiler insert).
+__device__ __forceinline__ float max2(float a, float b)
 {
-    float mx = s[0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r)
-        mx = fmaxf(mx, s[r]);
+    return __builtin_elementwise_maximum(a, b);
+}
+
+// The maximum of the 16 scores a lane holds, as a tree of three-input maxima
+// (depth 3 instead of a chain of 8). Both lanes of a query compare their own
+// maximum with the query's rescale threshold; only a rescale needs the pair's.
+__device__ __forceinline__ float lane_max(const f32x16_t& s)
+{
+    const float a = max2(max2(s[0], s[1]), s[2]), b = max2(max2(s[3], s[4]), s[5]);
+    const float d = max2(max2(s[6], s[7]), s[8]), e = max2(max2(s[9], s[10]), s[11]);
+    const float f = max2(max2(s[12], s[13]), s[14]);
+    return max2(max2(max2(a, b), d), max2(max2(e, f), s[15]));
+}
+
+// The maximum of a lane's value and its partner lane's (lane l ^ 32, the same
+// query's other 16 keys). The partner is read with v_permlane32_swap, which
+// exchanges the two 32-lane halves inside the VALU: of its two results, lanes
+// 0-31 find the upper half's value in the second and lanes 32-63 the lower
+// half's in the first, while the other result holds the lane's own value, so
+// the maximum of all three is the pair's. A ds_bpermute would put an LDS
+// round trip on the chain from the scores to the next block's exponentials.
+__device__ __forceinline__ float pair_max(float mx)
+{
     const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
     const auto sw = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
-    return fmaxf(fmaxf(mx, __builtin_bit_cast(float, (uint32_t)sw[0])),
-                 __builtin_bit_cast(float, (uint32_t)sw[1]));
+    return max2(max2(mx, __builtin_bit_cast(float, (uint32_t)sw[0])),
+                __builtin_bit_cast(float, (uint32_t)sw[1]));
 }
 
 // Probabilities of one q-block against the running maximum m (raw q.k
@@ -278,14 +292,15 @@ __device__ __forceinline__ void exponentiate(f32x16_t& s, float m, float& l, flo
     // GUARD: a workgroup that attends only part of the keys may have seen no
     // unmasked key of a query yet (m = -inf); its probabilities are then 0
     const float mc = GUARD && m == -__builtin_inff() ? 0.0f : m * c;
-    s[0] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[0], c, -mc));
-    float sum = s[0]; // an exponential is never -0, so this is 0 + s[0] exactly
 #pragma unroll
-    for (int r = 1; r < 16; ++r) {
+    for (int r = 0; r < 16; ++r)
         s[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c, -mc));
-        sum += s[r];
-    }
-    l += sum;
+    // a tree of sums (depth 4 instead of a chain of 15)
+    float q4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        q4[i] = (s[4 * i] + s[4 * i + 1]) + (s[4 * i + 2] + s[4 * i + 3]);
+    l += (q4[0] + q4[1]) + (q4[2] + q4[3]);
 }
 
 // W waves per workgroup: 8 (two per SIMD, eight LDS stages), or 4 for
@@ -558,11 +573,12 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
             }
         }
         sp = sc;
-        mx = block_max(sp);
+        // the lane's own maximum decides: both halves of a query share m_limit
+        mx = lane_max(sp);
         return __any(mx > m_limit);
     };
     auto rescale = [&]() {
-        const float m_new = fmaxf(m, mx);
+        const float m_new = fmaxf(m, pair_max(mx));
         float alpha = __builtin_amdgcn_exp2f((m - m_new) * c); // 0 at the start
         if constexpr (SPLIT)
             alpha = m_new == -__builtin_inff() ? 1.0f : alpha; // nothing attended yet

@@ -92,6 +92,29 @@ constexpr uint32_t prefill_record_floats = 128 + 4;
 constexpr uint32_t split_min_blocks = 8; // default of prefill_split::min_blocks
 constexpr uint32_t split_max = 8;        // shares a tile's keys are split into at most
 
+// A tile (or a workgroup's rows of it) whose keys span n_blocks 32-key
+// blocks is cut into at most n_split ranges of at least min_blocks each;
+// prefill_range_count gives how many. A tile shorter than three ranges' worth
+// is not cut (1): the handoff's round trips would cost more than the blocks
+// it takes off the longest range. n_split and min_blocks are at least 1
+// (prefill_plan).
+__host__ __device__ inline uint32_t prefill_range_count(uint32_t n_blocks, uint32_t n_split,
+                                                        uint32_t min_blocks)
+{
+    const uint32_t by_length = n_blocks / min_blocks;
+    return n_blocks >= 3 * min_blocks ? (by_length < n_split ? by_length : n_split) : 1;
+}
+
+// The key blocks [begin, end) of range `part` of n ranges. Range 0 starts at
+// block 0, so every query of the tile attends some key of it. 32-bit:
+// n_blocks < 2^27 (positions are 32-bit) and part < split_max.
+__host__ __device__ inline void prefill_range_bounds(uint32_t n_blocks, uint32_t n, uint32_t part,
+                                                     uint32_t& begin, uint32_t& end)
+{
+    begin = part * n_blocks / n;
+    end = (part + 1) * n_blocks / n;
+}
+
 // Largest query tile, in rows (positions): the prefill kernel covers a tile
 // with G workgroups of 256/G rows for GQA group size G.
 constexpr uint32_t prefill_tile_rows = 256;

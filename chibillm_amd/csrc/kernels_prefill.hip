@@ -357,14 +357,10 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
     // workgroups), range `part`.
     uint32_t n_parts = 1, kb_begin = 0, kb_end = n_blocks;
     if constexpr (SPLIT) {
-        // a tile shorter than 3 ranges' worth is not split: the handoff's round
-        // trips would cost more than the blocks it takes off the longest range
-        const uint32_t mb = split_scratch.min_blocks;
-        n_parts = n_blocks >= 3 * mb ? min(n_split, n_blocks / mb) : 1;
+        n_parts = prefill_range_count(n_blocks, n_split, split_scratch.min_blocks);
         if (part >= n_parts)
             return;
-        kb_begin = part * n_blocks / n_parts;
-        kb_end = (part + 1) * n_blocks / n_parts;
+        prefill_range_bounds(n_blocks, n_parts, part, kb_begin, kb_end);
     } else {
         (void)part;
     }

@@ -286,3 +286,106 @@ TEST("random batches at random GPU sizes: every plan is well formed")
         }
     }
 }
+
+// ---- the prefill's launch shape and key ranges ---------------------------
+
+namespace {
+
+ckv::prefill_shape_info prefill_shape_for(uint32_t n_tiles, uint32_t kv_heads, uint32_t q_heads,
+                                          int cus, int dtype = CKV_BF16)
+{
+    ckv::pool_view p {};
+    p.kv_heads = kv_heads;
+    p.head_dim = 128;
+    p.block_size = 16;
+    p.features = kv_heads * 128;
+    p.dtype = dtype;
+    ckv::meta_view m {};
+    m.n_tiles = n_tiles;
+    return ckv::prefill_plan(p, m, q_heads, cus);
+}
+
+} // namespace
+
+TEST("prefill key ranges: a partition of the tile's blocks, each range long enough")
+{
+    for (uint32_t n_blocks = 1; n_blocks <= 1200; ++n_blocks)
+        for (uint32_t n_split = 1; n_split <= ckv::split_max; ++n_split)
+            for (uint32_t least : { 1u, 2u, 3u, 8u, 16u }) {
+                const uint32_t n = ckv::prefill_range_count(n_blocks, n_split, least);
+                REQUIRE(n >= 1 && n <= n_split);
+                if (n_blocks < 3 * least)
+                    CHECK(n == 1);
+                uint32_t next = 0;
+                for (uint32_t part = 0; part < n; ++part) {
+                    uint32_t b = 0, e = 0;
+                    ckv::prefill_range_bounds(n_blocks, n, part, b, e);
+                    CHECK(b == next);         // contiguous, starting at block 0
+                    CHECK(e > b);             // never empty
+                    if (n > 1)
+                        CHECK(e - b >= least); // at least min_blocks each
+                    next = e;
+                }
+                CHECK(next == n_blocks); // covering every block once
+            }
+}
+
+TEST("prefill launch shape: 8-wave workgroups when they fill the GPU")
+{
+    // config 4: 64 sequences x 512 rows = 128 tiles, 8 kv heads, 16 q heads
+    const auto c4 = prefill_shape_for(128, 8, 16, 256);
+    CHECK(c4.waves == 8 && c4.n_split == 1 && c4.records_floats == 0 && c4.counters == 0);
+    // exactly one 8-wave workgroup per compute unit: 8-wave
+    CHECK(prefill_shape_for(16, 8, 16, 256).waves == 8);
+    // GQA groups of 8 always take 8-wave workgroups, and f32 pools their own kernel
+    CHECK(prefill_shape_for(1, 8, 64, 256).waves == 8);
+    CHECK(prefill_shape_for(1, 8, 16, 256, CKV_F32).waves == 8);
+    CHECK(prefill_shape_for(1, 8, 16, 256, CKV_F32).n_split == 1);
+}
+
+TEST("prefill launch shape: small launches take 4-wave workgroups and split keys to fill")
+{
+    // one sequence's 512-row chunk: 2 tiles x 2 x 8 = 32 eight-wave units for 256 CUs
+    const auto one = prefill_shape_for(2, 8, 16, 256);
+    CHECK(one.waves == 4 && one.n_split == 8 && one.min_blocks == ckv::split_min_blocks);
+    // 64 (tile rows, kv head) pairs of 4-wave workgroups, 8 ranges of 128 query vectors
+    CHECK(one.counters == 64);
+    CHECK(one.records_floats == 64ull * 8 * 128 * ckv::prefill_record_floats);
+    // four sequences: 8 tiles -> 256 pairs, two ranges each fill two per compute unit
+    const auto four = prefill_shape_for(8, 8, 16, 256);
+    CHECK(four.waves == 4 && four.n_split == 2 && four.counters == 256);
+    // never more than split_max ranges, and a launch of one pair per CU takes none
+    CHECK(prefill_shape_for(1, 1, 1, 256).n_split == ckv::split_max);
+    const auto full = prefill_shape_for(15, 8, 16, 256); // 240 units: 480 pairs
+    CHECK(full.waves == 4 && full.n_split == 1 && full.records_floats == 0);
+}
+
+TEST("prefill launch shape: the environment overrides")
+{
+    {
+        const env_guard e("CKV_PREFILL_SPLIT", "3");
+        CHECK(prefill_shape_for(2, 8, 16, 256).n_split == 3);
+    }
+    {
+        const env_guard e("CKV_PREFILL_SPLIT", "50");
+        CHECK(prefill_shape_for(2, 8, 16, 256).n_split == ckv::split_max);
+    }
+    {
+        const env_guard e("CKV_PREFILL_SPLIT", "0");
+        CHECK(prefill_shape_for(2, 8, 16, 256).n_split == 1);
+    }
+    {
+        const env_guard e("CKV_PREFILL_SPLIT_MIN", "2");
+        CHECK(prefill_shape_for(2, 8, 16, 256).min_blocks == 2);
+    }
+    {
+        const env_guard e("CKV_PREFILL_WAVES", "8");
+        const auto s = prefill_shape_for(2, 8, 16, 256);
+        CHECK(s.waves == 8 && s.n_split == 1);
+    }
+    {
+        const env_guard e("CKV_PREFILL_WAVES", "4");
+        const auto s = prefill_shape_for(128, 8, 16, 256); // config 4 forced to 4 waves
+        CHECK(s.waves == 4 && s.n_split == 1);
+    }
+}

@@ -24,6 +24,10 @@
 // outputs of layers 0 and L - 1 are written to <dir> for a CPU check of the
 // attention: up to eight decode rows (decode_rows.json) and one prefill chunk
 // (prefill_rows.json), with raw bf16 .bin files.
+//
+// --log-steps <file> writes one line per engine step with its batch's shape
+// (phase, rows, items, attended tokens, the longest item, and for decode steps
+// the fast decode's plan), to be read beside a kernel trace of the run.
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -60,6 +64,7 @@ struct options {
     bool device_tables = false; // sequence tables kept on the device (device_tables)
     bool host_timing = false;   // drain the GPU before each step's metadata work and time it
     std::string check_dir;      // --check: verify the trace and dump one decode step here
+    std::string log_steps;      // --log-steps: one line per step with its batch's shape
     std::size_t check_every = 250;
     std::size_t dump_after = 1000;
 };
@@ -163,7 +168,18 @@ public:
     churn_runner(const options& opt, hip_context& ctx)
         : opt_(opt)
         , ctx_(ctx)
-    {}
+    {
+        if (!opt_.log_steps.empty())
+            step_log_ = std::fopen(opt_.log_steps.c_str(), "w");
+    }
+    ~churn_runner() override
+    {
+        if (step_log_)
+            std::fclose(step_log_);
+    }
+    churn_runner(const churn_runner&) = delete;
+    churn_runner& operator=(const churn_runner&) = delete;
+    bool step_log_open() const noexcept { return opt_.log_steps.empty() || step_log_; }
 
     const model_info& info() const noexcept override { return info_; }
 
@@ -295,6 +311,8 @@ public:
             }
         }
         account(batch, h2d);
+        if (step_log_)
+            log_step(cache.pool(), batch);
         if (checking_) {
             auto recorded = record(batch);
             if (recorded && dumping) {
@@ -572,6 +590,27 @@ private:
     }
 
 private:
+    // --log-steps: phase (d or p), rows, items, attended tokens (every row's
+    // for decode, every tile's last row's for prefill), the longest item's,
+    // and for decode steps the fast decode's plan (pages per workgroup, work
+    // items, partial records; ckv_decode_plan)
+    void log_step(ckv_pool* pool, const model_batch& batch)
+    {
+        std::size_t attended = 0, longest = 0;
+        for (const auto& item : batch.items) {
+            const std::size_t a = batch.positions[item.token_offset + item.token_count - 1] + 1;
+            attended += a;
+            longest = std::max(longest, a);
+        }
+        const bool decode = batch.phase == batch_phase::decode;
+        std::uint32_t split_pages = 0, work_items = 0, records = 0;
+        if (decode)
+            (void)ckv_decode_plan(pool, &split_pages, &work_items, &records);
+        std::fprintf(step_log_, "%zu %c %zu %zu %zu %zu %u %u %u\n", step_ - 1, decode ? 'd' : 'p',
+                     batch.tokens.size(), batch.items.size(), attended, longest, split_pages,
+                     work_items, records);
+    }
+
     // Algorithmic bytes of one step, all layers: K+V of every attended token
     // (once per decode row; once per prefill tile, whose rows share it), the
     // appended rows, Q and O, and the uploaded metadata.
@@ -617,6 +656,7 @@ private:
     totals totals_;
     // --check
     bool checking_ = false;
+    std::FILE* step_log_ = nullptr;
     bool dump_decode_wanted_ = false, dump_prefill_wanted_ = false;
     bool dumped_decode_ = false, dumped_prefill_ = false;
     std::vector<std::vector<std::uint16_t>> k_host_, v_host_, q_host_; // per layer
@@ -673,6 +713,8 @@ parse(int argc, char** argv, options& o)
             o.prefill_chunk = std::strtoull(v, nullptr, 10);
         else if (a == "--sigma")
             o.sigma = std::strtod(v, nullptr);
+        else if (a == "--log-steps")
+            o.log_steps = v;
         else
             return false;
     }
@@ -690,7 +732,8 @@ main(int argc, char** argv)
                      "usage: churn [--steps N] [--seed S] [--pool-gb G] [--max-live N] "
                      "[--arrival-mean M] [--layers L] [--max-batch-tokens T] "
                      "[--prefill-chunk C] [--sigma S] [--profile] [--device-tables] "
-                     "[--host-timing] [--check DIR [--check-every N] [--dump-after STEP]]\n");
+                     "[--host-timing] [--check DIR [--check-every N] [--dump-after STEP]] "
+                     "[--log-steps FILE]\n");
         return 2;
     }
     auto ctx = hip_context::make(0);
@@ -708,6 +751,10 @@ main(int argc, char** argv)
     config.prefix_cache_bytes = 0;
 
     churn_runner runner(opt, *ctx);
+    if (!runner.step_log_open()) {
+        std::fprintf(stderr, "cannot write %s\n", opt.log_steps.c_str());
+        return 1;
+    }
     auto engine = inference_engine::make(config, runner);
     if (!engine) {
         std::fprintf(stderr, "engine: %s\n", describe_error(engine.error()).c_str());

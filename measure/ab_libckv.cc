@@ -176,15 +176,6 @@ int main(int argc, char** argv)
     CHECK(hipStreamCreate(&st));
     Lib libs[2] = { open_lib(argv[1]), open_lib(argv[2]) };
     void* outs[2] = { outA, outB };
-    for (auto& l : libs) {
-        if (l.context_create(0, &l.ctx) || l.context_set_stream(l.ctx, st)
-            || l.pool_wrap(l.ctx, L, blocks, BS, H, D, 1, kp, vp, &l.pool)
-            || l.tables_upload(l.pool, table.data(), table.size(), off.data(), lens.data(), pos.data(), pre ? nullptr : slot.data(), B)) {
-            printf("setup failed\n");
-            return 1;
-        }
-    }
-    const float scale = 0.08838834764831845f;
     // AB_ENV_A / AB_ENV_B = "NAME=value,NAME=value": set before that library's
     // launches and cleared before the other's (the libraries read such
     // settings at each launch), so one library can be compared with itself
@@ -213,6 +204,28 @@ int main(int argc, char** argv)
             }
         }
     };
+    // each side's settings apply from its pool's table upload on (the decode
+    // plan is built there)
+    for (int i = 0; i < 2; ++i) {
+        Lib& l = libs[i];
+        apply_env(i);
+        if (l.context_create(0, &l.ctx) || l.context_set_stream(l.ctx, st)
+            || l.pool_wrap(l.ctx, L, blocks, BS, H, D, 1, kp, vp, &l.pool)
+            || l.tables_upload(l.pool, table.data(), table.size(), off.data(), lens.data(), pos.data(), pre ? nullptr : slot.data(), B)) {
+            printf("setup failed\n");
+            return 1;
+        }
+    }
+    if (!pre)
+        for (int i = 0; i < 2; ++i) {
+            auto plan = reinterpret_cast<int (*)(void*, uint32_t*, uint32_t*, uint32_t*)>(
+                dlsym(libs[i].h, "ckv_decode_plan"));
+            uint32_t sp = 0, wi = 0, rec = 0;
+            if (plan && plan(libs[i].pool, &sp, &wi, &rec) == 0)
+                printf("%s plan: %u pages per workgroup, %u work items, %u records\n",
+                       i ? "B" : "A", sp, wi, rec);
+        }
+    const float scale = 0.08838834764831845f;
     hipEvent_t e0, e1;
     CHECK(hipEventCreate(&e0));
     CHECK(hipEventCreate(&e1));

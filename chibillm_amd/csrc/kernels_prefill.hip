@@ -689,8 +689,15 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
             stats(kb_begin, false);
             rescale();
         }
-        for (uint32_t kb = kb_begin + 1; kb < kb_end; ++kb) {
-            if (kb + 2 < kb_end)
+        // A steady iteration loads a block wholly inside the tile whose
+        // successor's pages exist (kb + 3 < n_blocks) and inside its range, so
+        // the load, the page fetch and the wait take no checks. (Skipping the
+        // diagonal test as well, for G >= 2, was 0.3-0.7 % slower.)
+        auto iteration4 = [&](uint32_t kb, auto steady) {
+            constexpr bool STEADY = decltype(steady)::value;
+            if constexpr (STEADY)
+                load_block_steady(kb + 2);
+            else if (kb + 2 < kb_end)
                 load_block(kb + 2);
             uint4 ka[8], va[4][2];
             uint4 pt[2];
@@ -701,11 +708,16 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
             read_v(kb - 1, va);
             pv(va, pt); // matrix: block kb - 1
             const bool grew = stats(kb, false);
-            wait_dma(newer(kb + 1, kb + 2));
+            wait_dma(STEADY ? shape::dmas : newer(kb + 1, kb + 2));
             __syncthreads();
             if (grew)
                 rescale();
-        }
+        };
+        uint32_t kb = kb_begin + 1;
+        for (; kb + 2 < kb_end && kb + 3 < n_blocks; ++kb)
+            iteration4(kb, std::true_type {});
+        for (; kb < kb_end; ++kb)
+            iteration4(kb, std::false_type {});
     }
     // the last block's probabilities and product
     {

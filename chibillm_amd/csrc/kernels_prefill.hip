@@ -901,8 +901,9 @@ bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, cons
 }
 
 // A launch of 8-wave workgroups (one per compute unit: their LDS stages take
-// 135 KB) that would not give every compute unit one takes 4-wave workgroups
-// instead, two to a compute unit (GQA groups up to 4); if those still leave
+// 135 KB) that would not give every compute unit one, or would end on a
+// partial round, takes 4-wave workgroups instead, two to a compute unit (GQA
+// groups up to 4); if those still leave
 // compute units idle, each tile's key blocks are split between as many
 // workgroups as fill them (at most split_max, each attending at least
 // split_min_blocks blocks; the kernel takes fewer for short tiles).
@@ -915,7 +916,14 @@ prefill_shape_info prefill_plan(const pool_view& p, const meta_view& m, uint32_t
     if (p.dtype == CKV_F32 || group == 0 || group > 4)
         return plan;
     const uint64_t grid8 = (uint64_t)m.n_tiles * group * p.kv_heads;
-    bool small = cu_count > 0 && grid8 < (uint64_t)cu_count;
+    const uint64_t cus = cu_count > 0 ? (uint64_t)cu_count : 0;
+    // Fewer 8-wave workgroups than compute units; or, under three rounds of
+    // them, a last round at most 5/8 full, whose compute units would wait
+    // out the others' tiles (4-wave workgroups, half the rows each, pack it:
+    // 9-12 sequences of config 4's shape 5-7 % faster, 17 and 20 3.5-6 %;
+    // full rounds or a last round 3/4 full are 3.5-8 % slower in 4-wave form).
+    const uint64_t rem = cus ? grid8 % cus : 0;
+    bool small = cus && (grid8 < cus || (grid8 < 3 * cus && rem > 0 && rem * 8 <= cus * 5));
     if (const char* forced = std::getenv("CKV_PREFILL_WAVES"))
         small = std::strtol(forced, nullptr, 10) == 4;
     if (!small)

@@ -335,8 +335,19 @@ TEST("prefill launch shape: 8-wave workgroups when they fill the GPU")
     // config 4: 64 sequences x 512 rows = 128 tiles, 8 kv heads, 16 q heads
     const auto c4 = prefill_shape_for(128, 8, 16, 256);
     CHECK(c4.waves == 8 && c4.n_split == 1 && c4.records_floats == 0 && c4.counters == 0);
-    // exactly one 8-wave workgroup per compute unit: 8-wave
+    // exactly one 8-wave workgroup per compute unit, or whole rounds of them: 8-wave
     CHECK(prefill_shape_for(16, 8, 16, 256).waves == 8);
+    CHECK(prefill_shape_for(32, 8, 16, 256).waves == 8);
+    CHECK(prefill_shape_for(48, 8, 16, 256).waves == 8);
+    // a last round 3/4 full (448 = 1.75 rounds): 8-wave
+    CHECK(prefill_shape_for(28, 8, 16, 256).waves == 8);
+    // a last round at most 5/8 full under three rounds: 4-wave, no key split
+    for (uint32_t tiles : { 18u, 24u, 34u, 40u }) {
+        const auto s = prefill_shape_for(tiles, 8, 16, 256);
+        CHECK(s.waves == 4 && s.n_split == 1 && s.records_floats == 0);
+    }
+    // from three rounds on: 8-wave (56 tiles = 3.5 rounds)
+    CHECK(prefill_shape_for(56, 8, 16, 256).waves == 8);
     // GQA groups of 8 always take 8-wave workgroups, and f32 pools their own kernel
     CHECK(prefill_shape_for(1, 8, 64, 256).waves == 8);
     CHECK(prefill_shape_for(1, 8, 16, 256, CKV_F32).waves == 8);

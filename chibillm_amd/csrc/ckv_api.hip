@@ -335,6 +335,20 @@ void heaviest_first(std::vector<uint32_t>& tiles)
     tiles.swap(sorted);
 }
 
+// The 32-key blocks the batch's shortest query tile attends (through its last
+// row).
+uint32_t shortest_tile_blocks(const std::vector<uint32_t>& tiles)
+{
+    const size_t n = tiles.size() / tile_entry_words;
+    uint64_t least = n ? UINT64_MAX : 0;
+    for (size_t t = 0; t < n; ++t) {
+        const uint64_t rows = tiles[tile_entry_words * t + 1];
+        const uint64_t first = tiles[tile_entry_words * t + 2];
+        least = std::min<uint64_t>(least, (first + rows - 1) / 32 + 1);
+    }
+    return (uint32_t)least;
+}
+
 // Words of the fast decode plan in the metadata block: the segments'
 // entries, each row's first partial record, then the cut rows.
 size_t plan_words(const decode_plan_shape& shape, size_t rows)
@@ -1281,6 +1295,7 @@ int ckv_tables_upload(ckv_pool* pool, const uint32_t* block_table, size_t n_entr
     m.slots = pool->d_meta + s_slots;
     m.tiles = pool->d_meta + s_tiles;
     m.n_tiles = (uint32_t)(tiles.size() / tile_entry_words);
+    m.tile_blocks = shortest_tile_blocks(tiles);
     adopt_batch(pool, rows, n_entries, slots != nullptr, shared, fusable, with_plan, false);
     return CKV_OK;
 }
@@ -1568,6 +1583,7 @@ int ckv_batch_upload(ckv_pool* pool, const uint32_t* seq, const uint32_t* first_
     m.slots = d + s_slots;
     m.tiles = d + s_tiles;
     m.n_tiles = (uint32_t)(tiles.size() / tile_entry_words);
+    m.tile_blocks = shortest_tile_blocks(tiles);
     adopt_batch(pool, rows, pool->seq_max * pool->seq_cap, with_slots != 0, shared, fusable,
                 with_plan, true);
     return CKV_OK;

@@ -55,6 +55,7 @@ struct meta_view {
     uint32_t n_items;
     uint32_t chunk; // tokens per decode work item, a multiple of 16
     uint32_t n_tiles;
+    uint32_t tile_blocks; // 32-key blocks the batch's shortest query tile attends (host side)
     uint32_t mean_pages; // pages attended per row, mean over the batch (host side)
     uint32_t n_plan;      // workgroups per kv head of the fast decode (the entries they start at)
     uint32_t n_segments;  // entries of plan

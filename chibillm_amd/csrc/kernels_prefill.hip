@@ -908,6 +908,10 @@ bool prefill_supported(const pool_view& p, uint32_t q_heads, const void* q, cons
 // workgroups as fill them (at most split_max, each attending at least
 // split_min_blocks blocks; the kernel takes fewer for short tiles).
 // CKV_PREFILL_WAVES (4 or 8), CKV_PREFILL_SPLIT and CKV_PREFILL_SPLIT_MIN (blocks) override.
+// a launch of more than half a round of 8-wave workgroups, and less than one,
+// takes 4-wave workgroups unless its shortest tile attends more 32-key blocks
+constexpr uint32_t sub_round_max_blocks = 40;
+
 prefill_shape_info prefill_plan(const pool_view& p, const meta_view& m, uint32_t q_heads,
                                 int cu_count)
 {
@@ -922,8 +926,19 @@ prefill_shape_info prefill_plan(const pool_view& p, const meta_view& m, uint32_t
     // out the others' tiles (4-wave workgroups, half the rows each, pack it:
     // 9-12 sequences of config 4's shape 5-7 % faster, 17 and 20 3.5-6 %;
     // full rounds or a last round 3/4 full are 3.5-8 % slower in 4-wave form).
+    // Under one round, 4-wave workgroups fill the compute units, and split
+    // long tiles' keys while at most half of them hold an 8-wave workgroup;
+    // past half, without a split, they lose to 8-wave workgroups when every
+    // tile is long (6 sequences of 512 rows over 0 or 512 tokens 15 % and 7 %
+    // faster in 4-wave form, over 1,008, 2,000 and 6,000 tokens 1 %, 5 % and
+    // 12 % slower); batches that mix short and long tiles (the churn's) keep
+    // the 4-wave form, whose smaller workgroups even out the tiles' lengths.
     const uint64_t rem = cus ? grid8 % cus : 0;
-    bool small = cus && (grid8 < cus || (grid8 < 3 * cus && rem > 0 && rem * 8 <= cus * 5));
+    bool small = false;
+    if (cus && grid8 < cus)
+        small = 2 * grid8 <= cus || m.tile_blocks <= sub_round_max_blocks;
+    else if (cus)
+        small = grid8 < 3 * cus && rem > 0 && rem * 8 <= cus * 5;
     if (const char* forced = std::getenv("CKV_PREFILL_WAVES"))
         small = std::strtol(forced, nullptr, 10) == 4;
     if (!small)

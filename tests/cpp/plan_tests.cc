@@ -292,7 +292,7 @@ TEST("random batches at random GPU sizes: every plan is well formed")
 namespace {
 
 ckv::prefill_shape_info prefill_shape_for(uint32_t n_tiles, uint32_t kv_heads, uint32_t q_heads,
-                                          int cus, int dtype = CKV_BF16)
+                                          int cus, int dtype = CKV_BF16, uint32_t tile_blocks = 75)
 {
     ckv::pool_view p {};
     p.kv_heads = kv_heads;
@@ -302,6 +302,7 @@ ckv::prefill_shape_info prefill_shape_for(uint32_t n_tiles, uint32_t kv_heads, u
     p.dtype = dtype;
     ckv::meta_view m {};
     m.n_tiles = n_tiles;
+    m.tile_blocks = tile_blocks;
     return ckv::prefill_plan(p, m, q_heads, cus);
 }
 
@@ -365,10 +366,16 @@ TEST("prefill launch shape: small launches take 4-wave workgroups and split keys
     // four sequences: 8 tiles -> 256 pairs, two ranges each fill two per compute unit
     const auto four = prefill_shape_for(8, 8, 16, 256);
     CHECK(four.waves == 4 && four.n_split == 2 && four.counters == 256);
-    // never more than split_max ranges, and a launch of one pair per CU takes none
+    // never more than split_max ranges
     CHECK(prefill_shape_for(1, 1, 1, 256).n_split == ckv::split_max);
-    const auto full = prefill_shape_for(15, 8, 16, 256); // 240 units: 480 pairs
+    // past half a round (240 units: 480 pairs, no split): 4-wave for short tiles only
+    const auto full = prefill_shape_for(15, 8, 16, 256, CKV_BF16, 30);
     CHECK(full.waves == 4 && full.n_split == 1 && full.records_floats == 0);
+    CHECK(prefill_shape_for(15, 8, 16, 256, CKV_BF16, 75).waves == 8);
+    CHECK(prefill_shape_for(12, 8, 16, 256, CKV_BF16, 40).waves == 4);
+    CHECK(prefill_shape_for(12, 8, 16, 256, CKV_BF16, 41).waves == 8);
+    // up to half a round: 4-wave whatever the tiles' lengths
+    CHECK(prefill_shape_for(8, 8, 16, 256, CKV_BF16, 500).waves == 4);
 }
 
 TEST("prefill launch shape: the environment overrides")

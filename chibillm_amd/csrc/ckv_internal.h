@@ -391,7 +391,7 @@ hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m,
                           prefill_split split);
 hipError_t launch_prefill_f32(hipStream_t s, const pool_view& p, const meta_view& m,
                               uint32_t layer, const void* q, uint32_t q_heads, float scale,
-                              void* out, const void* gate);
+                              void* out, const void* gate, prefill_split split);
 
 // ---- launchers (kernels_rope.hip) --------------------------------------------------
 // theta^(-2j/rotary) in float for j < rotary/2 (src/metal/metal_kernels.mm:186-191)

@@ -42,6 +42,7 @@
 // the pool), so no page outside a row's table is touched and masked keys
 // carry finite zeros into P.V.
 #include "ckv_internal.h"
+#include "prefill_records.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -147,46 +148,6 @@ __device__ __forceinline__ void wait_dma(uint32_t outstanding)
         __builtin_amdgcn_s_waitcnt(0x0F72); // vmcnt(2)
     else
         __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0)
-}
-
-// The split tiles' records pass between workgroups as the decode's split-K
-// partial records do (kernels_decode.hip), at 16 bytes per access: buffer
-// stores and loads with the sc1 cache policy, the same instructions at the
-// same policy that LLVM emits for relaxed agent-scope atomic stores and loads
-// on gfx950 (global/buffer_store/load sc1: the store writes through, the
-// load misses any L2 line that could be stale, so every XCD sees the data in
-// memory without an L2 writeback); a wait for the stores' completion before
-// one thread's relaxed agent-scope fetch-add counts the share in; the loads
-// of the share that arrives last are issued after that fetch-add returns.
-#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
-#error "kernels_prefill.hip's split-key handoff relies on gfx950's memory system; build for gfx950"
-#endif
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-constexpr int cache_sc1 = 16; // the buffer builtins' cache-policy operand: sc1
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t record_rsrc(float* base, uint32_t bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ void agent_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, float a,
-                                             float b, float c, float d)
-{
-    const u32x4_t v = { __float_as_uint(a), __float_as_uint(b), __float_as_uint(c),
-                        __float_as_uint(d) };
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, cache_sc1);
-}
-
-__device__ __forceinline__ u32x4_t agent_load4(__amdgpu_buffer_rsrc_t r, uint32_t off)
-{
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, cache_sc1);
-}
-
-// Waits until every vector memory access this wave issued (stores included)
-// has completed; a compiler barrier too.
-__device__ __forceinline__ void wait_vector_memory()
-{
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 __device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* ptr)
@@ -917,7 +878,25 @@ prefill_shape_info prefill_plan(const pool_view& p, const meta_view& m, uint32_t
 {
     prefill_shape_info plan { 8, 1, split_min_blocks, 0, 0 };
     const uint32_t group = p.kv_heads ? q_heads / p.kv_heads : 0;
-    if (p.dtype == CKV_F32 || group == 0 || group > 4)
+    if (const char* forced = std::getenv("CKV_PREFILL_SPLIT_MIN"))
+        plan.min_blocks = (uint32_t)std::max(1L, std::strtol(forced, nullptr, 10));
+    if (p.dtype == CKV_F32) {
+        // f32 pools: 8-wave workgroups, two to a compute unit; a launch that
+        // gives at most one to each splits its long tiles' keys to fill them
+        const uint64_t grid = (uint64_t)m.n_tiles * group * p.kv_heads;
+        uint64_t split = grid && cu_count > 0 && grid <= (uint64_t)cu_count
+            ? 2 * (uint64_t)cu_count / grid
+            : 1;
+        if (const char* forced = std::getenv("CKV_PREFILL_SPLIT"))
+            split = (uint64_t)std::max(1L, std::strtol(forced, nullptr, 10));
+        plan.n_split = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(split, 1), split_max);
+        if (plan.n_split > 1) {
+            plan.records_floats = grid * plan.n_split * 256 * prefill_record_floats;
+            plan.counters = grid;
+        }
+        return plan;
+    }
+    if (group == 0 || group > 4)
         return plan;
     const uint64_t grid8 = (uint64_t)m.n_tiles * group * p.kv_heads;
     const uint64_t cus = cu_count > 0 ? (uint64_t)cu_count : 0;
@@ -949,8 +928,6 @@ prefill_shape_info prefill_plan(const pool_view& p, const meta_view& m, uint32_t
     if (const char* forced = std::getenv("CKV_PREFILL_SPLIT"))
         split = (uint64_t)std::max(1L, std::strtol(forced, nullptr, 10));
     plan.n_split = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(split, 1), split_max);
-    if (const char* forced = std::getenv("CKV_PREFILL_SPLIT_MIN"))
-        plan.min_blocks = (uint32_t)std::max(1L, std::strtol(forced, nullptr, 10));
     if (plan.n_split > 1) {
         plan.records_floats = pairs * plan.n_split * 128 * prefill_record_floats;
         plan.counters = pairs;
@@ -963,12 +940,12 @@ hipError_t launch_prefill(hipStream_t s, const pool_view& p, const meta_view& m,
                           const void* gate, const prefill_shape_info& plan,
                           prefill_split split)
 {
-    if (p.dtype == CKV_F32)
-        return launch_prefill_f32(s, p, m, layer, q, q_heads, scale, out, gate);
     if (plan.n_split > 1 && (!split.records || !split.arrivals))
         return hipErrorInvalidValue;
     split.n_split = plan.n_split;
     split.min_blocks = plan.min_blocks;
+    if (p.dtype == CKV_F32)
+        return launch_prefill_f32(s, p, m, layer, q, q_heads, scale, out, gate, split);
     const float c = scale * log2e;
     switch (q_heads / p.kv_heads) {
     case 1:

@@ -32,7 +32,13 @@
 // start 16 bytes apart in the banks), the next block's loads in flight while
 // the current one is multiplied, one barrier per block. Keys past the tile's
 // last position are staged as zeros and never read from the pool.
+//
+// A launch that leaves compute units idle splits each long tile's key blocks
+// between up to 8 workgroups, as the 16-bit kernel does (kernels_prefill.hip):
+// each stores its unnormalised state as 16-byte records, and the last to
+// arrive folds them in range order.
 #include "ckv_internal.h"
+#include "prefill_records.h"
 
 namespace ckv {
 namespace {
@@ -64,14 +70,19 @@ __device__ __forceinline__ float sigmoid(float g)
 template <int G>
 __global__ __launch_bounds__(64 * waves, 2) void prefill_f32_kernel(
     pool_view p, meta_view md, uint32_t layer, const float* __restrict__ q,
-    float* __restrict__ out, uint32_t q_heads, float c, const float* __restrict__ gate)
+    float* __restrict__ out, uint32_t q_heads, float c, const float* __restrict__ gate,
+    prefill_split split_scratch)
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[n_stages * stage_bytes];
     constexpr uint32_t tile_rows = 256 / G;
 
     const uint32_t kv_heads = p.kv_heads;
     const uint32_t kvh = blockIdx.x % kv_heads;
-    const uint32_t rest = blockIdx.x / kv_heads;
+    // key ranges vary slowest: every tile's first range is dispatched first
+    const uint32_t n_split = split_scratch.n_split;
+    const uint32_t n_rest = md.n_tiles * G;
+    const uint32_t rest = blockIdx.x / kv_heads % n_rest;
+    const uint32_t part = blockIdx.x / kv_heads / n_rest; // this workgroup's range of the keys
     const uint32_t sub = rest % G;
     const uint32_t tile = rest / G;
     // the tile: first row, rows, first position, table offset
@@ -87,6 +98,12 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_f32_kernel(
     const uint32_t* table = md.table + te.w;
     const uint32_t n_blocks = pos_last / block_keys + 1;
     const uint32_t last_entry = pos_last / page_tokens;
+    // key blocks [kb_begin, kb_end) of this workgroup
+    const uint32_t n_parts = prefill_range_count(n_blocks, n_split, split_scratch.min_blocks);
+    if (part >= n_parts)
+        return;
+    uint32_t kb_begin, kb_end;
+    prefill_range_bounds(n_blocks, n_parts, part, kb_begin, kb_end);
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63, wave = tid >> 6;
@@ -194,10 +211,12 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_f32_kernel(
                 o[a] *= alpha;
             m = m_new;
         }
+        // a range of the keys may hold none a query attends yet (m = -inf)
+        const float mm = m == -__builtin_inff() ? 0.0f : m;
         float sum = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            s[r] = __builtin_amdgcn_exp2f(s[r] - m);
+            s[r] = __builtin_amdgcn_exp2f(s[r] - mm);
             sum += s[r];
         }
         l += sum;
@@ -214,11 +233,11 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_f32_kernel(
         }
     };
 
-    fetch(0);
-    store(0);
+    fetch(kb_begin);
+    store(kb_begin);
     __syncthreads();
-    for (uint32_t kb = 0; kb < n_blocks; ++kb) {
-        const bool more = kb + 1 < n_blocks; // workgroup-uniform
+    for (uint32_t kb = kb_begin; kb < kb_end; ++kb) {
+        const bool more = kb + 1 < kb_end; // workgroup-uniform
         if (more)
             fetch(kb + 1);
         attend(kb);
@@ -227,9 +246,86 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_f32_kernel(
         __syncthreads();
     }
 
+    float lt = l + __shfl_xor(l, 32); // the query's denominator (both lane halves)
+    if (n_parts > 1) {
+        // A range of a split tile: its record is 33 chunks of 4 floats per query
+        // vector, chunk 0 = [max (log2 units), denominator, 0, 0] and chunk
+        // 1 + j = features 4j .. 4j + 3 (lane half h, element r of the four
+        // accumulators: chunk 1 + 8 (r / 4) + 4h + r % 4), chunk-major with the
+        // workgroup's 256 query vectors consecutive. The range that arrives
+        // last folds every range's record in range order, two per round trip,
+        // with weights 2^(m_s - M).
+        const uint32_t pair = rest * kv_heads + kvh;
+        const uint32_t qv = wave * 32 + n;
+        constexpr uint32_t QV = 32 * waves, chunks = prefill_record_floats / 4;
+        const __amdgpu_buffer_rsrc_t rs = record_rsrc(
+            split_scratch.records + (uint64_t)pair * n_split * (chunks * QV * 4),
+            n_split * chunks * QV * 16);
+        auto off = [&](uint32_t share, uint32_t chunk) {
+            return ((share * chunks + chunk) * QV + qv) * 16u;
+        };
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            agent_store4(rs, off(part, 1 + 8 * (r >> 2) + 4 * h + (r & 3)), o[0][r], o[1][r],
+                         o[2][r], o[3][r]);
+        if (h == 0)
+            agent_store4(rs, off(part, 0), m, lt, 0.0f, 0.0f);
+        wait_vector_memory();
+        __syncthreads(); // also: every wave is past its LDS reads
+        uint32_t* const last_flag = reinterpret_cast<uint32_t*>(lds);
+        if (tid == 0) {
+            const uint32_t before = __hip_atomic_fetch_add(split_scratch.arrivals + pair, 1u,
+                                                           __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t last = before == n_parts - 1;
+            if (last)
+                __hip_atomic_store(split_scratch.arrivals + pair, 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            *last_flag = last;
+        }
+        __syncthreads();
+        if (!*last_flag)
+            return;
+        auto weight = [&](float ms, float to) { // 0 for a range that attended nothing
+            return ms == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(ms - to);
+        };
+        float M = -__builtin_inff();
+        lt = 0.0f;
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+            o[a] = f32x16_t {};
+        for (uint32_t sh = 0; sh < n_parts; sh += 2) {
+            const uint32_t s1 = min(sh + 1, n_parts - 1);
+            const u32x4_t ha = agent_load4(rs, off(sh, 0)), hb = agent_load4(rs, off(s1, 0));
+            u32x4_t va[16], vb[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                va[r] = agent_load4(rs, off(sh, 1 + 8 * (r >> 2) + 4 * h + (r & 3)));
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                vb[r] = agent_load4(rs, off(s1, 1 + 8 * (r >> 2) + 4 * h + (r & 3)));
+            const float ma = __uint_as_float(ha[0]);
+            const float mb = sh + 1 < n_parts ? __uint_as_float(hb[0]) : -__builtin_inff();
+            const float m_new = fmaxf(M, fmaxf(ma, mb));
+            const float keep = weight(M, m_new), wa = weight(ma, m_new), wb = weight(mb, m_new);
+            M = m_new;
+            lt = lt * keep + __uint_as_float(ha[1]) * wa;
+            lt += __uint_as_float(hb[1]) * wb;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+#pragma unroll
+                for (int a = 0; a < 4; ++a) {
+                    float acc = o[a][r] * keep;
+                    acc += __uint_as_float(va[r][a]) * wa;
+                    o[a][r] = acc + __uint_as_float(vb[r][a]) * wb;
+                }
+        }
+        // lt > 0 for a valid row: the tile's first range attends key 0
+    }
+
     if (!valid)
         return;
-    const float inv = 1.0f / (l + __shfl_xor(l, 32));
+    const float inv = 1.0f / lt;
     float* dst = out + qoff;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -250,11 +346,11 @@ __global__ __launch_bounds__(64 * waves, 2) void prefill_f32_kernel(
 template <int G>
 hipError_t launch_g(hipStream_t s, const pool_view& p, const meta_view& m, uint32_t layer,
                     const void* q, uint32_t q_heads, float c, void* out, uint32_t grid,
-                    const void* gate)
+                    const void* gate, prefill_split split)
 {
     hipLaunchKernelGGL((prefill_f32_kernel<G>), dim3(grid), dim3(64 * waves), 0, s, p, m, layer,
                        static_cast<const float*>(q), static_cast<float*>(out), q_heads, c,
-                       static_cast<const float*>(gate));
+                       static_cast<const float*>(gate), split);
     return hipGetLastError();
 }
 
@@ -262,10 +358,13 @@ hipError_t launch_g(hipStream_t s, const pool_view& p, const meta_view& m, uint3
 
 hipError_t launch_prefill_f32(hipStream_t s, const pool_view& p, const meta_view& m,
                               uint32_t layer, const void* q, uint32_t q_heads, float scale,
-                              void* out, const void* gate)
+                              void* out, const void* gate, prefill_split split)
 {
     const uint32_t group = q_heads / p.kv_heads;
-    const uint64_t grid = (uint64_t)m.n_tiles * group * p.kv_heads;
+    if (split.n_split < 1 || split.min_blocks < 1
+        || (split.n_split > 1 && (!split.records || !split.arrivals)))
+        return hipErrorInvalidValue;
+    const uint64_t grid = (uint64_t)m.n_tiles * group * p.kv_heads * split.n_split;
     if (!grid)
         return hipSuccess;
     if (grid > 0x7FFFFFFFull)
@@ -273,13 +372,13 @@ hipError_t launch_prefill_f32(hipStream_t s, const pool_view& p, const meta_view
     const float c = scale * log2e;
     switch (group) {
     case 1:
-        return launch_g<1>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
+        return launch_g<1>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate, split);
     case 2:
-        return launch_g<2>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
+        return launch_g<2>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate, split);
     case 4:
-        return launch_g<4>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
+        return launch_g<4>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate, split);
     case 8:
-        return launch_g<8>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate);
+        return launch_g<8>(s, p, m, layer, q, q_heads, c, out, (uint32_t)grid, gate, split);
     default:
         return hipErrorInvalidValue;
     }

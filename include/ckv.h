@@ -304,8 +304,8 @@ int ckv_append_decode(ckv_pool* pool, size_t layer, const void* keys, const void
  * matrix cores for head_dim 128, 16-token pages, 1, 2, 4 or 8 q heads per kv
  * head and scale > 0 (bf16/fp16 products for 16-bit pools, exact fp32
  * products for f32 pools); other geometries and scales take the decode form
- * row by row, with the same results. A 16-bit launch too small to fill the GPU
- * splits each tile's keys between workgroups and merges their partial states
+ * row by row, with the same results. A launch too small to fill the GPU
+ * splits each long tile's keys between workgroups and merges their partial states
  * in the pool's scratch (grown on first use, like the decode's split-K
  * records); the merge order is fixed, so results do not depend on timing.
  * Same arguments and checks as ckv_decode_attention. */

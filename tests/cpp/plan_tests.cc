@@ -352,7 +352,14 @@ TEST("prefill launch shape: 8-wave workgroups when they fill the GPU")
     // GQA groups of 8 always take 8-wave workgroups, and f32 pools their own kernel
     CHECK(prefill_shape_for(1, 8, 64, 256).waves == 8);
     CHECK(prefill_shape_for(1, 8, 16, 256, CKV_F32).waves == 8);
-    CHECK(prefill_shape_for(1, 8, 16, 256, CKV_F32).n_split == 1);
+    // f32: 8-wave workgroups two to a compute unit; at most one to each splits
+    const auto f32_small = prefill_shape_for(1, 8, 16, 256, CKV_F32); // 16 workgroups
+    CHECK(f32_small.n_split == ckv::split_max && f32_small.counters == 16);
+    CHECK(f32_small.records_floats == 16ull * ckv::split_max * 256 * ckv::prefill_record_floats);
+    CHECK(prefill_shape_for(8, 8, 16, 256, CKV_F32).n_split == 4);  // 128 workgroups
+    CHECK(prefill_shape_for(16, 8, 16, 256, CKV_F32).n_split == 2); // 256: one per CU
+    CHECK(prefill_shape_for(17, 8, 16, 256, CKV_F32).n_split == 1); // 272
+    CHECK(prefill_shape_for(128, 8, 16, 256, CKV_F32).n_split == 1); // config 4
 }
 
 TEST("prefill launch shape: small launches take 4-wave workgroups and split keys to fill")

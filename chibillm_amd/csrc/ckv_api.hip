@@ -2007,8 +2007,8 @@ int ckv_append_decode_noalloc(ckv_pool* pool, size_t layer, const void* keys, co
     if (!decode_fast_applies(view, (uint32_t)q_heads, queries, output))
         return fail_fixed(ctx, CKV_E_INVALID_ARGUMENT,
                           "no-allocation decode: needs head_dim 128, 16-token pages, 1, 2, 4 "
-                          "or 8 q heads per kv head (1, 2 or 4 for f32 pools) and 16-byte "
-                          "aligned pools, queries and output");
+                          "or 8 q heads per kv head and 16-byte aligned pools, queries and "
+                          "output");
     // a batch of multi-row query tiles is refused whatever ran on it before
     // (a decode launch or ckv_decode_plan would have derived its plan)
     if (pool->shared_tile || !pool->plan_ready)

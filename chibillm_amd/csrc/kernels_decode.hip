@@ -242,7 +242,7 @@ __host__ __device__ constexpr bool wide_lanes(uint32_t group, int dtype)
 }
 
 // Eight q heads of f32 pages do not fit 256 registers a lane (the kernel
-// would spill): such pools take the generic kernel.
+// would spill): such pools run the four-head kernel twice (launch_fast<8>).
 __host__ __device__ constexpr bool fast_fits(uint32_t group, int dtype)
 {
     return !(group == 8 && dtype == CKV_F32);
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(wide_lanes(G, DT) ? 512 : 1024, wide_lanes(G, DT) ?
     pool_view p, meta_view m, uint32_t layer, const char* __restrict__ q, uint32_t q_heads,
     float scale_log2, void* __restrict__ out, const char* __restrict__ k_in,
     const char* __restrict__ v_in, const void* __restrict__ gate, rope_table64 freq,
-    uint32_t rotary, split_scratch split)
+    uint32_t rotary, split_scratch split, uint32_t group_stride, uint32_t head_base)
 {
     static_assert(!(ROPE && DT == CKV_F32), "the fused rotation works on 16-bit pairs");
     constexpr bool F16 = DT == CKV_F16;
@@ -361,6 +361,9 @@ __global__ __launch_bounds__(wide_lanes(G, DT) ? 512 : 1024, wide_lanes(G, DT) ?
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // a scalar
     const uint32_t H = p.kv_heads;
     const uint32_t kv_head = blockIdx.x % H;
+    // the workgroup's q heads: qh0 .. qh0 + G - 1 (group_stride = G and
+    // head_base = 0, or one of the passes over half of a larger group)
+    const uint32_t qh0 = kv_head * group_stride + head_base;
     const uint32_t row_bytes = p.features * ES;
     const uint64_t page_bytes = (uint64_t)BS * row_bytes;
     const char* kl = static_cast<const char*>(p.keys) + (uint64_t)layer * p.layer_elems * ES;
@@ -392,14 +395,14 @@ __global__ __launch_bounds__(wide_lanes(G, DT) ? 512 : 1024, wide_lanes(G, DT) ?
         float gate_early = 0.0f; // the first epilogue iteration's gate value (one register)
         if constexpr (GATED) {
             if (tid < G * D)
-                gate_early = load_elem<DT>(gate, ((uint64_t)row * q_heads + kv_head * G) * D + tid);
+                gate_early = load_elem<DT>(gate, ((uint64_t)row * q_heads + qh0) * D + tid);
         }
         const uint32_t* tbl = m.table + (e0.w - pg_first); // the row's table
 
         row8 qv[G];
 #pragma unroll
         for (int g = 0; g < G; ++g)
-            qv[g] = load8<DT>(q + ((uint64_t)row * q_heads + kv_head * G + g) * D * ES + part * 16);
+            qv[g] = load8<DT>(q + ((uint64_t)row * q_heads + qh0 + g) * D * ES + part * 16);
 
         // ROPE: this lane's 8 features (pairs j0 .. j0 + 7) and their rotation;
         // every lane of the wave takes part in the exchanges. The queries and the
@@ -648,7 +651,7 @@ __global__ __launch_bounds__(wide_lanes(G, DT) ? 512 : 1024, wide_lanes(G, DT) ?
             }
         };
         auto emit = [&](uint32_t g, uint32_t f, uint32_t it, float o) {
-            const uint64_t at = ((uint64_t)row * q_heads + kv_head * G + g) * D + f;
+            const uint64_t at = ((uint64_t)row * q_heads + qh0 + g) * D + f;
             if constexpr (GATED)
                 o *= sigmoid(it == 0 ? gate_early : load_elem<DT>(gate, at));
             store_elem<DT>(out, at, o);
@@ -667,7 +670,7 @@ __global__ __launch_bounds__(wide_lanes(G, DT) ? 512 : 1024, wide_lanes(G, DT) ?
         constexpr uint32_t RF = D + 4;
         const uint64_t record_stride = (uint64_t)q_heads * RF; // between a row's chunks
         float* const records = split.records
-            + ((uint64_t)m.split_first[row] * q_heads + kv_head * G) * RF;
+            + ((uint64_t)m.split_first[row] * q_heads + qh0) * RF;
         for (uint32_t t = tid; t < G * D; t += blockDim.x) {
             const uint32_t g = t / D, f = t % D;
             float M, d, a;
@@ -996,10 +999,23 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
                        const void* q, uint32_t q_heads, float scale_log2, void* out, int dt,
                        const void* k_in, const void* v_in, const void* gate, int cu_count,
                        split_scratch split, const rope_table* rope = nullptr,
-                       uint32_t rotary = 0)
+                       uint32_t rotary = 0, uint32_t group_stride = G, uint32_t head_base = 0)
 {
     if (!m.plan || (m.n_cut && (!split.records || !split.arrivals)))
         return hipErrorInvalidValue;
+    if constexpr (G == 8) {
+        // f32 pages at 8 q heads per kv head: two passes over 4 heads each (one
+        // pass holds twice the registers its 512-lane workgroups allow); each
+        // reads the K/V once more, the fused append writes the same token twice
+        if (dt == CKV_F32) {
+            hipError_t e = launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, dt, k_in,
+                                          v_in, gate, cu_count, split, rope, rotary, 8, 0);
+            if (e == hipSuccess)
+                e = launch_fast<4>(s, p, m, layer, q, q_heads, scale_log2, out, dt, k_in, v_in,
+                                   gate, cu_count, split, rope, rotary, 8, 4);
+            return e;
+        }
+    }
     const uint32_t units = m.n_plan * p.kv_heads;
     const uint32_t waves = fast_waves(G, dt, units, cu_count, m.mean_pages, m.split_pages);
     const dim3 grid(units), block(64 * waves);
@@ -1020,7 +1036,8 @@ hipError_t launch_fast(hipStream_t s, const pool_view& p, const meta_view& m, ui
     case (ROPE_ ? 16 : 0) | (DT_ << 2) | (FUSED_ ? 2 : 0) | (GATED_ ? 1 : 0):                  \
         if constexpr (fast_fits(G, DT_))                                                       \
             decode_wg_kernel<G, DT_, FUSED_, GATED_, ROPE_><<<grid, block, lds, s>>>(          \
-                p, m, layer, qq, q_heads, scale_log2, out, ki, vi, gate, f64, rotary, split);  \
+                p, m, layer, qq, q_heads, scale_log2, out, ki, vi, gate, f64, rotary, split,   \
+                group_stride, head_base);                                                      \
         else                                                                                   \
             return hipErrorInvalidValue;                                                       \
         break;
@@ -1357,8 +1374,10 @@ void write_decode_plan(const std::vector<uint32_t>& positions,
 bool decode_uses_fast_path(const pool_view& p, uint32_t q_heads)
 {
     const uint32_t G = q_heads / p.kv_heads;
+    // f32 at G = 8 runs as two passes of G = 4 (launch_fast<8>)
     return p.head_dim == 128 && p.block_size == 16
-        && (G == 1 || G == 2 || G == 4 || G == 8) && fast_fits(G, p.dtype) && aligned16(p.keys)
+        && (G == 1 || G == 2 || G == 4 || G == 8)
+        && (fast_fits(G, p.dtype) || (G == 8 && p.dtype == CKV_F32)) && aligned16(p.keys)
         && aligned16(p.values);
 }
 

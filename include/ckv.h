@@ -277,8 +277,8 @@ int ckv_gather(ckv_pool* pool, size_t layer, size_t table_offset, size_t table_l
  * out = softmax(q . k * scale) . v with fp32 accumulation. queries and
  * output are device [rows, q_heads*head_dim] of the pool dtype.
  * Decode form: the q heads of a GQA group share every K/V read. Pools with
- * head_dim 128, 16-token pages and 1, 2, 4 or 8 q heads per kv head (1, 2 or
- * 4 for f32 pools) take one workgroup per (row, kv_head),
+ * head_dim 128, 16-token pages and 1, 2, 4 or 8 q heads per kv head (f32 pools
+ * with 8 in two passes of 4) take one workgroup per (row, kv_head),
  * or per page chunk of rows the batch plan cuts (ckv_decode_plan), the chunks
  * merged by the last to finish; other geometries take split-KV over token
  * chunks and a merge launch. Both are the split-K of
@@ -329,8 +329,8 @@ int ckv_attention(ckv_pool* pool, size_t layer, const void* queries, size_t q_he
  * the rest the records. It needs what the allocating calls already set up:
  * a batch of single-row query tiles uploaded with ckv_tables_upload or
  * ckv_batch_upload (its plan goes up with it), and the fast decode's geometry
- * (head_dim 128, 16-token pages, 1, 2, 4 or 8 q heads per kv head, 1, 2 or 4
- * for f32 pools, 16-byte aligned pools, queries and output); a batch with a multi-row query
+ * (head_dim 128, 16-token pages, 1, 2, 4 or 8 q heads per kv head, 16-byte
+ * aligned pools, queries and output); a batch with a multi-row query
  * tile is refused whatever ran on it before. Otherwise, and when the batch's
  * records exceed the array (n_records * q_heads * 528 bytes > 16 MiB - 256 KiB
  * or n_records * kv_heads * 4 bytes > 256 KiB, see ckv_decode_plan), it

@@ -177,10 +177,10 @@ def test_noalloc_refuses_a_tiled_batch_whatever_ran_before(ctx):
 
 
 def test_noalloc_refuses_instead_of_allocating(ctx, monkeypatch):
-    """A batch of multi-row query tiles (no decode plan uploaded), an f32 pool
-    with 8 q heads per kv head (the generic kernel's geometry) and a plan whose
-    records exceed the 16 MiB array are refused with invalid_argument; nothing
-    is launched."""
+    """A batch of multi-row query tiles (no decode plan uploaded), a pool of
+    64-feature heads (the generic kernel's geometry) and a plan whose records
+    exceed the 16 MiB array are refused with invalid_argument; nothing is
+    launched."""
     q = torch.zeros(4, 2048, dtype=torch.bfloat16, device="cuda")
     kv = torch.zeros(4, 1024, dtype=torch.bfloat16, device="cuda")
     out = torch.empty_like(q)
@@ -202,12 +202,12 @@ def test_noalloc_refuses_instead_of_allocating(ctx, monkeypatch):
     assert e.value.name == "ckv.invalid_argument" and "16 MiB" in str(e.value)
     monkeypatch.delenv("CKV_DECODE_SPLIT")
     pool.close()
-    f32, _, _ = new_pool(ctx, (1, 4, 16, 8, 128), orc.F32)
-    f32.upload([0, 1, 2, 3], [0, 1, 2, 3], [1] * 4, [0] * 4, slots=[0, 16, 32, 48])
-    qf = torch.zeros(4, 64 * 128, device="cuda")
-    kf = torch.zeros(4, 1024, device="cuda")
+    narrow, _, _ = new_pool(ctx, (1, 4, 16, 8, 64), orc.BF16)
+    narrow.upload([0, 1, 2, 3], [0, 1, 2, 3], [1] * 4, [0] * 4, slots=[0, 16, 32, 48])
+    qn = torch.zeros(4, 16 * 64, dtype=torch.bfloat16, device="cuda")
+    kn = torch.zeros(4, 8 * 64, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(ckv.CkvError) as e:
-        f32.append_decode_noalloc(0, kf, kf, qf, 64, SCALE, torch.empty_like(qf))
-    assert e.value.name == "ckv.invalid_argument" and "f32" in str(e.value)
+        narrow.append_decode_noalloc(0, kn, kn, qn, 16, SCALE, torch.empty_like(qn))
+    assert e.value.name == "ckv.invalid_argument" and "head_dim 128" in str(e.value)
     ctx.sync()
-    f32.close()
+    narrow.close()

@@ -575,29 +575,36 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
         rescale();
     }
     // Iteration kb finishes block kb - 1 and scores block kb. The steady
-    // state runs iterations in pairs (kb odd, kb + 1) while kb + 6 < n_blocks:
+    // state runs iterations in pairs (kb odd, kb + 1) while kb + 8 < n_blocks:
     // the blocks such a pair loads (kb + 4, kb + 5) hold only keys inside the
-    // tile and the pages it fetches (blocks kb + 5, kb + 6) exist, so its loads,
+    // tile and the pages it fetches (blocks kb + 6, kb + 7) exist, so its loads,
     // fetches and waits take no checks, and the barrier's place is fixed (ODD).
     // Cutting the per-block scalar work this way (with the 32-bit page
     // offsets) made config 4's prefill 4.6 % faster.
-    // A steady iteration's blocks end at least 129 positions before the tile's
-    // last one ((kb + 2) * 32 <= (n_blocks - 5) * 32 <= pos_last - 128), so
+    // A steady iteration's blocks end at least 193 positions before the tile's
+    // last one ((kb + 2) * 32 <= (n_blocks - 7) * 32 <= pos_last - 192), so
     // with tiles of at most 128 rows (G >= 2) they end before the tile's first
     // position and need no mask: the scores' maxima then follow P.V in the
     // same basic block (1.2 % faster on config 4).
     constexpr bool steady_clear = G >= 2;
-    auto iteration = [&](uint32_t kb, auto steady, auto odd) {
+    auto iteration = [&](uint32_t kb, auto steady, auto odd, auto prio, uint32_t pa, uint32_t pb) {
         constexpr bool STEADY = decltype(steady)::value;
         if constexpr (STEADY)
-            load_block_steady(kb + 4);
+            load_full(__builtin_amdgcn_readfirstlane(pa), __builtin_amdgcn_readfirstlane(pb),
+                      lds_base + ((kb + 4) % n_stages) * stage_bytes);
         else if (kb + 4 < n_blocks)
             load_block(kb + 4);
         // The two waves of a SIMD (w and w + 4) take turns at the higher issue
         // priority block by block; with a fixed one the older runs ahead and
         // waits at the barrier (0.7 % faster on config 4; levels 0 and 3, four
         // levels, or turns every two blocks were 0.4 % faster to 1.8 % slower).
-        if (((wave_u >> 2) + kb) & 1)
+        // `prio` is the level when the caller knows it (0 or 1), else 2: the
+        // level follows from the wave and the block, a branch per block.
+        if constexpr (decltype(prio)::value == 1)
+            __builtin_amdgcn_s_setprio(1);
+        else if constexpr (decltype(prio)::value == 0)
+            __builtin_amdgcn_s_setprio(0);
+        else if (((wave_u >> 2) + kb) & 1)
             __builtin_amdgcn_s_setprio(1);
         else
             __builtin_amdgcn_s_setprio(0);
@@ -622,13 +629,45 @@ __global__ __launch_bounds__(64 * W, 2) void prefill_kernel(
     };
     using yes = std::true_type;
     using no = std::false_type;
+    using p0 = std::integral_constant<int, 0>;
+    using p1 = std::integral_constant<int, 1>;
+    using prt = std::integral_constant<int, 2>;
     uint32_t kb = 1;
-    for (; kb + 6 < n_blocks; kb += 2) { // kb odd: a barrier follows it
-        iteration(kb, yes {}, yes {});
-        iteration(kb + 1, yes {}, no {});
+    // The steady loop in two copies, one per half of the workgroup, so each
+    // sets its priority levels without a branch (kb odd: waves 0-3 at 1, then
+    // 0 at kb + 1; waves 4-7 the reverse): config 4 0.9-1.4 % faster. Its
+    // pairs load blocks kb + 4 and kb + 5 from pages fetched by the pair
+    // before; kb + 8 < n_blocks keeps those blocks inside the tile and the
+    // fetched pages (blocks kb + 6 and kb + 7, neither the last) in the table.
+    if (kb + 8 < n_blocks) {
+        // pages of blocks kb + 4 (fetched by block 4's load) and kb + 5
+        uint32_t a0 = page_a, b0 = page_b;
+        fetch_pages_unchecked(kb + 5);
+        uint32_t a1 = page_a, b1 = page_b;
+        auto pairs = [&](auto first, auto second) {
+            for (; kb + 8 < n_blocks; kb += 2) { // kb odd: a barrier follows it
+                iteration(kb, yes {}, yes {}, first, a0, b0);
+                iteration(kb + 1, yes {}, no {}, second, a1, b1);
+                // the next pair's pages, carried into it: a fetch used in the
+                // same trip is moved next to its use by the compiler, its
+                // latency exposed once per pair (0.7-0.9 % slower)
+                using c32 = const __attribute__((address_space(4))) uint32_t;
+                const auto* cb = (const __attribute__((address_space(4))) uint8_t*)(uintptr_t)table;
+                a0 = *(c32*)(cb + 8 * (kb + 6));
+                b0 = *(c32*)(cb + 8 * (kb + 6) + 4);
+                a1 = *(c32*)(cb + 8 * (kb + 7));
+                b1 = *(c32*)(cb + 8 * (kb + 7) + 4);
+            }
+        };
+        if (wave_u < 4)
+            pairs(p1 {}, p0 {});
+        else
+            pairs(p0 {}, p1 {});
+        page_a = a0; // block kb + 4, for the checked iterations
+        page_b = b0;
     }
     for (; kb < n_blocks; ++kb)
-        iteration(kb, no {}, no {});
+        iteration(kb, no {}, no {}, prt {}, 0u, 0u);
     } else {
         // Four stages, loads two blocks ahead, a barrier after every block:
         // block b is loaded in iteration b - 2 into the stage of block b - 4,

@@ -172,6 +172,62 @@ def test_ragged_tiles_every_group_size(ctx, group, code, waves, monkeypatch):
     pool.close()
 
 
+# (first position, rows): tiles whose last key block is block 7, 8, ..., 16, so
+# the 8-wave kernel's steady loop (pairs of blocks while kb + 8 < n_blocks)
+# runs zero to four times and leaves each possible remainder to the checked
+# iterations, in both halves of the workgroup
+BOUNDARIES = [(250, 6), (270, 18), (300, 20), (330, 22), (360, 24), (400, 16), (420, 28),
+              (470, 10), (500, 12), (520, 24)]
+
+
+@pytest.mark.parametrize("waves", [None, "8"])
+@pytest.mark.parametrize("group", [2, 4])
+def test_steady_loop_boundaries(ctx, group, waves, monkeypatch):
+    """Tiles of 8 to 17 key blocks through the prefill kernel against the
+    oracle (bf16)."""
+    if waves:
+        monkeypatch.setenv("CKV_PREFILL_WAVES", waves)
+    print(f"steady-loop boundaries group {group} waves {waves}", flush=True)
+    code = orc.BF16
+    H = 2
+    Hq = H * group
+    F = H * D
+    rng = orc.Mt64(91 + group)
+    lengths_tok = [start + n for start, n in BOUNDARIES]
+    blocks = sum(pages_for(n) for n in lengths_tok) + 3
+    perm = rng.permutation(blocks)
+    geom = (1, blocks, 16, H, D)
+    slot_count = blocks * 16
+    kc = rng.normal(slot_count * F, code)
+    vc = rng.normal(slot_count * F, code)
+    tables, at = [], 0
+    for n in lengths_tok:
+        tables.append(perm[at:at + pages_for(n)])
+        at += pages_for(n)
+    flat = np.concatenate(tables)
+    positions, offsets, lengths = [], [], []
+    at = 0
+    for (start, n), t in zip(BOUNDARIES, tables):
+        positions += list(range(start, start + n))
+        offsets += [at] * n
+        lengths += [len(t)] * n
+        at += len(t)
+    rows = len(positions)
+    q = rng.normal(rows * Hq * D, code).reshape(rows, Hq * D)
+    pool, kd, vd = new_pool(ctx, geom, code)
+    kd.copy_(to_dev(kc, code))
+    vd.copy_(to_dev(vc, code))
+    pool.upload(flat, offsets, lengths, positions)
+    expected = orc.Attention(geom, kc, vc, code, q, code, positions, flat, offsets, lengths, Hq,
+                             0, scale()).online_threads(8)
+    qd = to_dev(q, code)
+    out = torch.full_like(qd, float("nan"))
+    pool.prefill(0, qd, Hq, scale(), out)
+    ctx.sync()
+    assert_close(to_f32(out), expected, what=f"boundaries, group {group}, waves {waves}")
+    pool.close()
+
+
 # a long chunk over a long prefix (three tiles, the last of one row), a short
 # sequence beside it, and a chunk that starts at position 0
 LONG = [(3000, 513), (40, 200), (0, 130)]

@@ -822,6 +822,14 @@ constexpr uint64_t split_per_share = 4;
 constexpr uint64_t split_segment_pages = 4;
 constexpr uint64_t split_max_chunks = 32;
 constexpr uint32_t split_waves = 8;
+// Waves per workgroup of a cut plan whose workgroups fit one per compute unit
+// and hold at least split_alone_min_pages pages each (one long row's pieces):
+// each wave holds one page in flight, and more waves per compute unit read
+// faster (one 32K-token row, 64 pages per workgroup, 2.1-2.3 % faster than
+// at 8 waves, a 64K-token row 1.3-2.4 %; 16 waves no faster than 8; at 32
+// pages per workgroup even, at 16 pages 1.6-2.1 % slower)
+constexpr uint32_t split_waves_alone = 12;
+constexpr uint32_t split_alone_min_pages = 48;
 // Pages (about 12 us of one workgroup's reads) by which the longest row may
 // exceed 9/8 of a compute unit's share and still stay whole, for batches of
 // one or two (row, kv head) units per compute unit. Measured on one
@@ -971,7 +979,8 @@ bool aligned16(const void* ptr)
 // (config 3); with 1-2 units per CU, 8 waves is 7-16 % slower. A smaller
 // batch takes the maximum (16, or 8 for wide lanes) so each row streams
 // as fast as one CU allows. Chunks of cut rows take split_waves (a chunk is
-// short, and several of them share a CU). f32 pages take 4 waves, two
+// short, and several of them share a CU), or split_waves_alone when the
+// plan's workgroups fit one per CU with enough pages each. f32 pages take 4 waves, two
 // workgroups per CU at their two waves per SIMD: on config 2's shape 4, 6 and
 // 8 waves measured 90.9, 97.9 and 96.6 us per launch, on config 3's 770, 768
 // and 779 us (one box).
@@ -987,8 +996,11 @@ uint32_t fast_waves(uint32_t group, int dtype, uint32_t units, int cu_count,
     }
     if (dtype == CKV_F32)
         return 4;
-    if (split_pages)
-        return std::min(limit, split_waves);
+    if (split_pages) {
+        const bool alone = units <= (uint32_t)std::max(cu_count, 1)
+            && split_pages >= split_alone_min_pages;
+        return std::min(limit, alone ? split_waves_alone : split_waves);
+    }
     if (limit > 10 && cu_count > 0 && units >= (uint32_t)cu_count)
         return units / (uint32_t)cu_count >= 6 && mean_pages < 256 ? 8 : 10;
     return limit;

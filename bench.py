@@ -10,8 +10,9 @@ a seeded random order so tables are non-contiguous. K/V/Q are synthetic
 N(0,1) bf16 already resident in HBM when timing starts.
 
 The default run then appends bounded legs of the other GPU configs under
-"legs" (config 2: 2,000 decode launches; config 4: 5 prefill steps at the
-2,008-token prefix; config 5: the first 1,000 churn steps), each with its own
+"legs" (config 2: 2,000 decode launches; the same layer over one 32,768-token
+row: 2,000 launches; config 4: 5 prefill steps at the 2,008-token prefix;
+config 5: the first 1,000 churn steps), each with its own
 roofline and CPU baseline; the line's "value" stays config 3's. --no-legs
 skips them.
 
@@ -1089,6 +1090,9 @@ def bench_ceiling(args):
 LEGS = (
     ("config2", {"steps": 2000, "warmup": 3},
      "one decode launch over config 2's batch per step, 2,000 timed steps"),
+    ("longrow", {"steps": 2000, "warmup": 3},
+     "one decode launch over a single 32,768-token row (config 2's layer and pool) per step, "
+     "2,000 timed steps"),
     ("config4", {"steps": 5, "warmup": 1, "prefix": 2008, "sequences": PREFILL_SEQS},
      "5 timed steps of config 4 at the 2,008-token prefix (copy-on-write tail)"),
     ("config5", {"steps": 1000},
@@ -1099,9 +1103,10 @@ LEG_DROP = ("n_gpus", "higher_is_better", "scaling", "vs_baseline", "dtype")
 
 
 def run_legs(args):
-    """Configs 2, 4 and 5 after the headline config 3, each with its own
-    roofline and CPU baseline, so one default run measures every BASELINE
-    config with a GPU workload. A leg's `value` is that config's own metric."""
+    """Configs 2, 4 and 5 after the headline config 3 (and config 2's layer
+    over one long row), each with its own roofline and CPU baseline, so one
+    default run measures every BASELINE config with a GPU workload. A leg's
+    `value` is that config's own metric."""
     legs = {}
     for name, overrides, what in LEGS:
         sub = argparse.Namespace(**vars(args))
@@ -1110,7 +1115,8 @@ def run_legs(args):
         sub.calibrate_copy = sub.gate = sub.rope = sub.no_fuse = False
         log(f"leg {name}: {what}")
         t0 = time.perf_counter()
-        fn = {"config2": bench_config2, "config4": bench_config4, "config5": bench_config5}[name]
+        fn = {"config2": bench_config2, "longrow": lambda a: bench_config2(a, long_row=True),
+              "config4": bench_config4, "config5": bench_config5}[name]
         res = fn(sub)
         leg = {k: v for k, v in res.items() if k not in LEG_DROP}
         leg["leg"] = what

@@ -330,6 +330,11 @@ struct decode_plan_shape {
 };
 decode_plan_shape shape_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
                                     uint32_t kv_heads, int cu_count);
+// Waves per workgroup of the fast decode for a launch of `units` (plan
+// workgroup, kv head) workgroups: a plan's split_pages (0 when no row is cut)
+// and the batch's mean row pages decide it; CKV_DECODE_WAVES overrides.
+uint32_t decode_fast_waves(uint32_t group, int dtype, uint32_t units, int cu_count,
+                           uint32_t mean_pages, uint32_t split_pages);
 constexpr size_t plan_entry_words = 8;
 constexpr uint32_t plan_last = 0xFFFFFFFFu; // no next entry
 // Writes shape.n_items plan entries to plan, rows words to split_first and the

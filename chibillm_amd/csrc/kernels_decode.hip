@@ -1172,6 +1172,12 @@ uint64_t forced_pages(const char* name, bool& set)
 
 } // namespace
 
+uint32_t decode_fast_waves(uint32_t group, int dtype, uint32_t units, int cu_count,
+                           uint32_t mean_pages, uint32_t split_pages)
+{
+    return fast_waves(group, dtype, units, cu_count, mean_pages, split_pages);
+}
+
 decode_plan_shape shape_decode_plan(const std::vector<uint32_t>& positions, uint32_t block_size,
                                     uint32_t kv_heads, int cu_count)
 {

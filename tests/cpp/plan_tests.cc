@@ -287,6 +287,42 @@ TEST("random batches at random GPU sizes: every plan is well formed")
     }
 }
 
+TEST("decode waves per workgroup: cut plans of one workgroup per compute unit take 12")
+{
+    auto waves = [](const std::vector<uint32_t>& positions, uint32_t group, int dtype) {
+        const auto shape = ckv::shape_decode_plan(positions, bs, 8, 256);
+        uint64_t pages = 0;
+        for (const uint32_t p : positions)
+            pages += pages_of(p);
+        const uint32_t n_wgs = shape.n_wgs ? shape.n_wgs : (uint32_t)positions.size();
+        return ckv::decode_fast_waves(group, dtype, n_wgs * 8, 256,
+                                      (uint32_t)(pages / positions.size()), shape.split_pages);
+    };
+    CHECK(waves({ 32767 }, 2, CKV_BF16) == 12);  // 32 pieces of 64 pages, one per CU
+    CHECK(waves({ 65535 }, 2, CKV_BF16) == 12);  // 128 pages each
+    CHECK(waves({ 16383 }, 2, CKV_BF16) == 8);   // 32 pages each: under the floor
+    CHECK(waves({ 32767 }, 1, CKV_F16) == 12);
+    CHECK(waves({ 32767 }, 8, CKV_BF16) == 8);   // wide lanes: 8 at most
+    CHECK(waves({ 32767 }, 2, CKV_F32) == 4);
+    std::vector<uint32_t> two(2, 40959);         // two long rows: two workgroups per CU
+    CHECK(waves(two, 2, CKV_BF16) == 8);
+    std::mt19937_64 rng(7);
+    std::vector<uint32_t> c2(32), c3(128), churn(512);
+    for (auto& p : c2)
+        p = 256 + (uint32_t)(rng() % 3841);
+    for (auto& p : c3)
+        p = 1024 + (uint32_t)(rng() % 7169);
+    for (auto& p : churn)
+        p = 256 + (uint32_t)(rng() % 1945);
+    CHECK(waves(c2, 2, CKV_BF16) == 8);   // config 2: two 8-wave workgroups per CU
+    CHECK(waves(c3, 2, CKV_BF16) == 10);  // config 3: whole rows, long on average
+    CHECK(waves(churn, 2, CKV_BF16) == 8); // many short whole rows
+    {
+        const env_guard e("CKV_DECODE_WAVES", "6");
+        CHECK(waves({ 32767 }, 2, CKV_BF16) == 6);
+    }
+}
+
 // ---- the prefill's launch shape and key ranges ---------------------------
 
 namespace {
